@@ -1,0 +1,224 @@
+#!/usr/bin/env python3
+"""Benchmark: dense bf16 linear layer on one MI355X through libinvision_hip.so.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload c2] [--all] [--no-cpu-baseline]
+
+A step is one Y = X . W^T + bias over the workload's full shape, with X, W,
+bias and Y resident in HBM (device pointers through the C ABI).  The default
+workload is the FLUX2-Klein-4B fused QKV projection, M x K x N = 4608 x 3072 x
+9216, bf16 X and W, fp32 bias and output, fp32 accumulation.
+
+Prints ONE JSON line on stdout.  `roofline` uses the dense bf16 MFMA peak;
+`achieved` is 2*M*N*K per launch over the average launch time measured with
+HIP events on the library's stream across the timed steps.  `cpu_baseline` is
+the reference's CPU GEMM algorithm (the oracle's restatement of qgemm/gemm_nt,
+src/quicknncpu.pas:1241-1337) timed on this host, with the reference's own
+sgemm2.cpp alongside when it was built.  Extra per-workload lines (--all) go to
+stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "GEMM TFLOP/s + % bf16 MFMA peak at 4608×3072×9216 (1 GPU)"
+PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 bf16 FLOP/clk/CU (dense)
+PEAK_HBM_GBS = 8000.0
+
+# name -> (description, M, K, N, bias, epilogue, x dtype, y dtype)
+WORKLOADS = {
+    "c1": ("single linear + bias (QNNLinear), fp32 X", 256, 3072, 3072, True, "none", "f32", "f32"),
+    "c2": ("FLUX2-Klein-4B fused QKV projection", 4608, 3072, 9216, True, "none", "bf16", "f32"),
+    "c3_up": ("DiT MLP up + SiLU, bf16 H out", 4608, 3072, 9216, True, "silu", "bf16", "bf16"),
+    "c3_down": ("DiT MLP down", 4608, 9216, 3072, True, "none", "bf16", "f32"),
+    "c4_gate_up": ("Qwen3-4B gate/up at M=512", 512, 2560, 9728, False, "none", "bf16", "f32"),
+    "c4_down": ("Qwen3-4B down at M=512", 512, 9728, 2560, False, "none", "bf16", "f32"),
+    "c5_qkv": ("Z-Image block QKV, 2 CFG branches", 9216, 3840, 11520, True, "none", "bf16", "f32"),
+    "c5_out": ("Z-Image attention out", 9216, 3840, 3840, True, "none", "bf16", "f32"),
+    "c5_up": ("Z-Image MLP up", 9216, 3840, 15360, True, "none", "bf16", "f32"),
+    "c5_down": ("Z-Image MLP down", 9216, 15360, 3840, True, "none", "bf16", "f32"),
+    "c5_adaln": ("Z-Image AdaLN modulation M=2", 2, 3840, 23040, True, "none", "bf16", "f32"),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_inputs(M, K, N, seed=0):
+    """Synthetic inputs of the workload's distributions: X ~ N(0,1), W ~ N(0,0.02), bias ~ N(0,0.01)."""
+    from invision_amd.bf16 import as_bf16_bits
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((M, K), dtype=np.float32)
+    W = as_bf16_bits(rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02))
+    b = (rng.standard_normal(N, dtype=np.float32) * np.float32(0.01)).astype(np.float32)
+    return X, W, b
+
+
+def algorithmic_bytes(M, K, N, bias, xdt, ydt):
+    xs = 2 if xdt == "bf16" else 4
+    ys = 2 if ydt == "bf16" else 4
+    return M * K * xs + N * K * 2 + M * N * ys + (4 * N if bias else 0)
+
+
+def run_workload(name, steps, warmup, check=True):
+    from invision_amd import hip
+    from invision_amd import quicknn_hip as q
+    from invision_amd.bf16 import as_bf16_bits, bf16_bits_to_f32
+
+    desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[name]
+    log(f"[bench] {name}: {desc} M={M} K={K} N={N} epilogue={epi} x={xdt} y={ydt}")
+    X, W, b = make_inputs(M, K, N)
+    Xin = as_bf16_bits(X) if xdt == "bf16" else X
+    w = q.Weight(W, b if has_bias else None)
+    xd = q.DeviceArray.from_host(Xin, xdt)
+    yd = q.DeviceArray((M, N), ydt)
+    for _ in range(warmup):
+        q.linear_device(xd, w, yd, M, epilogue=epi, asynchronous=True)
+    hip.call("inv_hip_synchronize")
+    # Timed region: host wall clock bracketed by synchronizations, and HIP
+    # events on the library stream around the same launches.
+    t0 = time.perf_counter()
+    hip.call("inv_hip_timer_start")
+    for _ in range(steps):
+        q.linear_device(xd, w, yd, M, epilogue=epi, asynchronous=True)
+    import ctypes
+    ms = ctypes.c_float()
+    hip.call("inv_hip_timer_stop", ctypes.byref(ms))
+    hip.call("inv_hip_synchronize")
+    t1 = time.perf_counter()
+    wall_ms = (t1 - t0) * 1e3 / steps
+    gpu_ms = ms.value / steps
+    flops = 2.0 * M * N * K
+    res = {"name": name, "M": M, "K": K, "N": N, "wall_ms": wall_ms, "kernel_ms": gpu_ms,
+           "tflops_wall": flops / (wall_ms * 1e-3) / 1e12, "tflops_kernel": flops / (gpu_ms * 1e-3) / 1e12,
+           "bytes": algorithmic_bytes(M, K, N, has_bias, xdt, ydt)}
+    res["gbs_kernel"] = res["bytes"] / (gpu_ms * 1e-3) / 1e9
+    if check:
+        # Spot parity on a few rows with numpy float64 (independent of the oracle).
+        Y = yd.to_host()
+        Yf = bf16_bits_to_f32(Y) if ydt == "bf16" else Y
+        rows = np.unique(np.linspace(0, M - 1, num=min(M, 6)).astype(int))
+        Xr = bf16_bits_to_f32(as_bf16_bits(X[rows])).astype(np.float64)
+        ref = Xr @ bf16_bits_to_f32(W).astype(np.float64).T
+        if has_bias:
+            ref += b.astype(np.float64)
+        if epi == "silu":
+            ref = ref / (1.0 + np.exp(-ref))
+        err = float(np.max(np.abs(Yf[rows] - ref)) / np.max(np.abs(ref)))
+        res["parity_normwise_sampled_rows"] = err
+    xd.free()
+    yd.free()
+    w.free()
+    return res
+
+
+def cpu_baseline(name):
+    """The reference's CPU GEMM on this host's cores (bounded: the c2 GEMM itself)."""
+    import oracle
+    desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[name]
+    threads = min(16, os.cpu_count() or 1)
+    os.environ.setdefault("OMP_NUM_THREADS", str(threads))
+    rng = np.random.default_rng(1)
+    A = rng.standard_normal((M, K), dtype=np.float32)
+    B = rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+    C = np.zeros((M, N), np.float32)
+    # warm-up on a slice, then the full shape once
+    oracle.qgemm(oracle.NO_TRANS, oracle.TRANS, 64, N, K, 1.0, A, K, B, K, 0.0, C, N, threads)
+    t = time.perf_counter()
+    oracle.qgemm(oracle.NO_TRANS, oracle.TRANS, M, N, K, 1.0, A, K, B, K, 0.0, C, N, threads)
+    dt = time.perf_counter() - t
+    out = {"value": 2.0 * M * N * K / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+           "sample": f"the full {M}x{K}x{N} fp32 GEMM once (after a 64-row warm-up): the reference's "
+                     f"qgemm/gemm_nt algorithm (8-row tiles over threads, 8-lane AVX2 FMA dots) restated in "
+                     f"oracle/oracle.c, {dt:.2f} s"}
+    if oracle.ref_lib() is not None:
+        # The reference's own sgemm2.cpp (OpenMP, 4x4x128 tiles) on the same arrays.
+        oracle.sgemm2_ref_nt(A[:64], B)
+        t = time.perf_counter()
+        oracle.sgemm2_ref_nt(A, B)
+        dt2 = time.perf_counter() - t
+        out["reference_sgemm2_tflops"] = 2.0 * M * N * K / dt2 / 1e12
+    try:
+        out["cpu_model"] = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if "model name" in l)
+    except Exception:
+        pass
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--all", action="store_true", help="also time every workload shape (stderr)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        return 2
+
+    from invision_amd import quicknn_hip as q
+    info = q.device_info()
+    log(f"[bench] device: {info}")
+
+    res = run_workload(args.workload, args.steps, args.warmup)
+    log(f"[bench] {json.dumps(res)}")
+    if args.all:
+        for name in WORKLOADS:
+            if name != args.workload:
+                r = run_workload(name, max(5, args.steps // 2), 3)
+                log(f"[bench] {json.dumps(r)}")
+
+    desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[args.workload]
+    achieved = res["tflops_kernel"]
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", f"gemm_{args.workload}_traffic.json")
+    if os.path.exists(tf):
+        try:
+            traffic = json.load(open(tf)).get("hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+    line = {
+        "metric": METRIC,
+        "value": round(res["tflops_wall"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["wall_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"{desc}: Y[{M}x{N}] = X[{M}x{K}] . W[{N}x{K}]^T + bias, bf16 X/W, fp32 "
+                               f"accumulate, fp32 bias and Y, device-resident",
+                   "M": M, "K": K, "N": N, "x_dtype": xdt, "y_dtype": ydt, "bias": has_bias, "epilogue": epi,
+                   "parallelism": "1 GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic},
+        "parity_normwise_sampled_rows": res.get("parity_normwise_sampled_rows"),
+        "device": info["name"],
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline ...")
+        line["cpu_baseline"] = cpu_baseline(args.workload)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+    q.shutdown()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,141 @@
+/*
+ * inv_hip.h -- C ABI of libinvision_hip.so, the MI355X (gfx950) backend for
+ * hshatti/Invision's dense linear layer  Y = X . W^T (+bias) (+SiLU/GELU).
+ *
+ * Plain C: no C++ or HIP types cross this boundary.  Every entry point returns
+ * an int status (INV_OK = 0) and never aborts; the message for the last
+ * failure on the calling thread is inv_hip_last_error().
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *  - the CBLAS slot  TQNNSingleOPS.cblas_sgemm   src/quicknncpu.pas:102-103
+ *    (bound by LoadLibrary/getProcAddress at src/quicknncpu.pas:3967-3992),
+ *    replaced by inv_hip_sgemm, same argument list and meaning;
+ *  - the bf16 slot   TQNNSingleOPS.cblas_sbgemm  src/quicknncpu.pas:110-111,
+ *    replaced by inv_hip_sbgemm;
+ *  - QNNLinear / QNNLinearNoBias / QNNLinearNoBias_BF16 / QNNMatMulNT /
+ *    QNNLINEAR_BF16_OR_F32  (src/quicknn_kernels.pas:216-223, 317;
+ *    src/quicknncpu.pas:1773-1784, 1807-1847, 3062-3071), replaced by
+ *    inv_hip_linear on a device-resident weight handle;
+ *  - the bf16 weight source  TSafeTensorFile.getTensorDataMemBlockBF16
+ *    (src/safetensor.pas:650-683), whose mmap pointer feeds
+ *    inv_hip_weight_upload once, instead of the per-call widening at
+ *    src/quicknncpu.pas:1842-1844.
+ */
+#ifndef INV_HIP_H
+#define INV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define INV_HIP_ABI_VERSION 1
+
+/* ---- status codes ------------------------------------------------------- */
+#define INV_OK               0
+#define INV_ERR_ARG          1  /* bad pointer, shape, leading dimension or enum   */
+#define INV_ERR_UNSUPPORTED  2  /* valid but not implemented (e.g. ColMajor)        */
+#define INV_ERR_NO_DEVICE    3  /* no gfx950 device visible                         */
+#define INV_ERR_OOM          4  /* device or pinned-host allocation failed          */
+#define INV_ERR_HIP          5  /* a HIP runtime call failed                        */
+#define INV_ERR_NOT_INIT     6  /* inv_hip_init has not succeeded                   */
+
+/* ---- element types: the reference's TQNNDataType values
+ *      (src/quicknn_common.pas:77-98: dtBf16 = 2, dtF32 = 3) ---------------- */
+#define INV_DT_BF16 2
+#define INV_DT_F32  3
+
+/* ---- CBLAS enums: src/quicknn_common.pas:55-58 -------------------------- */
+#define INV_CBLAS_ROW_MAJOR 101
+#define INV_CBLAS_COL_MAJOR 102
+#define INV_CBLAS_NO_TRANS  111
+#define INV_CBLAS_TRANS     112
+
+/* ---- epilogues fused into the GEMM's store ------------------------------- */
+#define INV_EPI_NONE      0 /* Y = acc (+bias)                                            */
+#define INV_EPI_SILU      1 /* Y = silu(acc + bias), exact: v / (1 + exp(-v))              */
+#define INV_EPI_GELU_ERF  2 /* Y = 0.5 v (1 + erf(v / sqrt 2)); the reference has no GELU */
+
+/* ---- flags for inv_hip_linear -------------------------------------------- */
+#define INV_FLAG_DEVICE_PTRS 0x1 /* X, Y and bias are device pointers (inv_hip_malloc) */
+#define INV_FLAG_ASYNC       0x2 /* with DEVICE_PTRS: return without waiting; call
+                                    inv_hip_synchronize before reading Y            */
+
+typedef struct inv_weight_s *inv_weight_t; /* opaque device-resident weight */
+
+/* ---- lifetime ------------------------------------------------------------- */
+/* Select device `device` (ordinal among visible devices), check it is gfx950,
+ * create the library stream.  Returns INV_ERR_NO_DEVICE when there is none, so
+ * the caller keeps its CPU GEMM bound (src/quicknncpu.pas:3951-3955). */
+int inv_hip_init(int device);
+/* Free every weight, workspace and the stream (src/quicknncpu.pas:4073-4086). */
+int inv_hip_shutdown(void);
+/* Message for the last failing call on this thread ("" if none). */
+const char *inv_hip_last_error(void);
+int inv_hip_abi_version(void);
+/* Name, compute-unit count and peak engine clock of the selected device. */
+int inv_hip_device_info(char *name, size_t name_len, int *cu_count, int *clock_khz);
+
+/* ---- weights -------------------------------------------------------------- */
+/* Copy W[N x K] bf16 (row-major, leading dimension K, e.g. the mmap pointer
+ * from getTensorDataMemBlockBF16) and an optional fp32 bias[N] to the device
+ * once.  The host buffer may be read-only; it is not retained. */
+int inv_hip_weight_upload(const uint16_t *w_bf16, int64_t N, int64_t K, const float *bias,
+                          inv_weight_t *out);
+/* Same from fp32 weights (getTensorDataMemBlock, src/safetensor.pas:584-647):
+ * each value is rounded to bf16, ties to even (exact for widened bf16). */
+int inv_hip_weight_upload_f32(const float *w_f32, int64_t N, int64_t K, const float *bias,
+                              inv_weight_t *out);
+int inv_hip_weight_free(inv_weight_t w);
+/* N and K of a handle. */
+int inv_hip_weight_shape(inv_weight_t w, int64_t *N, int64_t *K);
+
+/* ---- the linear layer ----------------------------------------------------- */
+/* Y[M x N] = epilogue(X[M x K] . W^T + bias), row-major, leading dims K and N.
+ *  X: fp32 (rounded to bf16, ties to even, on the device) or bf16.
+ *  Y: fp32 or bf16 (rounded to nearest even from the fp32 accumulator).
+ *  bias: NULL -> the handle's uploaded bias if it has one, else none.
+ *  Accumulation is fp32 in the MFMA units.  Host pointers by default (copied
+ *  in and out, synchronous); INV_FLAG_DEVICE_PTRS for resident buffers. */
+int inv_hip_linear(const void *X, int x_dtype, inv_weight_t W, const float *bias, void *Y,
+                   int y_dtype, int64_t M, int64_t K, int64_t N, int epilogue, int flags);
+
+/* ---- the CBLAS slots ------------------------------------------------------ */
+/* Exactly the signature of TQNNSingleOPS.cblas_sgemm (src/quicknncpu.pas:
+ * 102-103): C = alpha * op(A) . op(B) + beta * C on host fp32 arrays, RowMajor,
+ * every NoTrans/Trans combination.  A and B are rounded to bf16 (ties to even)
+ * on the device and multiplied with fp32 accumulation; beta == 0 does not read
+ * C (BLAS semantics).  Returns a status; the slot's callers ignore it, so the
+ * binding checks inv_hip_last_error (see the integration notes). */
+int inv_hip_sgemm(int order, int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha,
+                  const float *A, int64_t lda, const float *B, int64_t ldb, float beta, float *C,
+                  int64_t ldc);
+/* TQNNSingleOPS.cblas_sbgemm (src/quicknncpu.pas:110-111): bf16 A and B. */
+int inv_hip_sbgemm(int order, int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha,
+                   const uint16_t *A, int64_t lda, const uint16_t *B, int64_t ldb, float beta, float *C,
+                   int64_t ldc);
+
+/* ---- device memory and timing, for callers that keep activations resident */
+int inv_hip_malloc(void **ptr, size_t bytes);
+int inv_hip_free(void *ptr);
+int inv_hip_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int inv_hip_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int inv_hip_memset(void *dst, int value, size_t bytes);
+int inv_hip_synchronize(void);
+/* HIP events recorded on the library stream: start, then stop -> elapsed ms. */
+int inv_hip_timer_start(void);
+int inv_hip_timer_stop(float *ms);
+
+/* ---- statistics (the per-op accumulator of src/nopmetrics.pas:30-72) ------- */
+/* Number of inv_hip_linear/sgemm/sbgemm calls and the summed GPU time of their
+ * GEMM kernels in ms (HIP events, only while enabled). */
+int inv_hip_stats_enable(int enable);
+int inv_hip_stats(int64_t *calls, double *gemm_ms, double *flops);
+int inv_hip_stats_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* INV_HIP_H */

@@ -1,0 +1,106 @@
+// convert_kernels.hpp -- layout/precision staging for the GEMM operands.
+//
+// The GEMM consumes bf16 rows with K contiguous, K padded to a multiple of 8
+// and rows 16-byte aligned.  These kernels produce that layout:
+//  * fp32 rows -> bf16 rows (round to nearest even), the activation path of
+//    inv_hip_linear (the reference keeps activations fp32, so this rounding is
+//    the one precision step the HIP path adds);
+//  * fp32 [R x C] -> bf16 [C x R] (transposed), for the CBLAS slot's
+//    Trans-A / NoTrans-B operands;
+//  * bf16 rows -> bf16 rows (re-pitch / pad) and bf16 transpose, for the bf16
+//    slot and unaligned bf16 activations.
+// All are HBM-bound: 6 bytes (fp32 -> bf16) or 4 bytes (bf16) per element.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace inv {
+
+__device__ __forceinline__ uint16_t bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// dst[r, c] = bf16(src[r, c]) for c < cols, 0 for cols <= c < cols_pad.
+// One thread per 8 outputs; cols_pad % 8 == 0, ldd % 8 == 0, dst 16-B aligned.
+__global__ void __launch_bounds__(256) cvt_rows_f32_bf16(const float *__restrict__ src, int64_t lds,
+                                                         uint16_t *__restrict__ dst, int64_t ldd, int64_t rows,
+                                                         int64_t cols, int64_t cols_pad, int vec_src) {
+    const int64_t per_row = cols_pad >> 3;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= rows * per_row) return;
+    const int64_t r = idx / per_row;
+    const int64_t c0 = (idx - r * per_row) << 3;
+    const float *s = src + r * lds + c0;
+    float v[8];
+    if (vec_src && c0 + 8 <= cols) {
+        float4 a = *(const float4 *)s;
+        float4 b = *(const float4 *)(s + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (c0 + e < cols) ? s[e] : 0.0f;
+    }
+    uint4 o;
+    o.x = (uint32_t)bf16_rne(v[0]) | ((uint32_t)bf16_rne(v[1]) << 16);
+    o.y = (uint32_t)bf16_rne(v[2]) | ((uint32_t)bf16_rne(v[3]) << 16);
+    o.z = (uint32_t)bf16_rne(v[4]) | ((uint32_t)bf16_rne(v[5]) << 16);
+    o.w = (uint32_t)bf16_rne(v[6]) | ((uint32_t)bf16_rne(v[7]) << 16);
+    *(uint4 *)(dst + r * ldd + c0) = o;
+}
+
+// dst[r, c] = src[r, c] (bf16) for c < cols, 0 up to cols_pad.  One thread per 8 outputs.
+__global__ void __launch_bounds__(256) copy_rows_bf16(const uint16_t *__restrict__ src, int64_t lds,
+                                                      uint16_t *__restrict__ dst, int64_t ldd, int64_t rows,
+                                                      int64_t cols, int64_t cols_pad) {
+    const int64_t per_row = cols_pad >> 3;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= rows * per_row) return;
+    const int64_t r = idx / per_row;
+    const int64_t c0 = (idx - r * per_row) << 3;
+    const uint16_t *s = src + r * lds + c0;
+    uint16_t v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (c0 + e < cols) ? s[e] : (uint16_t)0;
+    uint4 o;
+    o.x = (uint32_t)v[0] | ((uint32_t)v[1] << 16);
+    o.y = (uint32_t)v[2] | ((uint32_t)v[3] << 16);
+    o.z = (uint32_t)v[4] | ((uint32_t)v[5] << 16);
+    o.w = (uint32_t)v[6] | ((uint32_t)v[7] << 16);
+    *(uint4 *)(dst + r * ldd + c0) = o;
+}
+
+// dst[c, r] = bf16(src[r, c]) : src [rows x cols] (ld lds) -> dst [cols x rows_pad]
+// (ld ldd), zero for rows <= r < rows_pad.  64x64 tiles through LDS.
+template <typename SrcT>
+__global__ void __launch_bounds__(256) transpose_to_bf16(const SrcT *__restrict__ src, int64_t lds,
+                                                         uint16_t *__restrict__ dst, int64_t ldd, int64_t rows,
+                                                         int64_t cols, int64_t rows_pad) {
+    __shared__ uint16_t tile[64][65];
+    const int64_t r0 = (int64_t)blockIdx.y * 64;
+    const int64_t c0 = (int64_t)blockIdx.x * 64;
+    const int tx = threadIdx.x & 63;
+    const int ty = threadIdx.x >> 6;  // 0..3
+    for (int i = ty; i < 64; i += 4) {
+        const int64_t r = r0 + i, c = c0 + tx;
+        uint16_t v = 0;
+        if (r < rows && c < cols) {
+            if constexpr (sizeof(SrcT) == 4)
+                v = bf16_rne((float)src[r * lds + c]);
+            else
+                v = (uint16_t)src[r * lds + c];
+        }
+        tile[i][tx] = v;
+    }
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4) {
+        const int64_t c = c0 + i, r = r0 + tx;
+        if (c < cols && r < rows_pad) dst[c * ldd + r] = tile[tx][i];
+    }
+}
+
+}  // namespace inv

@@ -1,0 +1,871 @@
+// inv_hip.hip -- host side of libinvision_hip.so (the C ABI in include/inv_hip.h).
+//
+// One library stream (default priority), one mutex: calls are synchronous on
+// return unless INV_FLAG_ASYNC, and concurrent calls are serialized, matching
+// the reference's single-threaded callers (src/quicknn_transformers.pas:1205,
+// 1304).  The library owns all device memory it uses: weights uploaded once
+// into handles, plus grow-only workspaces for staged activations, outputs,
+// split-K partials and counters.  Host buffers move through two pinned bounce
+// buffers, so read-only mmap pointers (src/safetensor.pas:308-317) need no
+// registration.
+#include "../../include/inv_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "convert_kernels.hpp"
+#include "gemm_kernel.hpp"
+
+namespace {
+
+thread_local std::string t_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    t_err = buf;
+    return code;
+}
+
+#define HIPCHK(expr)                                                                         \
+    do {                                                                                     \
+        hipError_t e_ = (expr);                                                              \
+        if (e_ != hipSuccess) return fail(INV_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+#define TRY(expr)              \
+    do {                       \
+        int rc_ = (expr);      \
+        if (rc_) return rc_;   \
+    } while (0)
+
+constexpr uint32_t kWeightMagic = 0x57484950u;  // "WHIP"
+constexpr size_t kPinChunk = 32u << 20;
+
+struct Buf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+struct State {
+    bool init = false;
+    int device = -1;
+    hipStream_t stream = nullptr;
+    hipEvent_t tim0 = nullptr, tim1 = nullptr, st0 = nullptr, st1 = nullptr;
+    hipEvent_t pin_ev[2] = {nullptr, nullptr};
+    void *pin[2] = {nullptr, nullptr};
+    int cu_count = 0, clock_khz = 0;
+    char name[256] = {0};
+    Buf xin, x16, w16, win, yout, cin, bias, partial, counters;
+    bool stats = false;
+    int64_t calls = 0;
+    double gemm_ms = 0.0, flops = 0.0;
+    std::vector<inv_weight_s *> weights;
+};
+
+State g;
+std::mutex g_mu;
+
+}  // namespace
+
+struct inv_weight_s {
+    uint32_t magic;
+    uint16_t *w;   // [N x ldw] bf16, zero padded beyond K
+    float *bias;   // [N] or null
+    int64_t N, K, ldw;
+};
+
+namespace {
+
+inline int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int ensure(Buf &b, size_t bytes) {
+    if (b.cap >= bytes) return INV_OK;
+    if (b.p) {
+        HIPCHK(hipStreamSynchronize(g.stream));
+        HIPCHK(hipFree(b.p));
+        b.p = nullptr;
+        b.cap = 0;
+    }
+    size_t nb = (size_t)round_up((int64_t)std::max<size_t>(bytes, 1), 2 << 20);
+    if (hipMalloc(&b.p, nb) != hipSuccess) {
+        (void)hipGetLastError();
+        b.p = nullptr;
+        return fail(INV_ERR_OOM, "device allocation of %zu bytes failed", nb);
+    }
+    b.cap = nb;
+    return INV_OK;
+}
+
+void release(Buf &b) {
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+}
+
+// Host rows -> contiguous device rows, through the pinned bounce buffers.
+// rows x width bytes; host rows are `pitch` bytes apart.
+int h2d_rows(void *dev, const void *host, int64_t rows, size_t width, size_t pitch) {
+    const char *src = (const char *)host;
+    char *dst = (char *)dev;
+    int k = 0;
+    if (width > kPinChunk) {  // very wide rows: one row at a time, in pieces
+        for (int64_t r = 0; r < rows; ++r)
+            for (size_t off = 0; off < width; off += kPinChunk) {
+                size_t n = std::min(kPinChunk, width - off);
+                HIPCHK(hipEventSynchronize(g.pin_ev[k]));
+                memcpy(g.pin[k], src + r * pitch + off, n);
+                HIPCHK(hipMemcpyAsync(dst + r * width + off, g.pin[k], n, hipMemcpyHostToDevice, g.stream));
+                HIPCHK(hipEventRecord(g.pin_ev[k], g.stream));
+                k ^= 1;
+            }
+        return INV_OK;
+    }
+    const int64_t rows_per = (int64_t)(kPinChunk / width);
+    for (int64_t r0 = 0; r0 < rows; r0 += rows_per) {
+        const int64_t nr = std::min(rows_per, rows - r0);
+        HIPCHK(hipEventSynchronize(g.pin_ev[k]));
+        char *pb = (char *)g.pin[k];
+        if (pitch == width) {
+            memcpy(pb, src + r0 * pitch, (size_t)nr * width);
+        } else {
+            for (int64_t r = 0; r < nr; ++r) memcpy(pb + r * width, src + (r0 + r) * pitch, width);
+        }
+        HIPCHK(hipMemcpyAsync(dst + r0 * width, pb, (size_t)nr * width, hipMemcpyHostToDevice, g.stream));
+        HIPCHK(hipEventRecord(g.pin_ev[k], g.stream));
+        k ^= 1;
+    }
+    return INV_OK;
+}
+
+// Contiguous device rows -> host rows `pitch` bytes apart (the bytes between
+// rows are not touched).  Synchronous.
+int d2h_rows(void *host, const void *dev, int64_t rows, size_t width, size_t pitch) {
+    char *dst = (char *)host;
+    const char *src = (const char *)dev;
+    struct Piece {
+        int64_t r0, nr;
+        size_t off, n;
+    };
+    std::vector<Piece> pieces;
+    if (width > kPinChunk) {
+        for (int64_t r = 0; r < rows; ++r)
+            for (size_t off = 0; off < width; off += kPinChunk) pieces.push_back({r, 1, off, std::min(kPinChunk, width - off)});
+    } else {
+        const int64_t rows_per = (int64_t)(kPinChunk / width);
+        for (int64_t r0 = 0; r0 < rows; r0 += rows_per) {
+            int64_t nr = std::min(rows_per, rows - r0);
+            pieces.push_back({r0, nr, 0, (size_t)nr * width});
+        }
+    }
+    auto drain = [&](size_t i) -> int {
+        const Piece &pc = pieces[i];
+        HIPCHK(hipEventSynchronize(g.pin_ev[i & 1]));
+        const char *pb = (const char *)g.pin[i & 1];
+        if (pc.nr == 1 && width > kPinChunk) {
+            memcpy(dst + pc.r0 * pitch + pc.off, pb, pc.n);
+        } else if (pitch == width) {
+            memcpy(dst + pc.r0 * pitch, pb, pc.n);
+        } else {
+            for (int64_t r = 0; r < pc.nr; ++r) memcpy(dst + (pc.r0 + r) * pitch, pb + r * width, width);
+        }
+        return INV_OK;
+    };
+    for (size_t i = 0; i < pieces.size(); ++i) {
+        const Piece &pc = pieces[i];
+        const char *s = (width > kPinChunk) ? src + pc.r0 * width + pc.off : src + pc.r0 * width;
+        HIPCHK(hipMemcpyAsync(g.pin[i & 1], s, pc.n, hipMemcpyDeviceToHost, g.stream));
+        HIPCHK(hipEventRecord(g.pin_ev[i & 1], g.stream));
+        if (i >= 1) TRY(drain(i - 1));
+    }
+    if (!pieces.empty()) TRY(drain(pieces.size() - 1));
+    return INV_OK;
+}
+
+// ---------------------------------------------------------------------------
+// GEMM launch
+// ---------------------------------------------------------------------------
+
+struct TileChoice {
+    int cfg;     // index into the instantiated tile shapes
+    int ksplit;  // 1 = no split
+};
+
+// Instantiated tile shapes (TN = W rows, TM = X rows, wave grid WN x WM).
+// 0: 256x256 2x2   1: 256x128 2x2   2: 128x128 2x2   3: 128x64 2x2   4: 128x32 4x1
+constexpr int kNumCfg = 5;
+constexpr int kCfgTN[kNumCfg] = {256, 256, 128, 128, 128};
+constexpr int kCfgTM[kNumCfg] = {256, 128, 128, 64, 32};
+
+template <int TN, int TM, int WN, int WM>
+int launch_tile(const inv::GemmParams &p, int epi, int out, bool split) {
+    dim3 block(WN * WM * 64);
+    dim3 grid((unsigned)(p.tiles_m * p.tiles_n * (split ? p.ksplit : 1)));
+#define INV_LAUNCH(E, O, S) \
+    hipLaunchKernelGGL((inv::gemm_nt_bf16_kernel<TN, TM, WN, WM, E, O, S>), grid, block, 0, g.stream, p)
+#define INV_LAUNCH_EO(S)                                                        \
+    do {                                                                        \
+        if (out == inv::OUT_F32) {                                              \
+            if (epi == inv::EPI_NONE) INV_LAUNCH(inv::EPI_NONE, inv::OUT_F32, S); \
+            else if (epi == inv::EPI_SILU) INV_LAUNCH(inv::EPI_SILU, inv::OUT_F32, S); \
+            else INV_LAUNCH(inv::EPI_GELU, inv::OUT_F32, S);                    \
+        } else {                                                                \
+            if (epi == inv::EPI_NONE) INV_LAUNCH(inv::EPI_NONE, inv::OUT_BF16, S); \
+            else if (epi == inv::EPI_SILU) INV_LAUNCH(inv::EPI_SILU, inv::OUT_BF16, S); \
+            else INV_LAUNCH(inv::EPI_GELU, inv::OUT_BF16, S);                   \
+        }                                                                       \
+    } while (0)
+    if (split)
+        INV_LAUNCH_EO(true);
+    else
+        INV_LAUNCH_EO(false);
+#undef INV_LAUNCH_EO
+#undef INV_LAUNCH
+    HIPCHK(hipGetLastError());
+    return INV_OK;
+}
+
+int launch_cfg(int cfg, const inv::GemmParams &p, int epi, int out, bool split) {
+    switch (cfg) {
+    case 0: return launch_tile<256, 256, 2, 2>(p, epi, out, split);
+    case 1: return launch_tile<256, 128, 2, 2>(p, epi, out, split);
+    case 2: return launch_tile<128, 128, 2, 2>(p, epi, out, split);
+    case 3: return launch_tile<128, 64, 2, 2>(p, epi, out, split);
+    case 4: return launch_tile<128, 32, 4, 1>(p, epi, out, split);
+    default: return fail(INV_ERR_ARG, "bad tile config %d", cfg);
+    }
+}
+
+int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return (v && *v) ? atoi(v) : dflt;
+}
+
+// Pick a tile shape and split-K factor.  Large problems take the 256x256 tile;
+// skinny ones stream W with a short X tile and split K until the grid covers
+// the chip at least twice.
+TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
+    TileChoice c{0, 1};
+    const int cus = g.cu_count > 0 ? g.cu_count : 256;
+    const int64_t KT = (K + 63) / 64;
+    if (M <= 32) c.cfg = 4;
+    else if (M <= 64) c.cfg = 3;
+    else {
+        // Among the three larger tiles, the one that wastes least of the last
+        // wave of workgroups, weighting smaller tiles by their lower MFMA
+        // efficiency per byte of LDS traffic.
+        const double eff[3] = {1.0, 0.9, 0.8};
+        double best = -1.0;
+        for (int cfg = 0; cfg < 3; ++cfg) {
+            int64_t tiles = ((M + kCfgTM[cfg] - 1) / kCfgTM[cfg]) * ((N + kCfgTN[cfg] - 1) / kCfgTN[cfg]);
+            double useful = (double)M * N;
+            double waves = (double)((tiles + cus - 1) / cus);
+            double score = useful / (waves * cus * kCfgTM[cfg] * kCfgTN[cfg]) * eff[cfg];
+            if (score > best) {
+                best = score;
+                c.cfg = cfg;
+            }
+        }
+    }
+    const int64_t tiles = ((M + kCfgTM[c.cfg] - 1) / kCfgTM[c.cfg]) * ((N + kCfgTN[c.cfg] - 1) / kCfgTN[c.cfg]);
+    const int64_t target = (c.cfg >= 3) ? 2 * cus : cus;
+    if (tiles < target && KT >= 16) {
+        int64_t s = (target + tiles - 1) / tiles;
+        s = std::min<int64_t>(s, KT / 8);
+        s = std::min<int64_t>(s, 16);
+        c.ksplit = (int)std::max<int64_t>(s, 1);
+    }
+    int ov = env_int("INV_HIP_TILE_CFG", -1);
+    if (ov >= 0 && ov < kNumCfg) c.cfg = ov;
+    int ks = env_int("INV_HIP_KSPLIT", -1);
+    if (ks >= 1) c.ksplit = ks;
+    return c;
+}
+
+// W [N x ldw], X [M x ldx] bf16 device; K a multiple of 8 (zero padded).
+int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, void *Y, int64_t ldy, int out,
+             const float *bias, const float *Cin, int64_t ldc, float alpha, float beta, int64_t M, int64_t N,
+             int64_t K, int epi) {
+    if (M == 0 || N == 0) return INV_OK;
+    if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return fail(INV_ERR_ARG, "dimension too large");
+    if (K % 8 || ldw % 8 || ldx % 8 || !aligned(W, 16) || !aligned(X, 16))
+        return fail(INV_ERR_ARG, "internal: GEMM operands not 16-byte granular");
+    if ((int64_t)256 * ldw * 2 >= ((int64_t)1 << 31) || (int64_t)256 * ldx * 2 >= ((int64_t)1 << 31))
+        return fail(INV_ERR_UNSUPPORTED, "leading dimension too large for 32-bit buffer offsets");
+    TileChoice tc = choose_tiles(M, N, K);
+    inv::GemmParams p{};
+    p.W = W;
+    p.X = X;
+    p.Y = Y;
+    p.bias = bias;
+    p.Cin = Cin;
+    p.ldw = ldw;
+    p.ldx = ldx;
+    p.ldy = ldy;
+    p.ldc = ldc;
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.tiles_m = (int)((M + kCfgTM[tc.cfg] - 1) / kCfgTM[tc.cfg]);
+    p.tiles_n = (int)((N + kCfgTN[tc.cfg] - 1) / kCfgTN[tc.cfg]);
+    p.group_m = std::max(1, std::min(p.tiles_m, env_int("INV_HIP_GROUP_M", 4)));
+    p.alpha = alpha;
+    p.beta = beta;
+    p.has_bias = bias != nullptr;
+    const size_t esz = (out == inv::OUT_F32) ? 4 : 2;
+    p.vec_store = (ldy % 4 == 0) && aligned(Y, 4 * esz) && (bias == nullptr || aligned(bias, 16));
+    if (bias && !aligned(bias, 16)) return fail(INV_ERR_ARG, "internal: bias not 16-byte aligned");
+    const int64_t KT = (K + 63) / 64;
+    bool split = tc.ksplit > 1 && KT > 1;
+    if (split) {
+        p.kt_per_split = (int)((KT + tc.ksplit - 1) / tc.ksplit);
+        p.ksplit = (int)((KT + p.kt_per_split - 1) / p.kt_per_split);
+        split = p.ksplit > 1;
+    }
+    if (!split) {
+        p.ksplit = 1;
+        p.kt_per_split = (int)KT;
+    } else {
+        const int64_t ntiles = (int64_t)p.tiles_m * p.tiles_n;
+        const int nthreads = (tc.cfg == 4) ? 256 : 256;
+        const int64_t acc_regs = (int64_t)kCfgTN[tc.cfg] * kCfgTM[tc.cfg] / nthreads;
+        TRY(ensure(g.partial, (size_t)(ntiles * p.ksplit * nthreads * acc_regs) * sizeof(float)));
+        size_t cbytes = (size_t)ntiles * sizeof(unsigned);
+        if (g.counters.cap < cbytes) {
+            TRY(ensure(g.counters, cbytes));
+            HIPCHK(hipMemsetAsync(g.counters.p, 0, g.counters.cap, g.stream));
+        }
+        p.partial = (float *)g.partial.p;
+        p.counters = (unsigned *)g.counters.p;
+    }
+    if (g.stats) HIPCHK(hipEventRecord(g.st0, g.stream));
+    TRY(launch_cfg(tc.cfg, p, epi, out, split));
+    if (g.stats) {
+        HIPCHK(hipEventRecord(g.st1, g.stream));
+        HIPCHK(hipEventSynchronize(g.st1));
+        float ms = 0.f;
+        HIPCHK(hipEventElapsedTime(&ms, g.st0, g.st1));
+        g.gemm_ms += ms;
+        g.flops += 2.0 * (double)M * (double)N * (double)K;
+    }
+    return INV_OK;
+}
+
+int launch_cvt_rows_f32(const float *src, int64_t lds, uint16_t *dst, int64_t ldd, int64_t rows, int64_t cols,
+                        int64_t cols_pad) {
+    if (rows == 0) return INV_OK;
+    int64_t work = rows * (cols_pad / 8);
+    int vec = aligned(src, 16) && (lds % 4 == 0);
+    hipLaunchKernelGGL(inv::cvt_rows_f32_bf16, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, g.stream, src, lds,
+                       dst, ldd, rows, cols, cols_pad, vec);
+    HIPCHK(hipGetLastError());
+    return INV_OK;
+}
+
+int launch_copy_rows_bf16(const uint16_t *src, int64_t lds, uint16_t *dst, int64_t ldd, int64_t rows, int64_t cols,
+                          int64_t cols_pad) {
+    if (rows == 0) return INV_OK;
+    int64_t work = rows * (cols_pad / 8);
+    hipLaunchKernelGGL(inv::copy_rows_bf16, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, g.stream, src, lds,
+                       dst, ldd, rows, cols, cols_pad);
+    HIPCHK(hipGetLastError());
+    return INV_OK;
+}
+
+// src [rows x cols] -> dst [cols x rows_pad] bf16
+template <typename T>
+int launch_transpose(const T *src, int64_t lds, uint16_t *dst, int64_t ldd, int64_t rows, int64_t cols,
+                     int64_t rows_pad) {
+    if (rows_pad == 0 || cols == 0) return INV_OK;
+    dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows_pad + 63) / 64));
+    if (grid.y > 65535) return fail(INV_ERR_UNSUPPORTED, "transpose: too many rows");
+    hipLaunchKernelGGL(inv::transpose_to_bf16<T>, grid, dim3(256), 0, g.stream, src, lds, dst, ldd, rows, cols,
+                       rows_pad);
+    HIPCHK(hipGetLastError());
+    return INV_OK;
+}
+
+int check_init() {
+    if (!g.init) return fail(INV_ERR_NOT_INIT, "inv_hip_init has not been called (or failed)");
+    HIPCHK(hipSetDevice(g.device));
+    return INV_OK;
+}
+
+bool valid_weight(inv_weight_t w) {
+    if (!w) return false;
+    for (auto *x : g.weights)
+        if (x == w) return w->magic == kWeightMagic;
+    return false;
+}
+
+int epi_ok(int epi) { return epi == INV_EPI_NONE || epi == INV_EPI_SILU || epi == INV_EPI_GELU_ERF; }
+
+int upload_bias(const float *bias, int64_t N, float **out) {
+    *out = nullptr;
+    if (!bias) return INV_OK;
+    float *d = nullptr;
+    if (hipMalloc(&d, (size_t)N * 4) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(INV_ERR_OOM, "bias allocation failed");
+    }
+    int rc = h2d_rows(d, bias, 1, (size_t)N * 4, (size_t)N * 4);
+    if (rc) {
+        (void)hipFree(d);
+        return rc;
+    }
+    *out = d;
+    return INV_OK;
+}
+
+int weight_upload_impl(const void *w, bool is_f32, int64_t N, int64_t K, const float *bias, inv_weight_t *out) {
+    TRY(check_init());
+    if (!out) return fail(INV_ERR_ARG, "out handle pointer is null");
+    *out = nullptr;
+    if (!w || N <= 0 || K <= 0) return fail(INV_ERR_ARG, "weight: null pointer or non-positive shape (N=%lld K=%lld)",
+                                            (long long)N, (long long)K);
+    if (N > INT32_MAX / 2 || K > INT32_MAX / 2) return fail(INV_ERR_ARG, "weight too large");
+    const int64_t ldw = round_up(K, 8);
+    uint16_t *dw = nullptr;
+    if (hipMalloc(&dw, (size_t)(N * ldw) * 2) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(INV_ERR_OOM, "weight allocation of %lld bytes failed", (long long)(N * ldw * 2));
+    }
+    int rc = INV_OK;
+    if (is_f32) {
+        rc = ensure(g.win, (size_t)(N * K) * 4);
+        if (!rc) rc = h2d_rows(g.win.p, w, N, (size_t)K * 4, (size_t)K * 4);
+        if (!rc) rc = launch_cvt_rows_f32((const float *)g.win.p, K, dw, ldw, N, K, ldw);
+    } else if (ldw == K) {
+        rc = h2d_rows(dw, w, N, (size_t)K * 2, (size_t)K * 2);
+    } else {
+        rc = ensure(g.win, (size_t)(N * K) * 2);
+        if (!rc) rc = h2d_rows(g.win.p, w, N, (size_t)K * 2, (size_t)K * 2);
+        if (!rc) rc = launch_copy_rows_bf16((const uint16_t *)g.win.p, K, dw, ldw, N, K, ldw);
+    }
+    float *db = nullptr;
+    if (!rc) rc = upload_bias(bias, N, &db);
+    if (!rc) {
+        hipError_t e = hipStreamSynchronize(g.stream);
+        if (e != hipSuccess) rc = fail(INV_ERR_HIP, "weight upload: %s", hipGetErrorString(e));
+    }
+    if (rc) {
+        (void)hipFree(dw);
+        if (db) (void)hipFree(db);
+        return rc;
+    }
+    auto *h = new inv_weight_s{kWeightMagic, dw, db, N, K, ldw};
+    g.weights.push_back(h);
+    *out = h;
+    return INV_OK;
+}
+
+void free_weight(inv_weight_s *w) {
+    if (w->w) (void)hipFree(w->w);
+    if (w->bias) (void)hipFree(w->bias);
+    w->magic = 0;
+    delete w;
+}
+
+// Stage an operand as bf16 rows [rows x cols_pad] with K contiguous.
+//  src: host or device; dtype f32/bf16; trans: src holds the operand transposed
+//  ([cols x rows] with leading dimension ld).
+int stage_operand(const void *src, int dtype, bool on_device, bool trans, int64_t rows, int64_t cols, int64_t ld,
+                  Buf &dst, Buf &tmp, const uint16_t **out, int64_t *out_ld) {
+    const size_t esz = dtype == INV_DT_F32 ? 4 : 2;
+    const int64_t cols_pad = round_up(cols, 8);
+    const int64_t src_rows = trans ? cols : rows;
+    const int64_t src_cols = trans ? rows : cols;
+    // bf16, not transposed, already 16-byte granular on the device: use in place.
+    if (on_device && dtype == INV_DT_BF16 && !trans && cols % 8 == 0 && ld % 8 == 0 && aligned(src, 16)) {
+        *out = (const uint16_t *)src;
+        *out_ld = ld;
+        return INV_OK;
+    }
+    const void *dsrc = src;
+    int64_t dld = ld;
+    if (!on_device) {
+        // Upload the exact extent into a contiguous device buffer.
+        if (!trans && dtype == INV_DT_BF16 && cols == cols_pad) {
+            TRY(ensure(dst, (size_t)(rows * cols_pad) * 2));
+            TRY(h2d_rows(dst.p, src, rows, (size_t)cols * 2, (size_t)ld * esz));
+            *out = (const uint16_t *)dst.p;
+            *out_ld = cols_pad;
+            return INV_OK;
+        }
+        TRY(ensure(tmp, (size_t)(src_rows * src_cols) * esz));
+        TRY(h2d_rows(tmp.p, src, src_rows, (size_t)src_cols * esz, (size_t)ld * esz));
+        dsrc = tmp.p;
+        dld = src_cols;
+    }
+    TRY(ensure(dst, (size_t)(rows * cols_pad) * 2));
+    uint16_t *d = (uint16_t *)dst.p;
+    if (!trans) {
+        if (dtype == INV_DT_F32)
+            TRY(launch_cvt_rows_f32((const float *)dsrc, dld, d, cols_pad, rows, cols, cols_pad));
+        else
+            TRY(launch_copy_rows_bf16((const uint16_t *)dsrc, dld, d, cols_pad, rows, cols, cols_pad));
+    } else {
+        // dsrc is [cols x rows] (ld dld) -> d [rows x cols_pad]
+        if (dtype == INV_DT_F32)
+            TRY(launch_transpose<float>((const float *)dsrc, dld, d, cols_pad, cols, rows, cols_pad));
+        else
+            TRY(launch_transpose<uint16_t>((const uint16_t *)dsrc, dld, d, cols_pad, cols, rows, cols_pad));
+    }
+    *out = d;
+    *out_ld = cols_pad;
+    return INV_OK;
+}
+
+int gemm_slot(int order, int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha, const void *A,
+              int64_t lda, const void *B, int64_t ldb, float beta, float *C, int64_t ldc, int dtype) {
+    TRY(check_init());
+    if (order == INV_CBLAS_COL_MAJOR) {
+        // Column-major C = op(A) op(B)  <=>  row-major C^T = op(B)^T op(A)^T.
+        std::swap(transA, transB);
+        std::swap(M, N);
+        std::swap(A, B);
+        std::swap(lda, ldb);
+        order = INV_CBLAS_ROW_MAJOR;
+    }
+    if (order != INV_CBLAS_ROW_MAJOR) return fail(INV_ERR_ARG, "sgemm: bad order %d", order);
+    auto tr_ok = [](int t) { return t == INV_CBLAS_NO_TRANS || t == INV_CBLAS_TRANS; };
+    if (!tr_ok(transA) || !tr_ok(transB)) return fail(INV_ERR_ARG, "sgemm: bad transpose flag");
+    if (M < 0 || N < 0 || K < 0) return fail(INV_ERR_ARG, "sgemm: negative dimension");
+    if (M == 0 || N == 0) return INV_OK;
+    if (!C) return fail(INV_ERR_ARG, "sgemm: C is null");
+    if (ldc < std::max<int64_t>(1, N)) return fail(INV_ERR_ARG, "sgemm: ldc < N");
+    const bool ta = transA == INV_CBLAS_TRANS, tb = transB == INV_CBLAS_TRANS;
+    // Row-major: op(A) is M x K (A is K x M when transposed); op(B) is K x N.
+    if (K > 0) {
+        if (!A || !B) return fail(INV_ERR_ARG, "sgemm: A or B is null");
+        if (lda < std::max<int64_t>(1, ta ? M : K)) return fail(INV_ERR_ARG, "sgemm: lda too small");
+        if (ldb < std::max<int64_t>(1, tb ? K : N)) return fail(INV_ERR_ARG, "sgemm: ldb too small");
+    }
+    if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return fail(INV_ERR_ARG, "sgemm: too large");
+    const int64_t Kp = round_up(std::max<int64_t>(K, 1), 8);
+    const uint16_t *Xd = nullptr, *Wd = nullptr;
+    int64_t ldx = 0, ldw = 0;
+    if (K > 0) {
+        // X = op(A) [M x K]: stored transposed when A is Trans.
+        TRY(stage_operand(A, dtype, false, ta, M, K, lda, g.x16, g.xin, &Xd, &ldx));
+        // W = op(B)^T [N x K]: B is [N x K] when Trans, [K x N] (transposed) otherwise.
+        TRY(stage_operand(B, dtype, false, !tb, N, K, ldb, g.w16, g.win, &Wd, &ldw));
+    } else {
+        // K == 0: C = beta * C.  Zero operands of width 8.
+        TRY(ensure(g.x16, (size_t)(M * 8) * 2));
+        TRY(ensure(g.w16, (size_t)(N * 8) * 2));
+        HIPCHK(hipMemsetAsync(g.x16.p, 0, (size_t)(M * 8) * 2, g.stream));
+        HIPCHK(hipMemsetAsync(g.w16.p, 0, (size_t)(N * 8) * 2, g.stream));
+        Xd = (const uint16_t *)g.x16.p;
+        Wd = (const uint16_t *)g.w16.p;
+        ldx = ldw = 8;
+    }
+    TRY(ensure(g.yout, (size_t)(M * N) * 4));
+    const float *cin = nullptr;
+    if (beta != 0.0f) {
+        TRY(ensure(g.cin, (size_t)(M * N) * 4));
+        TRY(h2d_rows(g.cin.p, C, M, (size_t)N * 4, (size_t)ldc * 4));
+        cin = (const float *)g.cin.p;
+    }
+    TRY(run_gemm(Wd, ldw, Xd, ldx, g.yout.p, N, inv::OUT_F32, nullptr, cin, N, alpha, beta, M, N, Kp, inv::EPI_NONE));
+    TRY(d2h_rows(C, g.yout.p, M, (size_t)N * 4, (size_t)ldc * 4));
+    g.calls++;
+    return INV_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+
+extern "C" {
+
+int inv_hip_abi_version(void) { return INV_HIP_ABI_VERSION; }
+
+const char *inv_hip_last_error(void) { return t_err.c_str(); }
+
+int inv_hip_init(int device) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g.init) {
+        if (device == g.device) return INV_OK;
+        return fail(INV_ERR_ARG, "already initialised on device %d", g.device);
+    }
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        return fail(INV_ERR_NO_DEVICE, "no HIP device visible");
+    }
+    if (device < 0 || device >= n) return fail(INV_ERR_NO_DEVICE, "device %d out of range (%d visible)", device, n);
+    hipDeviceProp_t prop;
+    HIPCHK(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(INV_ERR_NO_DEVICE, "device %d is %s, this library is built for gfx950", device, prop.gcnArchName);
+    HIPCHK(hipSetDevice(device));
+    HIPCHK(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
+    HIPCHK(hipEventCreate(&g.tim0));
+    HIPCHK(hipEventCreate(&g.tim1));
+    HIPCHK(hipEventCreate(&g.st0));
+    HIPCHK(hipEventCreate(&g.st1));
+    for (int k = 0; k < 2; ++k) {
+        HIPCHK(hipEventCreateWithFlags(&g.pin_ev[k], hipEventDisableTiming));
+        HIPCHK(hipEventRecord(g.pin_ev[k], g.stream));
+        if (hipHostMalloc(&g.pin[k], kPinChunk, hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(INV_ERR_OOM, "pinned bounce buffer allocation failed");
+        }
+    }
+    g.device = device;
+    g.cu_count = prop.multiProcessorCount;
+    g.clock_khz = prop.clockRate;
+    snprintf(g.name, sizeof g.name, "%s (%s)", prop.name, prop.gcnArchName);
+    g.init = true;
+    return INV_OK;
+}
+
+int inv_hip_shutdown(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g.init) return INV_OK;
+    (void)hipSetDevice(g.device);
+    (void)hipStreamSynchronize(g.stream);
+    for (auto *w : g.weights) free_weight(w);
+    g.weights.clear();
+    for (Buf *b : {&g.xin, &g.x16, &g.w16, &g.win, &g.yout, &g.cin, &g.bias, &g.partial, &g.counters}) release(*b);
+    for (int k = 0; k < 2; ++k) {
+        if (g.pin[k]) (void)hipHostFree(g.pin[k]);
+        if (g.pin_ev[k]) (void)hipEventDestroy(g.pin_ev[k]);
+        g.pin[k] = nullptr;
+        g.pin_ev[k] = nullptr;
+    }
+    for (hipEvent_t *e : {&g.tim0, &g.tim1, &g.st0, &g.st1}) {
+        if (*e) (void)hipEventDestroy(*e);
+        *e = nullptr;
+    }
+    (void)hipStreamDestroy(g.stream);
+    g.stream = nullptr;
+    g.init = false;
+    g.device = -1;
+    g.stats = false;
+    g.calls = 0;
+    g.gemm_ms = g.flops = 0.0;
+    return INV_OK;
+}
+
+int inv_hip_device_info(char *name, size_t name_len, int *cu_count, int *clock_khz) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    TRY(check_init());
+    if (name && name_len) snprintf(name, name_len, "%s", g.name);
+    if (cu_count) *cu_count = g.cu_count;
+    if (clock_khz) *clock_khz = g.clock_khz;
+    return INV_OK;
+}
+
+int inv_hip_weight_upload(const uint16_t *w_bf16, int64_t N, int64_t K, const float *bias, inv_weight_t *out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return weight_upload_impl(w_bf16, false, N, K, bias, out);
+}
+
+int inv_hip_weight_upload_f32(const float *w_f32, int64_t N, int64_t K, const float *bias, inv_weight_t *out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return weight_upload_impl(w_f32, true, N, K, bias, out);
+}
+
+int inv_hip_weight_free(inv_weight_t w) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!w) return INV_OK;
+    if (!g.init) return fail(INV_ERR_NOT_INIT, "library not initialised");
+    auto it = std::find(g.weights.begin(), g.weights.end(), w);
+    if (it == g.weights.end()) return fail(INV_ERR_ARG, "unknown weight handle");
+    (void)hipSetDevice(g.device);
+    (void)hipStreamSynchronize(g.stream);
+    free_weight(w);
+    g.weights.erase(it);
+    return INV_OK;
+}
+
+int inv_hip_weight_shape(inv_weight_t w, int64_t *N, int64_t *K) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!valid_weight(w)) return fail(INV_ERR_ARG, "unknown weight handle");
+    if (N) *N = w->N;
+    if (K) *K = w->K;
+    return INV_OK;
+}
+
+int inv_hip_linear(const void *X, int x_dtype, inv_weight_t W, const float *bias, void *Y, int y_dtype, int64_t M,
+                   int64_t K, int64_t N, int epilogue, int flags) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    TRY(check_init());
+    if (!valid_weight(W)) return fail(INV_ERR_ARG, "linear: unknown weight handle");
+    if (x_dtype != INV_DT_F32 && x_dtype != INV_DT_BF16) return fail(INV_ERR_ARG, "linear: bad x_dtype %d", x_dtype);
+    if (y_dtype != INV_DT_F32 && y_dtype != INV_DT_BF16) return fail(INV_ERR_ARG, "linear: bad y_dtype %d", y_dtype);
+    if (!epi_ok(epilogue)) return fail(INV_ERR_ARG, "linear: bad epilogue %d", epilogue);
+    if (flags & ~(INV_FLAG_DEVICE_PTRS | INV_FLAG_ASYNC)) return fail(INV_ERR_ARG, "linear: unknown flags 0x%x", flags);
+    if ((flags & INV_FLAG_ASYNC) && !(flags & INV_FLAG_DEVICE_PTRS))
+        return fail(INV_ERR_ARG, "linear: ASYNC requires DEVICE_PTRS");
+    if (M < 0) return fail(INV_ERR_ARG, "linear: negative M");
+    if (K != W->K || N != W->N)
+        return fail(INV_ERR_ARG, "linear: shape mismatch: call K=%lld N=%lld, weight K=%lld N=%lld", (long long)K,
+                    (long long)N, (long long)W->K, (long long)W->N);
+    if (M == 0) return INV_OK;
+    if (!X || !Y) return fail(INV_ERR_ARG, "linear: X or Y is null");
+    if (M > INT32_MAX / 2) return fail(INV_ERR_ARG, "linear: M too large");
+    const bool dev = (flags & INV_FLAG_DEVICE_PTRS) != 0;
+    const int out = (y_dtype == INV_DT_F32) ? inv::OUT_F32 : inv::OUT_BF16;
+    const size_t ysz = (y_dtype == INV_DT_F32) ? 4 : 2;
+
+    // Activations -> bf16 [M x ldw] (ldw = K rounded up to 8, zero padded).
+    const uint16_t *Xd = nullptr;
+    int64_t ldx = 0;
+    TRY(stage_operand(X, x_dtype, dev, false, M, K, K, g.x16, g.xin, &Xd, &ldx));
+
+    // Bias: explicit argument first, else the handle's.
+    const float *bd = W->bias;
+    if (bias) {
+        if (dev && aligned(bias, 16)) {
+            bd = bias;
+        } else {
+            TRY(ensure(g.bias, (size_t)N * 4));
+            if (dev)
+                HIPCHK(hipMemcpyAsync(g.bias.p, bias, (size_t)N * 4, hipMemcpyDeviceToDevice, g.stream));
+            else
+                TRY(h2d_rows(g.bias.p, bias, 1, (size_t)N * 4, (size_t)N * 4));
+            bd = (const float *)g.bias.p;
+        }
+    }
+
+    void *Yd = Y;
+    if (!dev) {
+        TRY(ensure(g.yout, (size_t)(M * N) * ysz));
+        Yd = g.yout.p;
+    }
+    TRY(run_gemm(W->w, W->ldw, Xd, ldx, Yd, N, out, bd, nullptr, 0, 1.0f, 0.0f, M, N, W->ldw, epilogue));
+    g.calls++;
+    if (!dev) {
+        TRY(d2h_rows(Y, Yd, M, (size_t)N * ysz, (size_t)N * ysz));
+    } else if (!(flags & INV_FLAG_ASYNC)) {
+        HIPCHK(hipStreamSynchronize(g.stream));
+    }
+    return INV_OK;
+}
+
+int inv_hip_sgemm(int order, int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha, const float *A,
+                  int64_t lda, const float *B, int64_t ldb, float beta, float *C, int64_t ldc) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return gemm_slot(order, transA, transB, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, INV_DT_F32);
+}
+
+int inv_hip_sbgemm(int order, int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha, const uint16_t *A,
+                   int64_t lda, const uint16_t *B, int64_t ldb, float beta, float *C, int64_t ldc) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return gemm_slot(order, transA, transB, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, INV_DT_BF16);
+}
+
+int inv_hip_malloc(void **ptr, size_t bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    TRY(check_init());
+    if (!ptr) return fail(INV_ERR_ARG, "malloc: null out pointer");
+    *ptr = nullptr;
+    if (hipMalloc(ptr, std::max<size_t>(bytes, 1)) != hipSuccess) {
+        (void)hipGetLastError();
+        *ptr = nullptr;
+        return fail(INV_ERR_OOM, "device allocation of %zu bytes failed", bytes);
+    }
+    return INV_OK;
+}
+
+int inv_hip_free(void *ptr) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    TRY(check_init());
+    if (!ptr) return INV_OK;
+    HIPCHK(hipStreamSynchronize(g.stream));
+    HIPCHK(hipFree(ptr));
+    return INV_OK;
+}
+
+int inv_hip_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    TRY(check_init());
+    if (!bytes) return INV_OK;
+    if (!dst || !src) return fail(INV_ERR_ARG, "memcpy_h2d: null pointer");
+    TRY(h2d_rows(dst, src, 1, bytes, bytes));
+    HIPCHK(hipStreamSynchronize(g.stream));
+    return INV_OK;
+}
+
+int inv_hip_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    TRY(check_init());
+    if (!bytes) return INV_OK;
+    if (!dst || !src) return fail(INV_ERR_ARG, "memcpy_d2h: null pointer");
+    return d2h_rows(dst, src, 1, bytes, bytes);
+}
+
+int inv_hip_memset(void *dst, int value, size_t bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    TRY(check_init());
+    if (!bytes) return INV_OK;
+    if (!dst) return fail(INV_ERR_ARG, "memset: null pointer");
+    HIPCHK(hipMemsetAsync(dst, value, bytes, g.stream));
+    HIPCHK(hipStreamSynchronize(g.stream));
+    return INV_OK;
+}
+
+int inv_hip_synchronize(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    TRY(check_init());
+    HIPCHK(hipStreamSynchronize(g.stream));
+    return INV_OK;
+}
+
+int inv_hip_timer_start(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    TRY(check_init());
+    HIPCHK(hipEventRecord(g.tim0, g.stream));
+    return INV_OK;
+}
+
+int inv_hip_timer_stop(float *ms) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    TRY(check_init());
+    if (!ms) return fail(INV_ERR_ARG, "timer_stop: null pointer");
+    HIPCHK(hipEventRecord(g.tim1, g.stream));
+    HIPCHK(hipEventSynchronize(g.tim1));
+    HIPCHK(hipEventElapsedTime(ms, g.tim0, g.tim1));
+    return INV_OK;
+}
+
+int inv_hip_stats_enable(int enable) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    TRY(check_init());
+    g.stats = enable != 0;
+    return INV_OK;
+}
+
+int inv_hip_stats(int64_t *calls, double *gemm_ms, double *flops) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (calls) *calls = g.calls;
+    if (gemm_ms) *gemm_ms = g.gemm_ms;
+    if (flops) *flops = g.flops;
+    return INV_OK;
+}
+
+int inv_hip_stats_reset(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    g.calls = 0;
+    g.gemm_ms = g.flops = 0.0;
+    return INV_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,318 @@
+"""Host-side mirror of the reference's linear-layer operators over libinvision_hip.so.
+
+Same names, argument order and meaning as the reference's L2 entry points
+(src/quicknn_kernels.pas:216-223, 317) and the CBLAS slot
+(src/quicknncpu.pas:102-103); host arrays are numpy arrays written in place,
+as TMemoryBlock storage is.  Bound violations raise AssertionError with the
+reference's messages (src/quicknncpu.pas:1775-1777); library failures raise
+HipError.  All arithmetic happens in the HIP library: this module only moves
+arguments across the C ABI.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import numpy as np
+
+from . import hip
+from .bf16 import as_bf16_bits
+
+_initialized = False
+
+
+def init(device: int = 0) -> None:
+    """inv_hip_init; idempotent."""
+    global _initialized
+    if not _initialized:
+        hip.call("inv_hip_init", device)
+        _initialized = True
+
+
+def shutdown() -> None:
+    global _initialized
+    if _initialized:
+        hip.call("inv_hip_shutdown")
+        _initialized = False
+
+
+def device_info() -> dict:
+    init()
+    name = ctypes.create_string_buffer(256)
+    cus, clk = ctypes.c_int(), ctypes.c_int()
+    hip.call("inv_hip_device_info", name, 256, ctypes.byref(cus), ctypes.byref(clk))
+    return {"name": name.value.decode(), "cu_count": cus.value, "clock_khz": clk.value}
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def _check_host(a: np.ndarray, dtype, name: str) -> None:
+    if not isinstance(a, np.ndarray):
+        raise TypeError(f"{name} must be a numpy array")
+    if a.dtype != dtype:
+        raise TypeError(f"{name} must be {np.dtype(dtype).name}, got {a.dtype}")
+    if not a.flags.c_contiguous:
+        raise ValueError(f"{name} must be C-contiguous")
+
+
+# ---------------------------------------------------------------------------
+# Device memory
+# ---------------------------------------------------------------------------
+
+class DeviceArray:
+    """A device buffer owned by the library (inv_hip_malloc)."""
+
+    _DT = {"f32": (np.float32, 4, hip.INV_DT_F32), "bf16": (np.uint16, 2, hip.INV_DT_BF16)}
+
+    def __init__(self, shape, dtype: str = "f32"):
+        init()
+        if dtype not in self._DT:
+            raise ValueError("dtype must be 'f32' or 'bf16'")
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = dtype
+        self.np_dtype, self.itemsize, self.inv_dtype = self._DT[dtype]
+        self.nbytes = int(np.prod(self.shape)) * self.itemsize
+        p = ctypes.c_void_p()
+        hip.call("inv_hip_malloc", ctypes.byref(p), max(self.nbytes, 1))
+        self.ptr = p.value
+
+    @classmethod
+    def from_host(cls, a: np.ndarray, dtype: Optional[str] = None) -> "DeviceArray":
+        if dtype is None:
+            dtype = "bf16" if a.dtype == np.uint16 else "f32"
+        d = cls(a.shape, dtype)
+        d.copy_from(a)
+        return d
+
+    def copy_from(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a, dtype=self.np_dtype)
+        if a.nbytes != self.nbytes:
+            raise ValueError("size mismatch")
+        hip.call("inv_hip_memcpy_h2d", self.ptr, _ptr(a), self.nbytes)
+
+    def to_host(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=self.np_dtype)
+        hip.call("inv_hip_memcpy_d2h", _ptr(out), self.ptr, self.nbytes)
+        return out
+
+    def fill_zero(self) -> None:
+        hip.call("inv_hip_memset", self.ptr, 0, self.nbytes)
+
+    def free(self) -> None:
+        if self.ptr:
+            hip.call("inv_hip_free", self.ptr)
+            self.ptr = None
+
+    def __del__(self):  # best effort
+        try:
+            if self.ptr and _initialized:
+                hip.load().inv_hip_free(self.ptr)
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------------------
+# Weights: uploaded once, device resident (the bf16 source is
+# TSafeTensorFile.getTensorDataMemBlockBF16, src/safetensor.pas:650-683)
+# ---------------------------------------------------------------------------
+
+class Weight:
+    """A device-resident [N x K] bf16 weight with an optional fp32 bias."""
+
+    def __init__(self, w: np.ndarray, bias: Optional[np.ndarray] = None):
+        init()
+        if w.ndim != 2:
+            raise ValueError("weight must be 2-D [out x in]")
+        self.N, self.K = (int(s) for s in w.shape)
+        b = None
+        if bias is not None:
+            b = np.ascontiguousarray(bias, dtype=np.float32)
+            if b.shape != (self.N,):
+                raise ValueError("bias must have shape (N,)")
+        h = ctypes.c_void_p()
+        bp = _ptr(b) if b is not None else None
+        if w.dtype == np.uint16:
+            w = np.ascontiguousarray(w)
+            hip.call("inv_hip_weight_upload", _ptr(w), self.N, self.K, bp, ctypes.byref(h))
+        elif w.dtype == np.float32:
+            w = np.ascontiguousarray(w)
+            hip.call("inv_hip_weight_upload_f32", _ptr(w), self.N, self.K, bp, ctypes.byref(h))
+        else:
+            raise TypeError("weight must be bf16 bits (uint16) or float32")
+        self.handle = h.value
+        self.has_bias = b is not None
+
+    def free(self) -> None:
+        if self.handle:
+            hip.call("inv_hip_weight_free", self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.free()
+
+
+_EPI = {"none": hip.INV_EPI_NONE, "silu": hip.INV_EPI_SILU, "gelu": hip.INV_EPI_GELU_ERF}
+
+
+def linear_device(x: DeviceArray, W: Weight, y: DeviceArray, M: int, epilogue: str = "none",
+                  bias: Optional[DeviceArray] = None, asynchronous: bool = False) -> None:
+    """inv_hip_linear on device-resident activations: y = epi(x . W^T + bias)."""
+    flags = hip.INV_FLAG_DEVICE_PTRS | (hip.INV_FLAG_ASYNC if asynchronous else 0)
+    hip.call("inv_hip_linear", x.ptr, x.inv_dtype, W.handle, bias.ptr if bias is not None else None, y.ptr,
+             y.inv_dtype, M, W.K, W.N, _EPI[epilogue], flags)
+
+
+def linear(x: np.ndarray, W: Weight, bias: Optional[np.ndarray] = None, epilogue: str = "none",
+           out_dtype: str = "f32") -> np.ndarray:
+    """Host arrays in and out: Y[M x N] = epi(X[M x K] . W^T + bias)."""
+    if x.dtype not in (np.float32, np.uint16):
+        raise TypeError("x must be float32 or bf16 bits (uint16)")
+    x = np.ascontiguousarray(x)
+    M = x.shape[0]
+    if x.ndim != 2 or x.shape[1] != W.K:
+        raise ValueError(f"x must be [M x {W.K}]")
+    xdt = hip.INV_DT_F32 if x.dtype == np.float32 else hip.INV_DT_BF16
+    ydt, ynp = (hip.INV_DT_F32, np.float32) if out_dtype == "f32" else (hip.INV_DT_BF16, np.uint16)
+    y = np.empty((M, W.N), dtype=ynp)
+    b = np.ascontiguousarray(bias, dtype=np.float32) if bias is not None else None
+    hip.call("inv_hip_linear", _ptr(x), xdt, W.handle, _ptr(b) if b is not None else None, _ptr(y), ydt, M, W.K,
+             W.N, _EPI[epilogue], 0)
+    return y
+
+
+# ---------------------------------------------------------------------------
+# The reference's operator surface
+# ---------------------------------------------------------------------------
+
+def _bound(cond: bool, msg: str) -> None:
+    if not cond:
+        raise AssertionError(msg)
+
+
+def cblas_gemm(Order: int, TransA: int, TransB: int, M: int, N: int, K: int, alpha: float, A: np.ndarray, lda: int,
+               B: np.ndarray, ldb: int, beta: float, C: np.ndarray, ldc: int) -> None:
+    """TQNNSingleOPS.cblas_gemm -> cblas_sgemm slot (src/quicknncpu.pas:335-350), fp32 host arrays."""
+    _check_host(A, np.float32, "A")
+    _check_host(B, np.float32, "B")
+    _check_host(C, np.float32, "C")
+    hip.call("inv_hip_sgemm", Order, TransA, TransB, M, N, K, float(alpha), _ptr(A), lda, _ptr(B), ldb,
+             float(beta), _ptr(C), ldc)
+
+
+def cblas_sbgemm(Order: int, TransA: int, TransB: int, M: int, N: int, K: int, alpha: float, A: np.ndarray,
+                 lda: int, B: np.ndarray, ldb: int, beta: float, C: np.ndarray, ldc: int) -> None:
+    """The cblas_sbgemm slot (src/quicknncpu.pas:110-111): bf16 A and B, fp32 C."""
+    _check_host(A, np.uint16, "A")
+    _check_host(B, np.uint16, "B")
+    _check_host(C, np.float32, "C")
+    hip.call("inv_hip_sbgemm", Order, TransA, TransB, M, N, K, float(alpha), _ptr(A), lda, _ptr(B), ldb,
+             float(beta), _ptr(C), ldc)
+
+
+def QNNMatMulNT(C: np.ndarray, A: np.ndarray, B: np.ndarray, M: int, K: int, N: int) -> None:
+    """C[M x N] = A[M x K] . B[N x K]^T  (src/quicknncpu.pas:1773-1784)."""
+    _bound(A.size >= M * K, "ERROR : QNNMatMul out of bound [A]")
+    _bound(B.size >= N * K, "ERROR : QNNMatMul out of bound [B]")
+    _bound(C.size >= M * N, "ERROR : QNNMatMul out of bound [C]")
+    cblas_gemm(hip.CblasRowMajor, hip.CblasNoTrans, hip.CblasTrans, M, N, K, 1.0, A, K, B, K, 0.0, C, N)
+
+
+def QNNMatMulNN(C: np.ndarray, A: np.ndarray, B: np.ndarray, M: int, K: int, N: int) -> None:
+    """C[M x N] = A[M x K] . B[K x N]  (src/quicknncpu.pas:1760-1771)."""
+    _bound(A.size >= M * K, "ERROR : QNNMatMul out of bound [A]")
+    _bound(B.size >= K * N, "ERROR : QNNMatMul out of bound [B]")
+    _bound(C.size >= M * N, "ERROR : QNNMatMul out of bound [C]")
+    cblas_gemm(hip.CblasRowMajor, hip.CblasNoTrans, hip.CblasNoTrans, M, N, K, 1.0, A, K, B, N, 0.0, C, N)
+
+
+def QNNMatMulTN(C: np.ndarray, A: np.ndarray, B: np.ndarray, M: int, K: int, N: int) -> None:
+    """C[M x N] = A[K x M]^T . B[K x N] as the reference calls it (src/quicknncpu.pas:1786-1797)."""
+    _bound(A.size >= K * M, "ERROR : QNNMatMul out of bound [A]")
+    _bound(B.size >= N * K, "ERROR : QNNMatMul out of bound [B]")
+    _bound(C.size >= M * N, "ERROR : QNNMatMul out of bound [C]")
+    cblas_gemm(hip.CblasRowMajor, hip.CblasTrans, hip.CblasNoTrans, M, N, K, 1.0, A, K, B, K, 0.0, C, N)
+
+
+def _linear_weight(W) -> Weight:
+    if isinstance(W, Weight):
+        return W
+    return Weight(W)
+
+
+def _run_linear(dst: np.ndarray, x: np.ndarray, W, B: Optional[np.ndarray], seqLen: int, inDIM: int,
+                outDIM: int) -> None:
+    _check_host(dst, np.float32, "dst")
+    _check_host(x, np.float32, "x")
+    _bound(x.size >= seqLen * inDIM, "ERROR : QNNLinear out of bound [x]")
+    _bound(dst.size >= seqLen * outDIM, "ERROR : QNNLinear out of bound [dst]")
+    w = _linear_weight(W)
+    try:
+        _bound(w.N == outDIM and w.K == inDIM, "ERROR : QNNLinear weight shape mismatch")
+        b = None
+        if B is not None:
+            _check_host(B, np.float32, "B")
+            _bound(B.size >= outDIM, "ERROR : QNNLinear out of bound [B]")
+            b = B
+        hip.call("inv_hip_linear", _ptr(x), hip.INV_DT_F32, w.handle, _ptr(b) if b is not None else None, _ptr(dst),
+                 hip.INV_DT_F32, seqLen, inDIM, outDIM, hip.INV_EPI_NONE, 0)
+    finally:
+        if w is not W:
+            w.free()
+
+
+def QNNLinear(dst: np.ndarray, x: np.ndarray, W, B: Optional[np.ndarray], seqLen: int, inDIM: int,
+              outDIM: int) -> None:
+    """dst = x . W^T (+ B per row)  (src/quicknncpu.pas:1807-1820).
+
+    W may be a resident Weight (uploaded once) or a host array (float32 or bf16
+    bits), which is uploaded for this call only."""
+    _run_linear(dst, x, W, B, seqLen, inDIM, outDIM)
+
+
+def QNNLinearNoBias(dst: np.ndarray, x: np.ndarray, W, seqLen: int, inDIM: int, outDIM: int) -> None:
+    """dst = x . W^T  (src/quicknncpu.pas:1822-1828)."""
+    if isinstance(W, Weight):
+        # A resident weight may carry a bias; QNNLinearNoBias must not add it.
+        _bound(not _weight_has_bias(W), "ERROR : QNNLinearNoBias called with a biased Weight")
+    _run_linear(dst, x, W, None, seqLen, inDIM, outDIM)
+
+
+def QNNLinearNoBias_BF16(dst: np.ndarray, x: np.ndarray, W: np.ndarray, seqLen: int, inDIM: int,
+                         outDIM: int) -> None:
+    """dst = x . bf16(W)^T  (src/quicknncpu.pas:1830-1847); W is bf16 bits or a Weight."""
+    if not isinstance(W, Weight):
+        _check_host(W, np.uint16, "W")
+    _run_linear(dst, x, W, None, seqLen, inDIM, outDIM)
+
+
+def QNNLINEAR_BF16_OR_F32(dst: np.ndarray, src: np.ndarray, weight, weight_bf16, seq: int, srcDim: int,
+                          dstDim: int) -> None:
+    """bf16 weight if assigned, else fp32 (src/quicknncpu.pas:3062-3071)."""
+    _bound(weight is not None or weight_bf16 is not None,
+           "ERROR QNNLINEAR_BF16_OR_F32 : no weight or weight_16 assigned!")
+    if weight_bf16 is not None:
+        QNNLinearNoBias_BF16(dst, src, weight_bf16, seq, srcDim, dstDim)
+    else:
+        QNNLinearNoBias(dst, src, weight, seq, srcDim, dstDim)
+
+
+def _weight_has_bias(W: Weight) -> bool:
+    return W.has_bias
+
+
+def stats() -> dict:
+    calls, ms, flops = ctypes.c_int64(), ctypes.c_double(), ctypes.c_double()
+    hip.call("inv_hip_stats", ctypes.byref(calls), ctypes.byref(ms), ctypes.byref(flops))
+    return {"calls": calls.value, "gemm_ms": ms.value, "flops": flops.value}
+
+
+def as_weight(w: np.ndarray, bias: Optional[np.ndarray] = None) -> Weight:
+    """Upload a host weight (bf16 bits, or float32 rounded to bf16)."""
+    if w.dtype not in (np.uint16, np.float32):
+        w = as_bf16_bits(w)
+    return Weight(w, bias)

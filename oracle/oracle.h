@@ -1,0 +1,81 @@
+/*
+ * oracle.h -- CPU restatement of hshatti/Invision's dense linear-layer path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * (or as the timed CPU baseline).  The product library (libinvision_hip.so)
+ * never links, loads or calls it.
+ *
+ * Every function cites the reference file:line it restates.  How each one is
+ * pinned (known-answer vectors, the reference's own sgemm2.cpp built under
+ * oracle/_ref, closed forms, brute force) is listed in tests/test_oracle.py.
+ */
+#ifndef INV_ORACLE_H
+#define INV_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- RNG: src/quicknn_sample.pas:212-276 ---------------------------------- */
+void     orc_rng_seed(uint64_t seed);              /* SplitMix64 -> 4 state words   */
+void     orc_rng_set_state(const uint64_t s[4]);   /* for known-answer tests        */
+void     orc_rng_get_state(uint64_t s[4]);
+uint64_t orc_xoshiro256ss(void);                   /* xoshiro256**                   */
+float    orc_rand(void);                           /* (x >> 11) * 2^-53 -> single    */
+float    orc_random_normal(void);                  /* Box-Muller, cos branch only    */
+void     orc_randn(float *dst, int64_t n);         /* randn(dst, N)                  */
+/* Draw n normals, scale by sigma, optionally round to bf16 (RNE) in place. */
+void     orc_randn_scaled(float *dst, int64_t n, float sigma, int round_bf16);
+
+/* ---- bf16: src/quicknn_common.pas:1991-2027 ------------------------------- */
+void     orc_bf16_to_f32(const uint16_t *src, float *dst, int64_t n);      /* exact <<16   */
+void     orc_f32_to_bf16_trunc(const float *src, uint16_t *dst, int64_t n); /* ref: >>16    */
+void     orc_f32_to_bf16_rne(const float *src, uint16_t *dst, int64_t n);   /* build: RNE   */
+
+/* ---- GEMM: src/quicknncpu.pas:1176-1496 (qgemm -> gemm_nn/nt/tn) ----------
+ * CBLAS semantics of the reference slot (quicknncpu.pas:102-103), RowMajor
+ * only.  order/trans use the reference enum values (quicknn_common.pas:55-58).
+ * Returns 0, or -1 for an unsupported combination (the reference asserts).
+ * nthreads <= 0 uses every OpenMP thread. */
+int orc_qgemm(int order, int transA, int transB, int64_t M, int64_t N, int64_t K,
+              float alpha, const float *A, int64_t lda, const float *B, int64_t ldb,
+              float beta, float *C, int64_t ldc, int nthreads);
+/* Same arithmetic as orc_qgemm's NT path, but scalar (no AVX2) with the same
+ * 8-lane FMA association; used to show the AVX2 path is bit-identical. */
+int orc_gemm_nt_scalar(int64_t M, int64_t N, int64_t K, float alpha,
+                       const float *A, int64_t lda, const float *B, int64_t ldb,
+                       float beta, float *C, int64_t ldc);
+
+/* fp64 gold: C[m,n] = sum_k A[m,k]*B[n,k] accumulated in double. */
+void orc_gemm_nt_f64(int64_t M, int64_t N, int64_t K, const float *A, int64_t lda,
+                     const float *B, int64_t ldb, double *C, int64_t ldc, int nthreads);
+
+/* ---- linear layer: src/quicknncpu.pas:1807-1847, 3062-3071 ----------------
+ * QNNLinear / QNNLinearNoBias / QNNLinearNoBias_BF16:
+ *   Y[M,N] = X[M,K] . widen(W_bf16)[N,K]^T  (+ bias[N] per row), then epilogue.
+ * epilogue: 0 none, 1 SiLU (exact expf), 2 GELU (erf form), 3 SiLU as the
+ * reference's sSiLU_avx2 computes it (polynomial exp2, exact reciprocal). */
+int orc_linear_bf16w(const float *X, const uint16_t *W, const float *bias, float *Y,
+                     int64_t M, int64_t K, int64_t N, int epilogue, int nthreads);
+
+/* ---- epilogue ops: src/ops_avx2.inc:22-35, 267-376; quicknncpu.pas:305-330, 2372-2418 */
+float orc_silu_exact(float x);
+float orc_gelu_erf(float x);
+/* sSiLU_avx2(N, src, up, outSigmoid, dst) with vrcpps replaced by 1/x. */
+void  orc_silu_qnn(int64_t n, const float *src, const float *up, float *out_sigmoid, float *dst);
+float orc_fast_exp(float x);
+
+/* ---- CBLAS-shaped epilogue helpers used by the tests ---------------------- */
+void orc_add_bias_rows(float *Y, const float *bias, int64_t M, int64_t N); /* QNNAddInplace per row */
+void orc_apply_epilogue(float *Y, int64_t n, int epilogue);
+
+int orc_has_avx2(void);
+int orc_max_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,286 @@
+"""GPU parity of libinvision_hip.so against the CPU oracle (marked gpu).
+
+Parity rule: normwise max|y - r| / max|r| <= 2e-3 against
+the reference's linear layer as it computes it (fp32 activations), and, to
+catch kernel bugs, <= 2e-5 against the oracle fed the same bf16-rounded
+activations the HIP path uses (round to nearest even).  Full-size shapes are
+checked on a seeded sample of rows (rows of X . W^T only depend on the same
+rows of X, so the sample is exact), plus determinism and finiteness of the
+whole output.
+
+Inputs: the reference RNG restated (quicknn_sample.pas:212-276), drawn in the
+order X ~ N(0,1), W ~ N(0,0.02) (bf16), bias ~ N(0,0.01).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from invision_amd import hip
+from invision_amd import quicknn_hip as q
+from invision_amd.bf16 import as_bf16_bits, bf16_bits_to_f32, round_bf16
+
+pytestmark = pytest.mark.gpu
+
+TOL_REF = 2e-3    # vs the reference's fp32-activation linear (north star)
+TOL_TIGHT = 2e-5  # vs the oracle on the same bf16-rounded activations
+
+
+def gen(seed, M, K, N, x_scale=1.0, w_scale=0.02, b_scale=0.01):
+    oracle.rng_seed(seed)
+    X = oracle.randn_scaled((M, K), x_scale, False)
+    W = oracle.f32_to_bf16_rne(oracle.randn_scaled((N, K), w_scale, False))
+    b = oracle.randn_scaled((N,), b_scale, False)
+    return X, W, b
+
+
+EPI_ORACLE = {"none": oracle.EPI_NONE, "silu": oracle.EPI_SILU, "gelu": oracle.EPI_GELU}
+
+
+def oracle_linear(X, W, b, epi="none", rows=None):
+    Xr = X if rows is None else X[rows]
+    return oracle.linear_bf16w(Xr, W, b, EPI_ORACLE[epi])
+
+
+def check(y, X, W, b, epi="none", rows=None, tight=TOL_TIGHT, ref_tol=TOL_REF):
+    ys = y if rows is None else y[rows]
+    r_tight = oracle_linear(round_bf16(X), W, b, epi, rows)
+    e_tight = oracle.normwise_err(ys, r_tight)
+    r_ref = oracle_linear(X, W, b, epi, rows)
+    e_ref = oracle.normwise_err(ys, r_ref)
+    print(f"  normwise err: vs bf16-X oracle {e_tight:.3e} (tol {tight}), vs fp32-X reference {e_ref:.3e} "
+          f"(tol {ref_tol})", flush=True)
+    assert np.all(np.isfinite(ys))
+    assert e_tight <= tight
+    assert e_ref <= ref_tol
+    return e_tight, e_ref
+
+
+def sample_rows(M, n=48, seed=0):
+    rng = np.random.default_rng(seed)
+    rows = np.unique(np.concatenate([[0, M - 1], rng.choice(M, size=min(n, M), replace=False)]))
+    return rows
+
+
+# ------------------------------------------------------------ small & ragged
+
+SMALL = [
+    (1, 8, 8), (2, 16, 4), (3, 24, 5), (5, 7, 3), (17, 19, 23), (31, 64, 33), (33, 96, 130), (64, 128, 64),
+    (65, 200, 257), (128, 64, 300), (129, 1000, 96), (250, 72, 510), (257, 256, 257), (300, 40, 1024),
+]
+
+
+@pytest.mark.parametrize("M,K,N", SMALL)
+def test_linear_small_ragged_shapes(hiplib, M, K, N):
+    X, W, b = gen(1000 + M + K + N, M, K, N)
+    with q.Weight(W, b) as w:
+        y = q.linear(X, w)
+    check(y, X, W, b)
+
+
+@pytest.mark.parametrize("epi", ["none", "silu", "gelu"])
+@pytest.mark.parametrize("out", ["f32", "bf16"])
+def test_linear_epilogues_and_output_types(hiplib, epi, out):
+    M, K, N = 200, 320, 264
+    X, W, b = gen(7, M, K, N)
+    with q.Weight(W) as w:
+        y = q.linear(X, w, bias=b, epilogue=epi, out_dtype=out)
+    if out == "f32":
+        check(y, X, W, b, epi)
+    else:
+        yf = bf16_bits_to_f32(y)
+        ref = oracle_linear(round_bf16(X), W, b, epi)
+        # bf16 output: each element is within half a bf16 ulp of the fp32 result
+        assert oracle.normwise_err(yf, ref) <= 2.5e-3
+        same = np.mean(y == oracle.f32_to_bf16_rne(ref))
+        print(f"  bf16 outputs equal to RNE(oracle): {same:.5f}", flush=True)
+        assert same > 0.999
+
+
+def test_golden_linear_fixtures(hiplib):
+    fx = np.load(os.path.join(os.path.dirname(__file__), "golden", "linear_small.npz"), allow_pickle=False)
+    epi_name = {oracle.EPI_NONE: "none", oracle.EPI_SILU: "silu", oracle.EPI_GELU: "gelu"}
+    for i, (M, K, N, has_bias, epi) in enumerate(fx["cases"]):
+        X, W, b, Y = fx[f"X{i}"], fx[f"W{i}"], fx[f"b{i}"], fx[f"Y{i}"]
+        with q.Weight(W) as w:
+            y = q.linear(X, w, bias=b if has_bias else None, epilogue=epi_name[int(epi)])
+        # X in the fixture is already bf16-exact: only accumulation order differs.
+        assert oracle.normwise_err(y, Y) <= TOL_TIGHT, i
+
+
+def test_bf16_activations_in(hiplib):
+    M, K, N = 96, 256, 192
+    X, W, b = gen(8, M, K, N)
+    with q.Weight(W, b) as w:
+        y16 = q.linear(as_bf16_bits(X), w)
+        y32 = q.linear(X, w)
+    np.testing.assert_array_equal(y16, y32)  # fp32 X is rounded RNE on the device
+
+
+def test_weight_upload_from_fp32_rounds_rne(hiplib):
+    M, K, N = 64, 136, 72
+    X, W, b = gen(9, M, K, N)
+    Wf = bf16_bits_to_f32(W)  # widened bf16: exact in fp32, so rounding is the identity
+    with q.Weight(Wf, b) as w32, q.Weight(W, b) as w16:
+        np.testing.assert_array_equal(q.linear(X, w32), q.linear(X, w16))
+    # A general fp32 weight is rounded to nearest even on upload.
+    oracle.rng_seed(99)
+    Wg = oracle.randn_scaled((N, K), 0.02, False)
+    with q.Weight(Wg, b) as wg, q.Weight(as_bf16_bits(Wg), b) as wr:
+        np.testing.assert_array_equal(q.linear(X, wg), q.linear(X, wr))
+
+
+# ------------------------------------------------------------ tiles, split-K
+
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("ksplit", [1, 3])
+def test_every_tile_shape_and_split(hiplib, monkeypatch, cfg, ksplit):
+    monkeypatch.setenv("INV_HIP_TILE_CFG", str(cfg))
+    monkeypatch.setenv("INV_HIP_KSPLIT", str(ksplit))
+    M, K, N = 300, 1000, 520
+    X, W, b = gen(10, M, K, N)
+    with q.Weight(W, b) as w:
+        y = q.linear(X, w, epilogue="silu")
+        y2 = q.linear(X, w, epilogue="silu")
+    check(y, X, W, b, "silu")
+    np.testing.assert_array_equal(y, y2)  # deterministic, counters reset
+
+
+def test_split_k_result_independent_of_split_count(hiplib, monkeypatch):
+    M, K, N = 256, 2048, 384
+    X, W, b = gen(11, M, K, N)
+    outs = []
+    with q.Weight(W, b) as w:
+        for ks in (1, 2, 4, 8):
+            monkeypatch.setenv("INV_HIP_KSPLIT", str(ks))
+            monkeypatch.setenv("INV_HIP_TILE_CFG", "2")
+            outs.append(q.linear(X, w))
+    for o in outs[1:]:
+        assert oracle.normwise_err(o, outs[0]) < 1e-6
+
+
+# ------------------------------------------------------------ workload shapes
+
+def test_c1_single_linear_with_bias(hiplib):
+    # X fp32 [256 x 3072], W [3072 x 3072], bias, fp32 out, seed 0.
+    M, K, N = 256, 3072, 3072
+    X, W, b = gen(0, M, K, N)
+    with q.Weight(W, b) as w:
+        y = q.linear(X, w)
+    check(y, X, W, b)
+
+
+def test_c2_fused_qkv_metric_shape(hiplib):
+    # 4608 x 3072 x 9216, bf16 X, fp32 out: the headline shape.
+    M, K, N = 4608, 3072, 9216
+    X, W, b = gen(0, M, K, N)
+    Xb = as_bf16_bits(X)
+    with q.Weight(W, b) as w:
+        y = q.linear(Xb, w)
+        y2 = q.linear(Xb, w)
+    assert np.all(np.isfinite(y))
+    np.testing.assert_array_equal(y, y2)
+    rows = sample_rows(M)
+    check(y, X, W, b, rows=rows)
+
+
+def test_c3_mlp_up_silu_then_down(hiplib):
+    M, K, F = 4608, 3072, 9216
+    oracle.rng_seed(0)
+    X = oracle.randn_scaled((M, K), 1.0, False)
+    Wu = oracle.f32_to_bf16_rne(oracle.randn_scaled((F, K), 0.02, False))
+    bu = oracle.randn_scaled((F,), 0.01, False)
+    Wd = oracle.f32_to_bf16_rne(oracle.randn_scaled((K, F), 0.02, False))
+    bd = oracle.randn_scaled((K,), 0.01, False)
+    with q.Weight(Wu, bu) as wu, q.Weight(Wd, bd) as wd:
+        xd = q.DeviceArray.from_host(as_bf16_bits(X))
+        hd = q.DeviceArray((M, F), "bf16")
+        yd = q.DeviceArray((M, K), "f32")
+        q.linear_device(xd, wu, hd, M, epilogue="silu")
+        q.linear_device(hd, wd, yd, M)
+        y = yd.to_host()
+        H = hd.to_host()
+        for d in (xd, hd, yd):
+            d.free()
+    rows = sample_rows(M, 32)
+    Xr = round_bf16(X[rows])
+    H_ref = oracle.linear_bf16w(Xr, Wu, bu, oracle.EPI_SILU)
+    e_h = oracle.normwise_err(bf16_bits_to_f32(H[rows]), H_ref)
+    Y_ref = oracle.linear_bf16w(round_bf16(H_ref), Wd, bd)
+    e_y = oracle.normwise_err(y[rows], Y_ref)
+    # fp32-activation reference chain: H kept fp32 between the GEMMs
+    H_f = oracle.linear_bf16w(X[rows], Wu, bu, oracle.EPI_SILU)
+    Y_f = oracle.linear_bf16w(H_f, Wd, bd)
+    e_ref = oracle.normwise_err(y[rows], Y_f)
+    print(f"  H err {e_h:.3e}, Y err (bf16 chain) {e_y:.3e}, Y err vs fp32 reference chain {e_ref:.3e}", flush=True)
+    assert e_h <= 2.5e-3 and e_y <= 1e-4 and e_ref <= TOL_REF
+
+
+@pytest.mark.parametrize("which", ["gate_up", "down"])
+def test_c4_qwen3_small_m_split_k(hiplib, which):
+    M = 512
+    K, N = (2560, 9728) if which == "gate_up" else (9728, 2560)
+    X, W, _ = gen(4, M, K, N)
+    with q.Weight(W) as w:
+        y = q.linear(as_bf16_bits(X), w)
+        y2 = q.linear(as_bf16_bits(X), w)
+    np.testing.assert_array_equal(y, y2)
+    check(y, X, W, None, rows=sample_rows(M, 64))
+
+
+def test_c5_adaln_modulation_m2(hiplib):
+    M, K, N = 2, 3840, 6 * 3840
+    X, W, b = gen(5, M, K, N)
+    with q.Weight(W, b) as w:
+        y = q.linear(as_bf16_bits(X), w)
+    check(y, X, W, b)
+
+
+def test_c5_zimage_qkv_batched_cfg(hiplib):
+    M, K, N = 2 * 4608, 3840, 11520
+    X, W, b = gen(6, M, K, N)
+    with q.Weight(W, b) as w:
+        y = q.linear(as_bf16_bits(X), w)
+    check(y, X, W, b, rows=sample_rows(M, 32))
+
+
+# ------------------------------------------------------------ device pointers
+
+def test_device_pointer_path_matches_host_path(hiplib):
+    M, K, N = 333, 512, 640
+    X, W, b = gen(12, M, K, N)
+    with q.Weight(W, b) as w:
+        y_host = q.linear(X, w)
+        xd = q.DeviceArray.from_host(X, "f32")
+        yd = q.DeviceArray((M, N), "f32")
+        q.linear_device(xd, w, yd, M, asynchronous=True)
+        hip.call("inv_hip_synchronize")
+        np.testing.assert_array_equal(yd.to_host(), y_host)
+        bd = q.DeviceArray.from_host(b, "f32")
+        with q.Weight(W) as w_nobias:
+            q.linear_device(xd, w_nobias, yd, M, bias=bd)
+        np.testing.assert_array_equal(yd.to_host(), y_host)
+        for d in (xd, yd, bd):
+            d.free()
+
+
+# ------------------------------------------------------------ errors
+
+def test_error_paths_return_status_not_abort(hiplib):
+    lib = hip.load()
+    X, W, b = gen(13, 8, 16, 8)
+    with q.Weight(W) as w:
+        y = np.zeros((8, 8), np.float32)
+        assert lib.inv_hip_linear(X.ctypes.data, 3, w.handle, None, y.ctypes.data, 3, 8, 17, 8, 0, 0) == hip.INV_ERR_ARG
+        assert "mismatch" in hip.last_error()
+        assert lib.inv_hip_linear(X.ctypes.data, 9, w.handle, None, y.ctypes.data, 3, 8, 16, 8, 0, 0) == hip.INV_ERR_ARG
+        assert lib.inv_hip_linear(X.ctypes.data, 3, w.handle, None, y.ctypes.data, 3, 8, 16, 8, 7, 0) == hip.INV_ERR_ARG
+        assert lib.inv_hip_linear(None, 3, w.handle, None, y.ctypes.data, 3, 8, 16, 8, 0, 0) == hip.INV_ERR_ARG
+        assert lib.inv_hip_linear(X.ctypes.data, 3, w.handle, None, y.ctypes.data, 3, 8, 16, 8, 0, 2) == hip.INV_ERR_ARG
+        stale = w.handle
+    assert lib.inv_hip_linear(X.ctypes.data, 3, stale, None, y.ctypes.data, 3, 8, 16, 8, 0, 0) == hip.INV_ERR_ARG
+    assert "unknown weight" in hip.last_error()
+    # M = 0 is a no-op
+    with q.Weight(W) as w:
+        assert lib.inv_hip_linear(X.ctypes.data, 3, w.handle, None, y.ctypes.data, 3, 0, 16, 8, 0, 0) == hip.INV_OK

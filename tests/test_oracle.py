@@ -1,0 +1,282 @@
+"""Pin the CPU oracle before trusting it (CPU only).
+
+Each restated reference function is checked against something it cannot
+agree with by construction if it is wrong: published known-answer vectors, the
+reference's own sgemm2.cpp (built under oracle/_ref), an independent library
+(numpy float64), closed forms, exact bit identities, or brute force on tiny
+inputs.  The last test plants mistakes in oracle inputs and shows the checks
+catch them.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# ---------------------------------------------------------------- RNG ------
+
+def test_splitmix64_seed0_matches_published_outputs():
+    # SplitMix64 from state 0: the first four outputs (Vigna's splitmix64.c),
+    # which rng_seed stores as the xoshiro state (quicknn_sample.pas:239-251).
+    oracle.rng_seed(0)
+    assert oracle.rng_state() == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F, 0xF88BB8A8724C81EC]
+
+
+def test_xoshiro256ss_known_answer():
+    # Published xoshiro256** outputs from state {1, 2, 3, 4}
+    # (the rand_xoshiro crate's reference test vector).
+    oracle.rng_set_state([1, 2, 3, 4])
+    assert oracle.xoshiro256ss(10) == [
+        11520, 0, 1509978240, 1215971899390074240, 1216172134540287360, 607988272756665600,
+        16172922978634559625, 8476171486693032832, 10595114339597558777, 2904607092377533576]
+
+
+def test_rand_is_top53_bits_rounded_to_single():
+    oracle.rng_seed(7)
+    raw = oracle.xoshiro256ss(64)
+    oracle.rng_seed(7)
+    got = np.array([oracle.lib().orc_rand() for _ in range(64)], dtype=np.float32)
+    want = np.array([(r >> 11) / 9007199254740992.0 for r in raw], dtype=np.float64).astype(np.float32)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_box_muller_pairs_u1_then_u2_cos_branch():
+    oracle.rng_seed(11)
+    us = [oracle.lib().orc_rand() for _ in range(40)]
+    oracle.rng_seed(11)
+    z = oracle.randn(20)
+    for i in range(20):
+        u1, u2 = np.float32(us[2 * i]), np.float32(us[2 * i + 1])
+        assert u1 != 0.0
+        want = np.float32(math.sqrt(-2.0 * math.log(float(u1))) * math.cos(2.0 * math.pi * float(u2)))
+        assert z[i] == want, (i, z[i], want)
+
+
+def test_normal_moments():
+    oracle.rng_seed(0)
+    z = oracle.randn(1_000_000).astype(np.float64)
+    assert abs(z.mean()) < 5e-3
+    assert abs(z.var() - 1.0) < 1e-2
+    assert abs(np.mean(z ** 3)) < 2e-2  # symmetric
+
+
+def test_rng_fixture_self_consistency():
+    with open(os.path.join(GOLDEN, "rng_seed0.json")) as f:
+        fx = json.load(f)
+    for seed, rec in fx.items():
+        oracle.rng_seed(int(seed))
+        assert [f"{s:016x}" for s in oracle.rng_state()] == rec["state_after_seed"]
+        assert [f"{r:016x}" for r in oracle.xoshiro256ss(8)] == rec["xoshiro256ss"]
+        oracle.rng_seed(int(seed))
+        got = [f"{int(v):08x}" for v in oracle.randn(8).view(np.uint32)]
+        assert got == rec["random_normal_f32"]
+
+
+# ---------------------------------------------------------------- bf16 -----
+
+def test_bf16_widening_is_shift_for_every_pattern():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = oracle.bf16_to_f32(h)
+    np.testing.assert_array_equal(f.view(np.uint32), h.astype(np.uint32) << 16)
+
+
+def test_bf16_truncation_special_cases():
+    u = np.array([0x3F80FFFF, 0x3F808000, 0xBF80FFFF, 0x7F800000, 0x7FC00001, 0x00000001], dtype=np.uint32)
+    t = oracle.f32_to_bf16_trunc(u.view(np.float32))
+    np.testing.assert_array_equal(t, np.array([0x3F80, 0x3F80, 0xBF80, 0x7F80, 0x7FC0, 0x0000], dtype=np.uint16))
+
+
+def test_bf16_rne_every_midpoint_and_neighbours():
+    # For every finite bf16 b (both signs), the fp32 midpoint between b and its
+    # successor rounds to the one with an even last bit; one ulp of fp32 either
+    # side rounds to the nearer one.
+    b = np.arange(0, 0x7F7F, dtype=np.uint32)  # finite, successor finite
+    for sign in (0, 0x8000):
+        lo = (b | sign) << 16
+        mid = lo + 0x8000
+        r_mid = oracle.f32_to_bf16_rne(mid.view(np.float32)).astype(np.uint32)
+        even = np.where((b & 1) == 0, b, b + 1) | sign
+        np.testing.assert_array_equal(r_mid, even)
+        np.testing.assert_array_equal(oracle.f32_to_bf16_rne((mid - 1).view(np.float32)), (b | sign).astype(np.uint16))
+        np.testing.assert_array_equal(oracle.f32_to_bf16_rne((mid + 1).view(np.float32)),
+                                      ((b + 1) | sign).astype(np.uint16))
+
+
+def test_bf16_rne_specials():
+    u = np.array([0x7F7FFFFF, 0x7F800000, 0xFF800000, 0x7FC00000, 0x7F800001, 0x00000000, 0x80000000],
+                 dtype=np.uint32)
+    r = oracle.f32_to_bf16_rne(u.view(np.float32))
+    assert r[0] == 0x7F80  # largest finite rounds to +inf
+    assert r[1] == 0x7F80 and r[2] == 0xFF80
+    assert (r[3] & 0x7F80) == 0x7F80 and (r[3] & 0x7F) != 0  # NaN stays NaN
+    assert (r[4] & 0x7F80) == 0x7F80 and (r[4] & 0x7F) != 0  # signalling NaN stays NaN
+    assert r[5] == 0 and r[6] == 0x8000
+
+
+# ---------------------------------------------------------------- GEMM -----
+
+def _rand(shape, seed, scale=1.0):
+    oracle.rng_seed(seed)
+    return oracle.randn_scaled(shape, scale, True)
+
+
+TINY = [(1, 1, 1), (3, 5, 7), (9, 13, 17), (8, 8, 8), (17, 33, 130), (64, 31, 257), (12, 4, 40)]
+
+
+@pytest.mark.parametrize("M,N,K", TINY)
+@pytest.mark.parametrize("alpha,beta", [(1.0, 0.0), (0.5, 2.0), (-1.25, 1.0)])
+def test_qgemm_nt_vs_fp64_brute_force(M, N, K, alpha, beta):
+    A, B, C0 = _rand((M, K), 1), _rand((N, K), 2), _rand((M, N), 3)
+    C = C0.copy()
+    oracle.qgemm(oracle.NO_TRANS, oracle.TRANS, M, N, K, alpha, A, K, B, K, beta, C, N)
+    want = alpha * (A.astype(np.float64) @ B.astype(np.float64).T) + beta * C0.astype(np.float64)
+    # fp32 accumulation: |err| <= K * 2^-24 * sum|a||b| (+ rounding of alpha, beta terms)
+    bound = (K + 3) * 2.0 ** -24 * (abs(alpha) * (np.abs(A) @ np.abs(B).T) + abs(beta) * np.abs(C0)) + 1e-30
+    assert np.all(np.abs(C - want) <= bound)
+
+
+@pytest.mark.parametrize("M,N,K", TINY)
+def test_qgemm_nn_tn_vs_numpy_float64(M, N, K):
+    A, B = _rand((M, K), 4), _rand((K, N), 5)
+    C = np.zeros((M, N), np.float32)
+    oracle.qgemm(oracle.NO_TRANS, oracle.NO_TRANS, M, N, K, 1.0, A, K, B, N, 0.0, C, N)
+    want = A.astype(np.float64) @ B.astype(np.float64)
+    assert oracle.normwise_err(C, want) < 1e-5
+    At = np.ascontiguousarray(A.T)  # [K x M]
+    C2 = np.zeros((M, N), np.float32)
+    oracle.qgemm(oracle.TRANS, oracle.NO_TRANS, M, N, K, 1.0, At, M, B, N, 0.0, C2, N)
+    assert oracle.normwise_err(C2, want) < 1e-5
+
+
+def test_qgemm_tt_is_rejected_like_the_reference():
+    A = np.zeros((4, 4), np.float32)
+    with pytest.raises(AssertionError):
+        oracle.qgemm(oracle.TRANS, oracle.TRANS, 4, 4, 4, 1.0, A, 4, A, 4, 0.0, A.copy(), 4)
+
+
+@pytest.mark.skipif(not oracle.lib().orc_has_avx2(), reason="host has no AVX2")
+@pytest.mark.parametrize("M,N,K", [(9, 13, 17), (16, 24, 64), (33, 10, 131)])
+def test_qgemm_avx2_bit_identical_to_scalar_association(M, N, K):
+    A, B = _rand((M, K), 6), _rand((N, K), 7)
+    C = np.zeros((M, N), np.float32)
+    oracle.qgemm(oracle.NO_TRANS, oracle.TRANS, M, N, K, 1.0, A, K, B, K, 0.0, C, N)
+    np.testing.assert_array_equal(C, oracle.gemm_nt_scalar(A, B))
+
+
+def test_gold_f64_matches_numpy_float64():
+    A, B = _rand((37, 300), 8), _rand((29, 300), 9)
+    g = oracle.gemm_nt_f64(A, B)
+    np.testing.assert_allclose(g, A.astype(np.float64) @ B.astype(np.float64).T, rtol=1e-12, atol=1e-12)
+
+
+def test_qgemm_matches_reference_sgemm2_fixtures():
+    # C computed by the reference's own sgemm2.cpp (tests/golden/make_golden.py).
+    fx = np.load(os.path.join(GOLDEN, "sgemm2_ref.npz"), allow_pickle=False)
+    for i, (M, N, K) in enumerate(fx["shapes"]):
+        A, B, C_ref = fx[f"A{i}"], fx[f"B{i}"], fx[f"C{i}"]
+        C = np.zeros((M, N), np.float32)
+        oracle.qgemm(oracle.NO_TRANS, oracle.TRANS, int(M), int(N), int(K), 1.0, A, int(K), B, int(K), 0.0, C, int(N))
+        assert oracle.normwise_err(C, C_ref) < 1e-6, (M, N, K)
+        gold = A.astype(np.float64) @ B.astype(np.float64).T
+        assert oracle.normwise_err(C_ref, gold) < 1e-6
+
+
+@pytest.mark.skipif(oracle.ref_lib() is None, reason="oracle/_ref not built (reference tree absent)")
+def test_qgemm_matches_reference_sgemm2_live():
+    for seed, (M, N, K) in enumerate([(16, 24, 256), (20, 36, 1024), (8, 12, 384)]):
+        A, B = _rand((M, K), 50 + seed), _rand((N, K), 60 + seed, 0.02)
+        C = np.zeros((M, N), np.float32)
+        oracle.qgemm(oracle.NO_TRANS, oracle.TRANS, M, N, K, 1.0, A, K, B, K, 0.0, C, N)
+        assert oracle.normwise_err(C, oracle.sgemm2_ref_nt(A, B)) < 1e-6
+
+
+@pytest.mark.skipif(oracle.ref_lib() is None, reason="oracle/_ref not built (reference tree absent)")
+def test_reference_sgemm2_skips_k_below_128():
+    # Hazard recorded for the oracle choice: sgemm2.cpp never enters its K loop
+    # when K < 128 (sgemm2.cpp:348-365), so it returns C untouched (zeros).
+    A, B = _rand((4, 64), 70), _rand((8, 64), 71)
+    assert np.all(oracle.sgemm2_ref_nt(A, B) == 0.0)
+    C = np.zeros((4, 8), np.float32)
+    oracle.qgemm(oracle.NO_TRANS, oracle.TRANS, 4, 8, 64, 1.0, A, 64, B, 64, 0.0, C, 8)
+    assert np.abs(C).max() > 0.0
+
+
+# ----------------------------------------------------------- epilogue ops --
+
+def test_silu_and_gelu_closed_forms():
+    xs = np.linspace(-30, 30, 2001).astype(np.float32)
+    for x in xs[::7]:
+        s = oracle.lib().orc_silu_exact(float(x))
+        assert s == np.float32(float(x) / (1.0 + math.exp(-float(x))))
+        gl = oracle.lib().orc_gelu_erf(float(x))
+        assert gl == np.float32(0.5 * float(x) * (1.0 + math.erf(float(x) / math.sqrt(2.0))))
+
+
+def test_fast_exp_close_to_exp():
+    xs = np.linspace(-80, 80, 4001)
+    rel = max(abs(oracle.lib().orc_fast_exp(float(x)) / math.exp(x) - 1.0) for x in xs)
+    assert rel < 1e-5
+    assert oracle.lib().orc_fast_exp(-90.0) == 0.0
+
+
+def test_reference_silu_approximation_error_is_its_documented_size():
+    # sSiLU_avx2's quadratic exp2 has max relative error ~1.72e-3 on exp(-x);
+    # the restatement must show that size of error (not 0: it is not exact,
+    # not larger: constants in the right places).
+    x = np.linspace(-20, 20, 100001).astype(np.float32)
+    sig, silu = oracle.silu_qnn(x)
+    exact = 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
+    rel = np.abs(sig / exact - 1.0)
+    assert 1.0e-3 < rel.max() < 2.0e-3
+    np.testing.assert_allclose(silu, sig * x, rtol=1e-6, atol=1e-30)
+    # exp(-0) ~= C2 = 1.00172476 (the constant term of the polynomial)
+    s0, _ = oracle.silu_qnn(np.zeros(1, np.float32))
+    assert abs(float(s0[0]) - 1.0 / (1.0 + 1.00172476)) < 1e-7
+
+
+def test_silu_qnn_gated_form():
+    x = np.linspace(-5, 5, 101).astype(np.float32)
+    up = np.linspace(2, -2, 101).astype(np.float32)
+    sig, out = oracle.silu_qnn(x, up)
+    np.testing.assert_allclose(out, sig * x * up, rtol=1e-6, atol=1e-30)
+
+
+# --------------------------------------------------------------- linear ----
+
+def test_linear_fixtures_against_closed_form():
+    fx = np.load(os.path.join(GOLDEN, "linear_small.npz"), allow_pickle=False)
+    for i, (M, K, N, has_bias, epi) in enumerate(fx["cases"]):
+        X, W, b, Y = fx[f"X{i}"], fx[f"W{i}"], fx[f"b{i}"], fx[f"Y{i}"]
+        got = oracle.linear_bf16w(X, W, b if has_bias else None, int(epi))
+        assert oracle.normwise_err(got, Y) < 1e-6, i
+
+
+def test_linear_bias_is_added_per_row():
+    X, W = _rand((3, 16), 20), oracle.f32_to_bf16_rne(_rand((5, 16), 21))
+    b = np.arange(5, dtype=np.float32)
+    y0 = oracle.linear_bf16w(X, W)
+    y1 = oracle.linear_bf16w(X, W, b)
+    np.testing.assert_allclose(y1 - y0, np.broadcast_to(b, (3, 5)), rtol=0, atol=1e-5)
+
+
+# ------------------------------------------------------- planted mistakes --
+
+def test_checks_catch_planted_mistakes():
+    """A wrong operand (transposed W, dropped bias, X not rounded the way the
+    GPU path rounds it) must fail the parity metric used by the GPU tests."""
+    X = _rand((16, 64), 30, 1.0)
+    W = oracle.f32_to_bf16_rne(_rand((64, 64), 31, 0.02))
+    b = _rand((64,), 32, 0.01)
+    good = oracle.linear_bf16w(X, W, b)
+    Wt = oracle.f32_to_bf16_rne(oracle.bf16_to_f32(W).T.copy())
+    assert oracle.normwise_err(oracle.linear_bf16w(X, Wt, b), good) > 1e-2
+    assert oracle.normwise_err(oracle.linear_bf16w(X, W, None), good) > 1e-3
+    Xs = X.copy()
+    Xs[:, 3] *= -1.0  # a sign error in one column of K
+    assert oracle.normwise_err(oracle.linear_bf16w(Xs, W, b), good) > 1e-3
