@@ -154,6 +154,27 @@ def cpu_baseline(name):
     return out
 
 
+def profile_run(args):
+    """Launches for counter collection: copy_words16 over 512 MiB (known traffic:
+    512 MiB read + 512 MiB written per launch), then the workload."""
+    from invision_amd import hip
+    from invision_amd import quicknn_hip as q
+    n = 512 << 20
+    a = q.DeviceArray((n // 4,), "f32")
+    b = q.DeviceArray((n // 4,), "f32")
+    a.fill_zero()
+    for _ in range(5):
+        hip.call("inv_hip_memcpy_d2d", b.ptr, a.ptr, n)
+    a.free()
+    b.free()
+    log(f"[profile] copy calibration: 5 x copy_words16 of {n} bytes")
+    res = run_workload(args.workload, args.steps, args.warmup, check=False)
+    log(f"[profile] {json.dumps(res)}")
+    print(json.dumps({"profile_run": args.workload, "copy_bytes": n, **res}), flush=True)
+    q.shutdown()
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -162,6 +183,9 @@ def main():
     ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
     ap.add_argument("--all", action="store_true", help="also time every workload shape (stderr)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-run", action="store_true",
+                    help="for rocprofv3 passes: a 512 MiB copy-kernel calibration (5 launches), then --steps "
+                         "launches of the workload; no CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -170,6 +194,8 @@ def main():
     from invision_amd import quicknn_hip as q
     info = q.device_info()
     log(f"[bench] device: {info}")
+    if args.profile_run:
+        return profile_run(args)
 
     res = run_workload(args.workload, args.steps, args.warmup)
     log(f"[bench] {json.dumps(res)}")

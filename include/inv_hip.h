@@ -62,6 +62,16 @@ extern "C" {
 #define INV_FLAG_DEVICE_PTRS 0x1 /* X, Y and bias are device pointers (inv_hip_malloc) */
 #define INV_FLAG_ASYNC       0x2 /* with DEVICE_PTRS: return without waiting; call
                                     inv_hip_synchronize before reading Y            */
+#define INV_FLAG_PRECISE     0x4 /* fp32 X is split into bf16 hi + lo and both halves
+                                    are multiplied (2 MFMA passes): the result then
+                                    matches the reference's fp32-activation GEMM to
+                                    ~1e-5 instead of ~1.5e-3 (no effect for bf16 X)   */
+
+/* ---- precision of the CBLAS fp32 slot (inv_hip_set_sgemm_precision) ----- */
+#define INV_PREC_BF16     0 /* A and B rounded to bf16: 1 MFMA pass                      */
+#define INV_PREC_SPLIT_A  1 /* A split hi + lo, B rounded: 2 passes (exact for bf16 B)    */
+#define INV_PREC_SPLIT_AB 2 /* both split, A.B ~ AhBh + AlBh + AhBl: 3 passes (default),
+                               relative error ~2^-16, the accuracy an fp32 slot expects */
 
 typedef struct inv_weight_s *inv_weight_t; /* opaque device-resident weight */
 
@@ -104,24 +114,33 @@ int inv_hip_linear(const void *X, int x_dtype, inv_weight_t W, const float *bias
 
 /* ---- the CBLAS slots ------------------------------------------------------ */
 /* Exactly the signature of TQNNSingleOPS.cblas_sgemm (src/quicknncpu.pas:
- * 102-103): C = alpha * op(A) . op(B) + beta * C on host fp32 arrays, RowMajor,
- * every NoTrans/Trans combination.  A and B are rounded to bf16 (ties to even)
- * on the device and multiplied with fp32 accumulation; beta == 0 does not read
- * C (BLAS semantics).  Returns a status; the slot's callers ignore it, so the
- * binding checks inv_hip_last_error (see the integration notes). */
+ * 102-103): C = alpha * op(A) . op(B) + beta * C on host fp32 arrays, RowMajor
+ * or ColMajor, every NoTrans/Trans combination.  A and B are converted to bf16
+ * on the device per the slot's precision mode (default INV_PREC_SPLIT_AB) and
+ * multiplied with fp32 accumulation; beta == 0 does not read C (BLAS
+ * semantics).  Returns a status; the slot's callers ignore it, so the binding
+ * checks the status itself. */
 int inv_hip_sgemm(int order, int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha,
                   const float *A, int64_t lda, const float *B, int64_t ldb, float beta, float *C,
                   int64_t ldc);
-/* TQNNSingleOPS.cblas_sbgemm (src/quicknncpu.pas:110-111): bf16 A and B. */
+/* TQNNSingleOPS.cblas_sbgemm (src/quicknncpu.pas:110-111): bf16 A and B
+ * (exact in one MFMA pass). */
 int inv_hip_sbgemm(int order, int transA, int transB, int64_t M, int64_t N, int64_t K, float alpha,
                    const uint16_t *A, int64_t lda, const uint16_t *B, int64_t ldb, float beta, float *C,
                    int64_t ldc);
+
+/* Precision of inv_hip_sgemm for subsequent calls (INV_PREC_*).  No
+ * counterpart in the reference, whose fp32 slot is always fp32. */
+int inv_hip_set_sgemm_precision(int mode);
 
 /* ---- device memory and timing, for callers that keep activations resident */
 int inv_hip_malloc(void **ptr, size_t bytes);
 int inv_hip_free(void *ptr);
 int inv_hip_memcpy_h2d(void *dst, const void *src, size_t bytes);
 int inv_hip_memcpy_d2h(void *dst, const void *src, size_t bytes);
+/* Device-to-device copy on the library stream (a 16-byte-word copy kernel when
+ * both pointers and the size are 16-byte granular). */
+int inv_hip_memcpy_d2d(void *dst, const void *src, size_t bytes);
 int inv_hip_memset(void *dst, int value, size_t bytes);
 int inv_hip_synchronize(void);
 /* HIP events recorded on the library stream: start, then stop -> elapsed ms. */

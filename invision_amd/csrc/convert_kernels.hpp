@@ -24,11 +24,33 @@ __device__ __forceinline__ uint16_t bf16_rne(float f) {
     return (uint16_t)(u >> 16);
 }
 
-// dst[r, c] = bf16(src[r, c]) for c < cols, 0 for cols <= c < cols_pad.
-// One thread per 8 outputs; cols_pad % 8 == 0, ldd % 8 == 0, dst 16-B aligned.
+// Split of an fp32 value into two bf16: hi = RNE(v), lo = RNE(v - hi), so that
+// hi + lo carries 16 significant bits; a product (Ah + Al)(Bh + Bl) then
+// differs from AB by the dropped Al*Bl term (relative 2^-16 or less).
+__device__ __forceinline__ void bf16_split(float v, uint16_t &hi, uint16_t &lo) {
+    hi = bf16_rne(v);
+    const float h = __uint_as_float((uint32_t)hi << 16);
+    lo = ((hi & 0x7f80u) == 0x7f80u) ? (uint16_t)0 : bf16_rne(v - h);
+}
+
+__device__ __forceinline__ uint4 pack8(const uint16_t (&h)[8]) {
+    uint4 o;
+    o.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+    o.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+    o.z = (uint32_t)h[4] | ((uint32_t)h[5] << 16);
+    o.w = (uint32_t)h[6] | ((uint32_t)h[7] << 16);
+    return o;
+}
+
+// Row-wise fp32 -> bf16 with nseg segments per output row: segment s of row r
+// starts at dst + r*ldd + s*cols_pad and holds lo parts if bit s of lo_mask is
+// set, hi parts otherwise (nseg = 1, lo_mask = 0: plain RNE rounding).
+// Columns cols..cols_pad-1 of each segment are zero.  One thread per 8 columns;
+// cols_pad % 8 == 0, ldd % 8 == 0, dst 16-byte aligned.
 __global__ void __launch_bounds__(256) cvt_rows_f32_bf16(const float *__restrict__ src, int64_t lds,
                                                          uint16_t *__restrict__ dst, int64_t ldd, int64_t rows,
-                                                         int64_t cols, int64_t cols_pad, int vec_src) {
+                                                         int64_t cols, int64_t cols_pad, int vec_src, int nseg,
+                                                         int lo_mask) {
     const int64_t per_row = cols_pad >> 3;
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= rows * per_row) return;
@@ -45,12 +67,13 @@ __global__ void __launch_bounds__(256) cvt_rows_f32_bf16(const float *__restrict
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = (c0 + e < cols) ? s[e] : 0.0f;
     }
-    uint4 o;
-    o.x = (uint32_t)bf16_rne(v[0]) | ((uint32_t)bf16_rne(v[1]) << 16);
-    o.y = (uint32_t)bf16_rne(v[2]) | ((uint32_t)bf16_rne(v[3]) << 16);
-    o.z = (uint32_t)bf16_rne(v[4]) | ((uint32_t)bf16_rne(v[5]) << 16);
-    o.w = (uint32_t)bf16_rne(v[6]) | ((uint32_t)bf16_rne(v[7]) << 16);
-    *(uint4 *)(dst + r * ldd + c0) = o;
+    uint16_t hi[8], lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) bf16_split(v[e], hi[e], lo[e]);
+    const uint4 ohi = pack8(hi);
+    const uint4 olo = pack8(lo);
+    uint16_t *d = dst + r * ldd + c0;
+    for (int sg = 0; sg < nseg; ++sg) *(uint4 *)(d + sg * cols_pad) = ((lo_mask >> sg) & 1) ? olo : ohi;
 }
 
 // dst[r, c] = src[r, c] (bf16) for c < cols, 0 up to cols_pad.  One thread per 8 outputs.
@@ -74,33 +97,46 @@ __global__ void __launch_bounds__(256) copy_rows_bf16(const uint16_t *__restrict
     *(uint4 *)(dst + r * ldd + c0) = o;
 }
 
-// dst[c, r] = bf16(src[r, c]) : src [rows x cols] (ld lds) -> dst [cols x rows_pad]
-// (ld ldd), zero for rows <= r < rows_pad.  64x64 tiles through LDS.
+// dst[c, s*rows_pad + r] = part_s(src[r, c]) : src [rows x cols] (ld lds) ->
+// dst [cols x nseg*rows_pad] (ld ldd), parts as in cvt_rows_f32_bf16, zero for
+// rows <= r < rows_pad.  64x64 tiles through LDS.
 template <typename SrcT>
 __global__ void __launch_bounds__(256) transpose_to_bf16(const SrcT *__restrict__ src, int64_t lds,
                                                          uint16_t *__restrict__ dst, int64_t ldd, int64_t rows,
-                                                         int64_t cols, int64_t rows_pad) {
-    __shared__ uint16_t tile[64][65];
+                                                         int64_t cols, int64_t rows_pad, int nseg, int lo_mask) {
+    __shared__ float tile[64][65];
     const int64_t r0 = (int64_t)blockIdx.y * 64;
     const int64_t c0 = (int64_t)blockIdx.x * 64;
     const int tx = threadIdx.x & 63;
     const int ty = threadIdx.x >> 6;  // 0..3
     for (int i = ty; i < 64; i += 4) {
         const int64_t r = r0 + i, c = c0 + tx;
-        uint16_t v = 0;
+        float v = 0.0f;
         if (r < rows && c < cols) {
             if constexpr (sizeof(SrcT) == 4)
-                v = bf16_rne((float)src[r * lds + c]);
+                v = (float)src[r * lds + c];
             else
-                v = (uint16_t)src[r * lds + c];
+                v = __uint_as_float((uint32_t)src[r * lds + c] << 16);
         }
         tile[i][tx] = v;
     }
     __syncthreads();
     for (int i = ty; i < 64; i += 4) {
         const int64_t c = c0 + i, r = r0 + tx;
-        if (c < cols && r < rows_pad) dst[c * ldd + r] = tile[tx][i];
+        if (c < cols && r < rows_pad) {
+            uint16_t hi, lo;
+            bf16_split(tile[tx][i], hi, lo);
+            for (int sg = 0; sg < nseg; ++sg) dst[c * ldd + sg * rows_pad + r] = ((lo_mask >> sg) & 1) ? lo : hi;
+        }
     }
+}
+
+// dst[i] = src[i] for n16 16-byte words, grid-stride (device-to-device copy of
+// resident buffers; also the reference kernel of known traffic, 2 x bytes).
+__global__ void __launch_bounds__(256) copy_words16(const uint4 *__restrict__ src, uint4 *__restrict__ dst,
+                                                    int64_t n16) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
 }
 
 }  // namespace inv

@@ -48,7 +48,8 @@ struct GemmParams {
     const float *bias;  // [N] or null
     const float *Cin;   // [M x ldc] f32, read when beta != 0
     int64_t ldw, ldx, ldy, ldc;
-    int M, N, K;
+    int M, N, K;  // K: the reduction length of X (and of W unless it wraps)
+    int w_seg_tiles, Kw;  // W wraps every w_seg_tiles k-tiles (0: no wrap); Kw: valid K of W
     int tiles_m, tiles_n, group_m;
     int ksplit, kt_per_split;  // K tiles per split
     float alpha, beta;
@@ -128,17 +129,24 @@ struct TileCfg {
 template <class C>
 __device__ __forceinline__ void issue_tile_loads(__amdgpu_buffer_rsrc_t rsw, __amdgpu_buffer_rsrc_t rsx,
                                                  lds_char_t *stage, int wave, uint32_t a_base, uint32_t a_step,
-                                                 uint32_t b_base, uint32_t b_step, uint32_t kadd) {
+                                                 uint32_t b_base, uint32_t b_step, uint32_t kadd_a,
+                                                 uint32_t kadd_b) {
     lds_char_t *sa = stage + wave * 1024;
     lds_char_t *sb = sa + C::A_BYTES;
 #pragma unroll
     for (int i = 0; i < C::A_LOADS; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, sa + i * C::NTHREADS * 16, 16, a_base + i * a_step + kadd, 0,
-                                                 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, sa + i * C::NTHREADS * 16, 16, a_base + i * a_step + kadd_a,
+                                                 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < C::B_LOADS; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsx, sb + i * C::NTHREADS * 16, 16, b_base + i * b_step + kadd, 0,
-                                                 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsx, sb + i * C::NTHREADS * 16, 16, b_base + i * b_step + kadd_b,
+                                                 0, 0, 0);
+}
+
+// Byte offset of k-tile `ktile` in a row, or an offset past every buffer
+// (reads as zeros) when the chunk is not valid.
+__device__ __forceinline__ uint32_t k_byte_offset(bool valid, int ktile) {
+    return valid ? (uint32_t)(ktile * 64) * 2 : 0x80000000u;
 }
 
 // MFMA fragments of one 16-wide k substep: FN rows blocks of W, FM of X.
@@ -240,10 +248,14 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_bf16_kernel(const GemmParams p
     // A k-tile at or past kt_end gets out-of-range offsets for every lane, so
     // its copy writes zeros and reads nothing; the prefetch of the next tile
     // is then unconditional and the loop body stays one basic block.
+    // W may wrap along K (split-precision passes reuse the resident weight):
+    // its k-tile index runs modulo w_seg_tiles, tracked incrementally.
+    int ktw = p.w_seg_tiles ? kt_begin % p.w_seg_tiles : kt_begin;
     {
-        const bool valid = (kt_begin < kt_end) && (kt_begin * BK + ld_chunk * 8) < p.K;
+        const bool in = kt_begin < kt_end;
         issue_tile_loads<C>(rsw, rsx, lds, wave, a_base, a_step, b_base, b_step,
-                            valid ? (uint32_t)(kt_begin * BK) * 2 : 0x80000000u);
+                            k_byte_offset(in && ktw * BK + ld_chunk * 8 < p.Kw, ktw),
+                            k_byte_offset(in && kt_begin * BK + ld_chunk * 8 < p.K, kt_begin));
     }
 
     for (int kt = kt_begin; kt < kt_end; ++kt) {
@@ -252,9 +264,11 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_bf16_kernel(const GemmParams p
         __syncthreads();
         {
             const int kn = kt + 1;
-            const bool valid = (kn < kt_end) && (kn * BK + ld_chunk * 8) < p.K;
+            ktw = (p.w_seg_tiles && ktw + 1 == p.w_seg_tiles) ? 0 : ktw + 1;
+            const bool in = kn < kt_end;
             issue_tile_loads<C>(rsw, rsx, lds + (stage ^ 1) * C::STAGE_BYTES, wave, a_base, a_step, b_base, b_step,
-                                valid ? (uint32_t)(kn * BK) * 2 : 0x80000000u);
+                                k_byte_offset(in && ktw * BK + ld_chunk * 8 < p.Kw, ktw),
+                                k_byte_offset(in && kn * BK + ld_chunk * 8 < p.K, kn));
         }
 
         const lds_char_t *sbase = lds + stage * C::STAGE_BYTES;

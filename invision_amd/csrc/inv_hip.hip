@@ -68,6 +68,7 @@ struct State {
     int cu_count = 0, clock_khz = 0;
     char name[256] = {0};
     Buf xin, x16, w16, win, yout, cin, bias, partial, counters;
+    int sgemm_prec = INV_PREC_SPLIT_AB;
     bool stats = false;
     int64_t calls = 0;
     double gemm_ms = 0.0, flops = 0.0;
@@ -297,7 +298,7 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
 // W [N x ldw], X [M x ldx] bf16 device; K a multiple of 8 (zero padded).
 int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, void *Y, int64_t ldy, int out,
              const float *bias, const float *Cin, int64_t ldc, float alpha, float beta, int64_t M, int64_t N,
-             int64_t K, int epi) {
+             int64_t K, int epi, int w_seg_tiles = 0, int64_t Kw = -1) {
     if (M == 0 || N == 0) return INV_OK;
     if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return fail(INV_ERR_ARG, "dimension too large");
     if (K % 8 || ldw % 8 || ldx % 8 || !aligned(W, 16) || !aligned(X, 16))
@@ -318,6 +319,8 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
     p.M = (int)M;
     p.N = (int)N;
     p.K = (int)K;
+    p.w_seg_tiles = w_seg_tiles;
+    p.Kw = (int)(Kw < 0 ? K : Kw);
     p.tiles_m = (int)((M + kCfgTM[tc.cfg] - 1) / kCfgTM[tc.cfg]);
     p.tiles_n = (int)((N + kCfgTN[tc.cfg] - 1) / kCfgTN[tc.cfg]);
     p.group_m = std::max(1, std::min(p.tiles_m, env_int("INV_HIP_GROUP_M", 4)));
@@ -364,12 +367,12 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
 }
 
 int launch_cvt_rows_f32(const float *src, int64_t lds, uint16_t *dst, int64_t ldd, int64_t rows, int64_t cols,
-                        int64_t cols_pad) {
+                        int64_t cols_pad, int nseg = 1, int lo_mask = 0) {
     if (rows == 0) return INV_OK;
     int64_t work = rows * (cols_pad / 8);
     int vec = aligned(src, 16) && (lds % 4 == 0);
     hipLaunchKernelGGL(inv::cvt_rows_f32_bf16, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, g.stream, src, lds,
-                       dst, ldd, rows, cols, cols_pad, vec);
+                       dst, ldd, rows, cols, cols_pad, vec, nseg, lo_mask);
     HIPCHK(hipGetLastError());
     return INV_OK;
 }
@@ -387,12 +390,12 @@ int launch_copy_rows_bf16(const uint16_t *src, int64_t lds, uint16_t *dst, int64
 // src [rows x cols] -> dst [cols x rows_pad] bf16
 template <typename T>
 int launch_transpose(const T *src, int64_t lds, uint16_t *dst, int64_t ldd, int64_t rows, int64_t cols,
-                     int64_t rows_pad) {
+                     int64_t rows_pad, int nseg = 1, int lo_mask = 0) {
     if (rows_pad == 0 || cols == 0) return INV_OK;
     dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows_pad + 63) / 64));
     if (grid.y > 65535) return fail(INV_ERR_UNSUPPORTED, "transpose: too many rows");
     hipLaunchKernelGGL(inv::transpose_to_bf16<T>, grid, dim3(256), 0, g.stream, src, lds, dst, ldd, rows, cols,
-                       rows_pad);
+                       rows_pad, nseg, lo_mask);
     HIPCHK(hipGetLastError());
     return INV_OK;
 }
@@ -478,17 +481,23 @@ void free_weight(inv_weight_s *w) {
     delete w;
 }
 
-// Stage an operand as bf16 rows [rows x cols_pad] with K contiguous.
-//  src: host or device; dtype f32/bf16; trans: src holds the operand transposed
-//  ([cols x rows] with leading dimension ld).
+// Stage an operand as bf16 rows with K contiguous: [rows x nseg*cols_pad],
+// cols_pad = cols rounded up to seg_align (a multiple of 8).  With nseg > 1
+// (fp32 sources only) segment s holds the lo parts of a hi/lo bf16 split if bit
+// s of lo_mask is set, the hi parts otherwise.
+//  src: host or device; dtype f32/bf16; trans: src holds the operand
+//  transposed ([cols x rows] with leading dimension ld).
 int stage_operand(const void *src, int dtype, bool on_device, bool trans, int64_t rows, int64_t cols, int64_t ld,
-                  Buf &dst, Buf &tmp, const uint16_t **out, int64_t *out_ld) {
+                  int nseg, int lo_mask, int64_t seg_align, Buf &dst, Buf &tmp, const uint16_t **out,
+                  int64_t *out_ld) {
     const size_t esz = dtype == INV_DT_F32 ? 4 : 2;
-    const int64_t cols_pad = round_up(cols, 8);
+    const int64_t cols_pad = round_up(cols, seg_align);
+    const int64_t row_w = nseg * cols_pad;
     const int64_t src_rows = trans ? cols : rows;
     const int64_t src_cols = trans ? rows : cols;
+    if (dtype == INV_DT_BF16 && nseg != 1) return fail(INV_ERR_ARG, "internal: split of a bf16 operand");
     // bf16, not transposed, already 16-byte granular on the device: use in place.
-    if (on_device && dtype == INV_DT_BF16 && !trans && cols % 8 == 0 && ld % 8 == 0 && aligned(src, 16)) {
+    if (on_device && dtype == INV_DT_BF16 && !trans && cols == cols_pad && ld % 8 == 0 && aligned(src, 16)) {
         *out = (const uint16_t *)src;
         *out_ld = ld;
         return INV_OK;
@@ -509,22 +518,22 @@ int stage_operand(const void *src, int dtype, bool on_device, bool trans, int64_
         dsrc = tmp.p;
         dld = src_cols;
     }
-    TRY(ensure(dst, (size_t)(rows * cols_pad) * 2));
+    TRY(ensure(dst, (size_t)(rows * row_w) * 2));
     uint16_t *d = (uint16_t *)dst.p;
     if (!trans) {
         if (dtype == INV_DT_F32)
-            TRY(launch_cvt_rows_f32((const float *)dsrc, dld, d, cols_pad, rows, cols, cols_pad));
+            TRY(launch_cvt_rows_f32((const float *)dsrc, dld, d, row_w, rows, cols, cols_pad, nseg, lo_mask));
         else
-            TRY(launch_copy_rows_bf16((const uint16_t *)dsrc, dld, d, cols_pad, rows, cols, cols_pad));
+            TRY(launch_copy_rows_bf16((const uint16_t *)dsrc, dld, d, row_w, rows, cols, cols_pad));
     } else {
-        // dsrc is [cols x rows] (ld dld) -> d [rows x cols_pad]
+        // dsrc is [cols x rows] (ld dld) -> d [rows x row_w]
         if (dtype == INV_DT_F32)
-            TRY(launch_transpose<float>((const float *)dsrc, dld, d, cols_pad, cols, rows, cols_pad));
+            TRY(launch_transpose<float>((const float *)dsrc, dld, d, row_w, cols, rows, cols_pad, nseg, lo_mask));
         else
-            TRY(launch_transpose<uint16_t>((const uint16_t *)dsrc, dld, d, cols_pad, cols, rows, cols_pad));
+            TRY(launch_transpose<uint16_t>((const uint16_t *)dsrc, dld, d, row_w, cols, rows, cols_pad, 1, 0));
     }
     *out = d;
-    *out_ld = cols_pad;
+    *out_ld = row_w;
     return INV_OK;
 }
 
@@ -557,12 +566,28 @@ int gemm_slot(int order, int transA, int transB, int64_t M, int64_t N, int64_t K
     const int64_t Kp = round_up(std::max<int64_t>(K, 1), 8);
     const uint16_t *Xd = nullptr, *Wd = nullptr;
     int64_t ldx = 0, ldw = 0;
+    // Precision: fp32 operands are rounded to bf16 (1 pass), or split into
+    // hi + lo and concatenated along K: A' = [Ah|Al], B' = [Bh|Bh] (2 passes)
+    // or A' = [Ah|Al|Ah], B' = [Bh|Bh|Bl] (3 passes, ~fp32 accuracy).
+    int nseg = 1, amask = 0, bmask = 0;
+    if (dtype == INV_DT_F32) {
+        if (g.sgemm_prec == INV_PREC_SPLIT_A) {
+            nseg = 2;
+            amask = 0x2;
+        } else if (g.sgemm_prec == INV_PREC_SPLIT_AB) {
+            nseg = 3;
+            amask = 0x2;
+            bmask = 0x4;
+        }
+    }
+    int64_t Kgemm = nseg * Kp;
     if (K > 0) {
         // X = op(A) [M x K]: stored transposed when A is Trans.
-        TRY(stage_operand(A, dtype, false, ta, M, K, lda, g.x16, g.xin, &Xd, &ldx));
+        TRY(stage_operand(A, dtype, false, ta, M, K, lda, nseg, amask, 8, g.x16, g.xin, &Xd, &ldx));
         // W = op(B)^T [N x K]: B is [N x K] when Trans, [K x N] (transposed) otherwise.
-        TRY(stage_operand(B, dtype, false, !tb, N, K, ldb, g.w16, g.win, &Wd, &ldw));
+        TRY(stage_operand(B, dtype, false, !tb, N, K, ldb, nseg, bmask, 8, g.w16, g.win, &Wd, &ldw));
     } else {
+        Kgemm = 8;
         // K == 0: C = beta * C.  Zero operands of width 8.
         TRY(ensure(g.x16, (size_t)(M * 8) * 2));
         TRY(ensure(g.w16, (size_t)(N * 8) * 2));
@@ -579,7 +604,8 @@ int gemm_slot(int order, int transA, int transB, int64_t M, int64_t N, int64_t K
         TRY(h2d_rows(g.cin.p, C, M, (size_t)N * 4, (size_t)ldc * 4));
         cin = (const float *)g.cin.p;
     }
-    TRY(run_gemm(Wd, ldw, Xd, ldx, g.yout.p, N, inv::OUT_F32, nullptr, cin, N, alpha, beta, M, N, Kp, inv::EPI_NONE));
+    TRY(run_gemm(Wd, ldw, Xd, ldx, g.yout.p, N, inv::OUT_F32, nullptr, cin, N, alpha, beta, M, N, Kgemm,
+                 inv::EPI_NONE));
     TRY(d2h_rows(C, g.yout.p, M, (size_t)N * 4, (size_t)ldc * 4));
     g.calls++;
     return INV_OK;
@@ -711,7 +737,8 @@ int inv_hip_linear(const void *X, int x_dtype, inv_weight_t W, const float *bias
     if (x_dtype != INV_DT_F32 && x_dtype != INV_DT_BF16) return fail(INV_ERR_ARG, "linear: bad x_dtype %d", x_dtype);
     if (y_dtype != INV_DT_F32 && y_dtype != INV_DT_BF16) return fail(INV_ERR_ARG, "linear: bad y_dtype %d", y_dtype);
     if (!epi_ok(epilogue)) return fail(INV_ERR_ARG, "linear: bad epilogue %d", epilogue);
-    if (flags & ~(INV_FLAG_DEVICE_PTRS | INV_FLAG_ASYNC)) return fail(INV_ERR_ARG, "linear: unknown flags 0x%x", flags);
+    if (flags & ~(INV_FLAG_DEVICE_PTRS | INV_FLAG_ASYNC | INV_FLAG_PRECISE))
+        return fail(INV_ERR_ARG, "linear: unknown flags 0x%x", flags);
     if ((flags & INV_FLAG_ASYNC) && !(flags & INV_FLAG_DEVICE_PTRS))
         return fail(INV_ERR_ARG, "linear: ASYNC requires DEVICE_PTRS");
     if (M < 0) return fail(INV_ERR_ARG, "linear: negative M");
@@ -725,10 +752,15 @@ int inv_hip_linear(const void *X, int x_dtype, inv_weight_t W, const float *bias
     const int out = (y_dtype == INV_DT_F32) ? inv::OUT_F32 : inv::OUT_BF16;
     const size_t ysz = (y_dtype == INV_DT_F32) ? 4 : 2;
 
-    // Activations -> bf16 [M x ldw] (ldw = K rounded up to 8, zero padded).
+    // Activations -> bf16 [M x ldw] (ldw = K rounded up to 8, zero padded), or
+    // with INV_FLAG_PRECISE and fp32 X: [Xh | Xl], each half K rounded up to 64,
+    // multiplied against the resident W read twice (the W k-tiles wrap).
+    const bool precise = (flags & INV_FLAG_PRECISE) && x_dtype == INV_DT_F32;
     const uint16_t *Xd = nullptr;
     int64_t ldx = 0;
-    TRY(stage_operand(X, x_dtype, dev, false, M, K, K, g.x16, g.xin, &Xd, &ldx));
+    const int64_t kseg = precise ? round_up(K, 64) : W->ldw;
+    TRY(stage_operand(X, x_dtype, dev, false, M, K, K, precise ? 2 : 1, precise ? 0x2 : 0, precise ? 64 : 8, g.x16,
+                      g.xin, &Xd, &ldx));
 
     // Bias: explicit argument first, else the handle's.
     const float *bd = W->bias;
@@ -750,13 +782,25 @@ int inv_hip_linear(const void *X, int x_dtype, inv_weight_t W, const float *bias
         TRY(ensure(g.yout, (size_t)(M * N) * ysz));
         Yd = g.yout.p;
     }
-    TRY(run_gemm(W->w, W->ldw, Xd, ldx, Yd, N, out, bd, nullptr, 0, 1.0f, 0.0f, M, N, W->ldw, epilogue));
+    if (precise)
+        TRY(run_gemm(W->w, W->ldw, Xd, ldx, Yd, N, out, bd, nullptr, 0, 1.0f, 0.0f, M, N, 2 * kseg, epilogue,
+                     (int)(kseg / 64), W->ldw));
+    else
+        TRY(run_gemm(W->w, W->ldw, Xd, ldx, Yd, N, out, bd, nullptr, 0, 1.0f, 0.0f, M, N, W->ldw, epilogue));
     g.calls++;
     if (!dev) {
         TRY(d2h_rows(Y, Yd, M, (size_t)N * ysz, (size_t)N * ysz));
     } else if (!(flags & INV_FLAG_ASYNC)) {
         HIPCHK(hipStreamSynchronize(g.stream));
     }
+    return INV_OK;
+}
+
+int inv_hip_set_sgemm_precision(int mode) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (mode != INV_PREC_BF16 && mode != INV_PREC_SPLIT_A && mode != INV_PREC_SPLIT_AB)
+        return fail(INV_ERR_ARG, "bad precision mode %d", mode);
+    g.sgemm_prec = mode;
     return INV_OK;
 }
 
@@ -810,6 +854,24 @@ int inv_hip_memcpy_d2h(void *dst, const void *src, size_t bytes) {
     if (!bytes) return INV_OK;
     if (!dst || !src) return fail(INV_ERR_ARG, "memcpy_d2h: null pointer");
     return d2h_rows(dst, src, 1, bytes, bytes);
+}
+
+int inv_hip_memcpy_d2d(void *dst, const void *src, size_t bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    TRY(check_init());
+    if (!bytes) return INV_OK;
+    if (!dst || !src) return fail(INV_ERR_ARG, "memcpy_d2d: null pointer");
+    if (aligned(dst, 16) && aligned(src, 16) && bytes % 16 == 0) {
+        const int64_t n16 = (int64_t)(bytes / 16);
+        const int64_t blocks = std::min<int64_t>((n16 + 255) / 256, (int64_t)g.cu_count * 16);
+        hipLaunchKernelGGL(inv::copy_words16, dim3((unsigned)blocks), dim3(256), 0, g.stream, (const uint4 *)src,
+                           (uint4 *)dst, n16);
+        HIPCHK(hipGetLastError());
+    } else {
+        HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g.stream));
+    }
+    HIPCHK(hipStreamSynchronize(g.stream));
+    return INV_OK;
 }
 
 int inv_hip_memset(void *dst, int value, size_t bytes) {

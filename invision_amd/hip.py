@@ -37,6 +37,11 @@ INV_EPI_GELU_ERF = 2
 
 INV_FLAG_DEVICE_PTRS = 0x1
 INV_FLAG_ASYNC = 0x2
+INV_FLAG_PRECISE = 0x4
+
+INV_PREC_BF16 = 0
+INV_PREC_SPLIT_A = 1
+INV_PREC_SPLIT_AB = 2
 
 # Every symbol include/inv_hip.h declares, with (restype, argtypes).
 _PROTOS = {
@@ -55,10 +60,12 @@ _PROTOS = {
                               c_int64, c_float, c_void_p, c_int64]),
     "inv_hip_sbgemm": (c_int, [c_int, c_int, c_int, c_int64, c_int64, c_int64, c_float, c_void_p, c_int64, c_void_p,
                                c_int64, c_float, c_void_p, c_int64]),
+    "inv_hip_set_sgemm_precision": (c_int, [c_int]),
     "inv_hip_malloc": (c_int, [POINTER(c_void_p), c_size_t]),
     "inv_hip_free": (c_int, [c_void_p]),
     "inv_hip_memcpy_h2d": (c_int, [c_void_p, c_void_p, c_size_t]),
     "inv_hip_memcpy_d2h": (c_int, [c_void_p, c_void_p, c_size_t]),
+    "inv_hip_memcpy_d2d": (c_int, [c_void_p, c_void_p, c_size_t]),
     "inv_hip_memset": (c_int, [c_void_p, c_int, c_size_t]),
     "inv_hip_synchronize": (c_int, []),
     "inv_hip_timer_start": (c_int, []),

@@ -160,15 +160,16 @@ _EPI = {"none": hip.INV_EPI_NONE, "silu": hip.INV_EPI_SILU, "gelu": hip.INV_EPI_
 
 
 def linear_device(x: DeviceArray, W: Weight, y: DeviceArray, M: int, epilogue: str = "none",
-                  bias: Optional[DeviceArray] = None, asynchronous: bool = False) -> None:
+                  bias: Optional[DeviceArray] = None, asynchronous: bool = False, precise: bool = False) -> None:
     """inv_hip_linear on device-resident activations: y = epi(x . W^T + bias)."""
     flags = hip.INV_FLAG_DEVICE_PTRS | (hip.INV_FLAG_ASYNC if asynchronous else 0)
+    flags |= hip.INV_FLAG_PRECISE if precise else 0
     hip.call("inv_hip_linear", x.ptr, x.inv_dtype, W.handle, bias.ptr if bias is not None else None, y.ptr,
              y.inv_dtype, M, W.K, W.N, _EPI[epilogue], flags)
 
 
 def linear(x: np.ndarray, W: Weight, bias: Optional[np.ndarray] = None, epilogue: str = "none",
-           out_dtype: str = "f32") -> np.ndarray:
+           out_dtype: str = "f32", precise: bool = False) -> np.ndarray:
     """Host arrays in and out: Y[M x N] = epi(X[M x K] . W^T + bias)."""
     if x.dtype not in (np.float32, np.uint16):
         raise TypeError("x must be float32 or bf16 bits (uint16)")
@@ -181,8 +182,14 @@ def linear(x: np.ndarray, W: Weight, bias: Optional[np.ndarray] = None, epilogue
     y = np.empty((M, W.N), dtype=ynp)
     b = np.ascontiguousarray(bias, dtype=np.float32) if bias is not None else None
     hip.call("inv_hip_linear", _ptr(x), xdt, W.handle, _ptr(b) if b is not None else None, _ptr(y), ydt, M, W.K,
-             W.N, _EPI[epilogue], 0)
+             W.N, _EPI[epilogue], hip.INV_FLAG_PRECISE if precise else 0)
     return y
+
+
+def set_sgemm_precision(mode: int) -> None:
+    """INV_PREC_BF16 / INV_PREC_SPLIT_A / INV_PREC_SPLIT_AB for cblas_gemm."""
+    init()
+    hip.call("inv_hip_set_sgemm_precision", mode)
 
 
 # ---------------------------------------------------------------------------

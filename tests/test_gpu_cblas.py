@@ -39,16 +39,40 @@ def oracle_gemm(ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C0, ldc):
 @pytest.mark.parametrize("M,N,K", [(37, 53, 129), (256, 128, 512), (5, 300, 64)])
 @pytest.mark.parametrize("alpha,beta", [(1.0, 0.0), (0.75, -0.5)])
 def test_sgemm_all_transposes(hiplib, ta, tb, M, N, K, alpha, beta):
+    # Default precision (INV_PREC_SPLIT_AB): fp32-slot accuracy.
     A = rnd((K, M) if ta == T else (M, K), 1)
     B = rnd((N, K) if tb == T else (K, N), 2, 0.05)
     lda, ldb = A.shape[1], B.shape[1]
     C0 = rnd((M, N), 3)
     C = C0.copy()
     q.cblas_gemm(hip.CblasRowMajor, ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, N)
-    want_tight = oracle_gemm(ta, tb, M, N, K, alpha, round_bf16(A), lda, round_bf16(B), ldb, beta, C0, N)
     want_ref = oracle_gemm(ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C0, N)
-    assert oracle.normwise_err(C, want_tight) <= 2e-5
-    assert oracle.normwise_err(C, want_ref) <= 2e-3
+    err = oracle.normwise_err(C, want_ref)
+    print(f"  split-AB sgemm vs fp32 qgemm: {err:.3e}", flush=True)
+    assert err <= 5e-5
+
+
+@pytest.mark.parametrize("mode", [hip.INV_PREC_BF16, hip.INV_PREC_SPLIT_A, hip.INV_PREC_SPLIT_AB])
+def test_sgemm_precision_modes(hiplib, mode):
+    M, N, K = 96, 160, 384
+    A = rnd((M, K), 21)
+    B = rnd((N, K), 22, 0.05)
+    C = np.zeros((M, N), np.float32)
+    q.set_sgemm_precision(mode)
+    try:
+        q.cblas_gemm(hip.CblasRowMajor, NT, T, M, N, K, 1.0, A, K, B, K, 0.0, C, N)
+    finally:
+        q.set_sgemm_precision(hip.INV_PREC_SPLIT_AB)
+    ref32 = oracle_gemm(NT, T, M, N, K, 1.0, A, K, B, K, 0.0, np.zeros((M, N), np.float32), N)
+    if mode == hip.INV_PREC_BF16:
+        tight = oracle_gemm(NT, T, M, N, K, 1.0, round_bf16(A), K, round_bf16(B), K, 0.0, np.zeros_like(C), N)
+        assert oracle.normwise_err(C, tight) <= 2e-5
+        assert oracle.normwise_err(C, ref32) <= 4e-3  # both operands rounded: twice the linear budget
+    elif mode == hip.INV_PREC_SPLIT_A:
+        tight = oracle_gemm(NT, T, M, N, K, 1.0, A, K, round_bf16(B), K, 0.0, np.zeros_like(C), N)
+        assert oracle.normwise_err(C, tight) <= 5e-5
+    else:
+        assert oracle.normwise_err(C, ref32) <= 5e-5
 
 
 def test_sgemm_leading_dimensions_and_untouched_padding(hiplib):
@@ -58,8 +82,8 @@ def test_sgemm_leading_dimensions_and_untouched_padding(hiplib):
     B = rnd((N, ldb), 5, 0.05)
     C = np.full((M, ldc), 7.0, np.float32)
     q.cblas_gemm(hip.CblasRowMajor, NT, T, M, N, K, 1.0, A, lda, B, ldb, 0.0, C, ldc)
-    want = oracle.linear_bf16w(round_bf16(A[:, :K]), as_bf16_bits(B[:, :K]))
-    assert oracle.normwise_err(C[:, :N], want) <= 2e-5
+    want = A[:, :K].astype(np.float64) @ B[:, :K].astype(np.float64).T
+    assert oracle.normwise_err(C[:, :N], want) <= 5e-5
     assert np.all(C[:, N:] == 7.0)  # bytes between rows are not written
 
 
@@ -69,8 +93,8 @@ def test_sgemm_col_major(hiplib):
     B = rnd((N, K), 7)   # col-major K x N  == row-major N x K
     Ccm = np.zeros((N, M), np.float32)  # col-major M x N, ldc = M
     q.cblas_gemm(hip.CblasColMajor, NT, NT, M, N, K, 1.0, A, M, B, K, 0.0, Ccm, M)
-    want = round_bf16(A).T.astype(np.float64) @ round_bf16(B).T.astype(np.float64)
-    assert oracle.normwise_err(Ccm.T, want) <= 2e-5
+    want = A.T.astype(np.float64) @ B.T.astype(np.float64)
+    assert oracle.normwise_err(Ccm.T, want) <= 5e-5
 
 
 def test_sgemm_k_zero_scales_c(hiplib):
@@ -132,8 +156,8 @@ def test_qnnlinear_family_matches_oracle(hiplib):
         q.QNNLinearNoBias(y, X, w, M, K, N)
     assert oracle.normwise_err(y, ref_nb) <= 2e-5
     c = np.zeros((M, N), np.float32)
-    q.QNNMatMulNT(c, X, Wf, M, K, N)
-    assert oracle.normwise_err(c, ref_nb) <= 2e-5
+    q.QNNMatMulNT(c, X, Wf, M, K, N)  # the fp32 CBLAS slot: ~fp32 accuracy
+    assert oracle.normwise_err(c, oracle.linear_bf16w(X, Wb)) <= 5e-5
 
 
 def test_qnnmatmul_nn_tn(hiplib):
@@ -142,8 +166,8 @@ def test_qnnmatmul_nn_tn(hiplib):
     B = rnd((K, N), 14)
     C = np.zeros((M, N), np.float32)
     q.QNNMatMulNN(C, A, B, M, K, N)
-    want = round_bf16(A).astype(np.float64) @ round_bf16(B).astype(np.float64)
-    assert oracle.normwise_err(C, want) <= 2e-5
+    want = A.astype(np.float64) @ B.astype(np.float64)
+    assert oracle.normwise_err(C, want) <= 5e-5
 
 
 def test_reference_assertions_are_kept(hiplib):

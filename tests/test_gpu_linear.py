@@ -109,6 +109,20 @@ def test_golden_linear_fixtures(hiplib):
         assert oracle.normwise_err(y, Y) <= TOL_TIGHT, i
 
 
+@pytest.mark.parametrize("M,K,N", [(64, 200, 96), (300, 1000, 520), (4608, 3072, 256)])
+def test_precise_flag_matches_fp32_activation_reference(hiplib, M, K, N):
+    # INV_FLAG_PRECISE: X = Xh + Xl, two MFMA passes over the resident W.
+    X, W, b = gen(14, M, K, N)
+    with q.Weight(W, b) as w:
+        y = q.linear(X, w, precise=True)
+        y1 = q.linear(X, w)
+    rows = sample_rows(M, 64)
+    e = oracle.normwise_err(y[rows], oracle_linear(X, W, b, rows=rows))
+    e1 = oracle.normwise_err(y1[rows], oracle_linear(X, W, b, rows=rows))
+    print(f"  vs fp32-X reference: precise {e:.3e}, default {e1:.3e}", flush=True)
+    assert e <= 3e-5 and e < e1
+
+
 def test_bf16_activations_in(hiplib):
     M, K, N = 96, 256, 192
     X, W, b = gen(8, M, K, N)
