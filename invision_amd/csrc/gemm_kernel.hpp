@@ -16,8 +16,8 @@
 //    past K are given an out-of-range offset and also read as zero.  K must be
 //    a multiple of 8 and rows 16-byte aligned (the host pads otherwise).
 //  * LDS holds each tile as rows of 64 bf16 (8 chunks of 16 B); chunk c of row
-//    r is stored in slot c ^ (r & 7), so the 8 rows read by 8 consecutive lanes
-//    of a ds_read_b128 fall in 8 different 16-byte bank groups.
+//    r is stored in slot c ^ key(r) (row_slot_key), so the rows read by
+//    consecutive lanes of a ds_read_b128 fall in different bank groups.
 //  * Two LDS stages: the loads of k-tile t+1 run while k-tile t is multiplied.
 //  * Workgroups are remapped so that the tiles resident on one XCD (hardware
 //    dispatches workgroup b to XCD b % 8) form a compact block of the output,
@@ -54,6 +54,7 @@ struct GemmParams {
     int ksplit, kt_per_split;  // K tiles per split
     float alpha, beta;
     int has_bias, vec_store;
+    int swizzle;  // LDS slot permutation: 0 -> row & 7, 1 -> (row + row/8) & 7
     float *partial;       // split-K workspace: [tiles][ksplit][threads][acc regs]
     unsigned *counters;   // split-K arrival counters, one per tile, zero between calls
 };
@@ -143,6 +144,15 @@ __device__ __forceinline__ void issue_tile_loads(__amdgpu_buffer_rsrc_t rsw, __a
                                                  0, 0, 0);
 }
 
+// Per-row key of the LDS slot permutation: chunk c of row r lives in slot
+// c ^ key(r).  key = r & 7 spreads any 8 consecutive rows over the 8 16-byte
+// slots of a 128-byte row (conflict-free when 8 lanes share 32 banks); key =
+// (r + r/8) & 7 also spreads the even and the odd rows of any aligned 16-row
+// window (conflict-free when 16 lanes share 64 banks).  Depends on r mod 16 only.
+__device__ __forceinline__ int row_slot_key(int r, int mode) {
+    return mode ? ((r + (r >> 3)) & 7) : (r & 7);
+}
+
 // Byte offset of k-tile `ktile` in a row, or an offset past every buffer
 // (reads as zeros) when the chunk is not valid.
 __device__ __forceinline__ uint32_t k_byte_offset(bool valid, int ktile) {
@@ -216,7 +226,7 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_bf16_kernel(const GemmParams p
     // Per-lane global offsets.  Position q = i*NTHREADS + tid of the tile maps to
     // row q/8 and LDS slot q%8; the chunk loaded there is slot ^ (row & 7).  With
     // NTHREADS a multiple of 64 the chunk is the same for every i.
-    const int ld_chunk = (tid & 7) ^ ((tid >> 3) & 7);
+    const int ld_chunk = (tid & 7) ^ row_slot_key(tid >> 3, p.swizzle);
     const int ld_row = tid >> 3;
     const uint32_t a_base = (uint32_t)(ld_row * p.ldw * 2 + ld_chunk * 16);
     const uint32_t b_base = (uint32_t)(ld_row * p.ldx * 2 + ld_chunk * 16);
@@ -238,7 +248,7 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_bf16_kernel(const GemmParams p
     // logical chunk 2*kk + (lane >> 5), stored at slot chunk ^ (row & 7).
     const int frow = lane & 31;
     const int fh = lane >> 5;
-    const int fsw = frow & 7;
+    const int fsw = row_slot_key(frow, p.swizzle);
     const int a_frag = (wn * C::WTN + frow) * (BK * 2);
     const int b_frag = C::A_BYTES + (wm * C::WTM + frow) * (BK * 2);
     int coff[4];

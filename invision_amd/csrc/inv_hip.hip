@@ -324,6 +324,7 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
     p.tiles_m = (int)((M + kCfgTM[tc.cfg] - 1) / kCfgTM[tc.cfg]);
     p.tiles_n = (int)((N + kCfgTN[tc.cfg] - 1) / kCfgTN[tc.cfg]);
     p.group_m = std::max(1, std::min(p.tiles_m, env_int("INV_HIP_GROUP_M", 4)));
+    p.swizzle = env_int("INV_HIP_SWZ", 1) ? 1 : 0;
     p.alpha = alpha;
     p.beta = beta;
     p.has_bias = bias != nullptr;

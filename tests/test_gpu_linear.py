@@ -23,8 +23,9 @@ from invision_amd.bf16 import as_bf16_bits, bf16_bits_to_f32, round_bf16
 
 pytestmark = pytest.mark.gpu
 
-TOL_REF = 2e-3    # vs the reference's fp32-activation linear (north star)
+TOL_REF = 2e-3    # vs the reference's fp32-activation linear (north star), K >= 1024
 TOL_TIGHT = 2e-5  # vs the oracle on the same bf16-rounded activations
+TOL_BF16_OUT = 2.0 ** -8 + TOL_TIGHT  # bf16 output: half an ulp is up to 2^-8 of the value
 
 
 def gen(seed, M, K, N, x_scale=1.0, w_scale=0.02, b_scale=0.01):
@@ -44,16 +45,22 @@ def oracle_linear(X, W, b, epi="none", rows=None):
 
 
 def check(y, X, W, b, epi="none", rows=None, tight=TOL_TIGHT, ref_tol=TOL_REF):
+    """Tight check against the oracle on bf16-rounded X, and the north-star
+    check against the fp32-X reference.  The latter is asserted for K >= 1024
+    (every workload shape has K >= 2560): rounding X to bf16 costs ~1.5e-3 at
+    K = 3072 but can exceed 2e-3 when a handful of products make up each
+    output; small-K shapes assert it on the INV_FLAG_PRECISE path instead."""
     ys = y if rows is None else y[rows]
     r_tight = oracle_linear(round_bf16(X), W, b, epi, rows)
     e_tight = oracle.normwise_err(ys, r_tight)
     r_ref = oracle_linear(X, W, b, epi, rows)
     e_ref = oracle.normwise_err(ys, r_ref)
     print(f"  normwise err: vs bf16-X oracle {e_tight:.3e} (tol {tight}), vs fp32-X reference {e_ref:.3e} "
-          f"(tol {ref_tol})", flush=True)
+          f"(tol {ref_tol} for K >= 1024)", flush=True)
     assert np.all(np.isfinite(ys))
     assert e_tight <= tight
-    assert e_ref <= ref_tol
+    if X.shape[1] >= 1024:
+        assert e_ref <= ref_tol
     return e_tight, e_ref
 
 
@@ -76,7 +83,10 @@ def test_linear_small_ragged_shapes(hiplib, M, K, N):
     X, W, b = gen(1000 + M + K + N, M, K, N)
     with q.Weight(W, b) as w:
         y = q.linear(X, w)
+        yp = q.linear(X, w, precise=True)
     check(y, X, W, b)
+    # The split-X path meets the reference bar at every K.
+    assert oracle.normwise_err(yp, oracle_linear(X, W, b)) <= TOL_REF
 
 
 @pytest.mark.parametrize("epi", ["none", "silu", "gelu"])
@@ -92,7 +102,7 @@ def test_linear_epilogues_and_output_types(hiplib, epi, out):
         yf = bf16_bits_to_f32(y)
         ref = oracle_linear(round_bf16(X), W, b, epi)
         # bf16 output: each element is within half a bf16 ulp of the fp32 result
-        assert oracle.normwise_err(yf, ref) <= 2.5e-3
+        assert oracle.normwise_err(yf, ref) <= TOL_BF16_OUT
         same = np.mean(y == oracle.f32_to_bf16_rne(ref))
         print(f"  bf16 outputs equal to RNE(oracle): {same:.5f}", flush=True)
         assert same > 0.999
@@ -228,7 +238,7 @@ def test_c3_mlp_up_silu_then_down(hiplib):
     Y_f = oracle.linear_bf16w(H_f, Wd, bd)
     e_ref = oracle.normwise_err(y[rows], Y_f)
     print(f"  H err {e_h:.3e}, Y err (bf16 chain) {e_y:.3e}, Y err vs fp32 reference chain {e_ref:.3e}", flush=True)
-    assert e_h <= 2.5e-3 and e_y <= 1e-4 and e_ref <= TOL_REF
+    assert e_h <= TOL_BF16_OUT and e_y <= 1e-4 and e_ref <= TOL_REF
 
 
 @pytest.mark.parametrize("which", ["gate_up", "down"])
