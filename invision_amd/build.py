@@ -21,42 +21,66 @@ LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["inv_hip.hip"]
-HEADERS = ["gemm_kernel.hpp", "convert_kernels.hpp"]
+BUILD_DIR = os.path.join(PKG_DIR, "_build")
+NUM_GEMM_CONFIGS = 8  # INV_GEMM_NUM_CONFIGS in csrc/gemm_configs.hpp
+
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-command-line-argument",
+    # No packed-FP32 instructions anywhere in device code.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
 
 
-def hipcc_cmd(out: str = LIB_PATH) -> list[str]:
-    return [
-        HIPCC,
-        f"--offload-arch={ARCH}",
-        "-O3",
-        "-std=c++17",
-        "-fPIC",
-        "-shared",
-        "-Wall",
-        "-Wno-unused-command-line-argument",
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        "-I", os.path.join(ROOT, "include"),
-        "-o", out,
-    ] + [os.path.join(CSRC, s) for s in SOURCES]
+def compile_jobs() -> list[tuple[list[str], str]]:
+    """(hipcc command, object path) for every translation unit."""
+    inc = ["-I", os.path.join(ROOT, "include")]
+    jobs = []
+    obj = os.path.join(BUILD_DIR, "inv_hip.o")
+    jobs.append(([HIPCC] + COMMON_FLAGS + inc + ["-c", os.path.join(CSRC, "inv_hip.hip"), "-o", obj], obj))
+    for cfg in range(NUM_GEMM_CONFIGS):
+        obj = os.path.join(BUILD_DIR, f"gemm_cfg{cfg}.o")
+        jobs.append(([HIPCC] + COMMON_FLAGS + inc + [f"-DINV_CFG_ID={cfg}", "-c",
+                                                     os.path.join(CSRC, "gemm_instance.hip"), "-o", obj], obj))
+    return jobs
 
 
-def build_lib(verbose: bool = True) -> str:
-    """Compile libinvision_hip.so in place (always recompiles)."""
-    tmp = LIB_PATH + ".tmp"
-    cmd = hipcc_cmd(tmp)
-    t0 = time.time()
+def _run(cmd: list[str]) -> tuple[int, str, list[str]]:
     res = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the packed-fp32 feature; that warning is harmless.
     noise = ("packed-fp32-ops", "not a recognized feature")
     err = "\n".join(l for l in res.stderr.splitlines() if not any(n in l for n in noise))
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{err}")
+    return res.returncode, err, cmd
+
+
+def build_lib(verbose: bool = True, jobs: int = 0) -> str:
+    """Compile libinvision_hip.so in place (always recompiles); translation units in parallel."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    t0 = time.time()
+    todo = compile_jobs()
+    workers = jobs or min(len(todo), max(1, min(16, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        results = list(ex.map(lambda j: _run(j[0]), todo))
+    for rc, err, cmd in results:
+        if rc != 0:
+            raise RuntimeError(f"hipcc failed ({rc}):\n{' '.join(cmd)}\n{err}")
+    tmp = LIB_PATH + ".tmp"
+    link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + [o for _, o in todo]
+    rc, err, cmd = _run(link)
+    if rc != 0:
+        raise RuntimeError(f"link failed ({rc}):\n{' '.join(cmd)}\n{err}")
     os.replace(tmp, LIB_PATH)
     if verbose:
-        print(f"[build] {LIB_NAME} in {time.time() - t0:.1f}s", flush=True)
-        if err.strip():
-            print(err, flush=True)
+        print(f"[build] {LIB_NAME} ({len(todo)} translation units) in {time.time() - t0:.1f}s", flush=True)
+        warn = "\n".join(e for rc, e, _ in results if e.strip())
+        if warn.strip():
+            print(warn, flush=True)
     return LIB_PATH
 
 

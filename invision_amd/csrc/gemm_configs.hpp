@@ -1,0 +1,31 @@
+// gemm_configs.hpp -- the instantiated GEMM tile configurations.
+//
+// INV_CFG_PARAMS_<id> = TN, TM, WN, WM, BK, NST: a TN x TM output tile (W rows
+// x X rows), WN x WM waves of 64 threads, BK-wide k-tiles, NST LDS stages.
+// Each configuration is compiled in its own translation unit
+// (gemm_instance.hip with -DINV_CFG_ID=<id>) and reached through
+// inv_gemm_launch_<id>.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#define INV_CFG_PARAMS_0 256, 256, 2, 4, 32, 4  /* 8 waves of 128x64, 4-stage ring (128 KiB) */
+#define INV_CFG_PARAMS_1 256, 256, 2, 4, 32, 5  /* same, 5 stages (160 KiB) */
+#define INV_CFG_PARAMS_2 256, 128, 2, 2, 64, 3  /* 4 waves of 128x64 */
+#define INV_CFG_PARAMS_3 128, 128, 2, 2, 64, 4  /* 4 waves of 64x64 */
+#define INV_CFG_PARAMS_4 128, 64, 2, 2, 64, 4   /* 4 waves of 64x32 */
+#define INV_CFG_PARAMS_5 128, 32, 4, 1, 64, 4   /* 4 waves of 32x32: W streaming for M <= 32 */
+#define INV_CFG_PARAMS_6 256, 256, 4, 2, 32, 4  /* 8 waves of 64x128 */
+#define INV_CFG_PARAMS_7 256, 256, 2, 2, 32, 4  /* 4 waves of 128x128 */
+
+#define INV_GEMM_CONFIG_IDS(X) X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7)
+#define INV_GEMM_NUM_CONFIGS 8
+
+namespace inv {
+struct GemmParams;
+}
+
+#define INV_DECLARE_LAUNCH(id) \
+    hipError_t inv_gemm_launch_##id(const inv::GemmParams &p, int epi, int out, bool split, hipStream_t s);
+INV_GEMM_CONFIG_IDS(INV_DECLARE_LAUNCH)
+#undef INV_DECLARE_LAUNCH

@@ -1,0 +1,53 @@
+// gemm_instance.hip -- one translation unit per tile configuration: compiled
+// with -DINV_CFG_ID=<id>, it instantiates gemm_nt_bf16_kernel for that
+// configuration's epilogues, output types and split-K modes and defines
+// inv_gemm_launch_<id>.
+#include "gemm_configs.hpp"
+#include "gemm_kernel.hpp"
+
+#ifndef INV_CFG_ID
+#error "compile with -DINV_CFG_ID=<configuration id>"
+#endif
+
+namespace {
+
+template <class C, int EPI, int OUT, bool SPLIT>
+void launch_one(const inv::GemmParams &p, dim3 grid, dim3 block, hipStream_t s) {
+    hipLaunchKernelGGL((inv::gemm_nt_bf16_kernel<C, EPI, OUT, SPLIT>), grid, block, 0, s, p);
+}
+
+template <class C, bool SPLIT>
+void launch_epi(const inv::GemmParams &p, int epi, int out, dim3 grid, dim3 block, hipStream_t s) {
+    const bool f32 = out == inv::OUT_F32;
+    if (epi == inv::EPI_SILU) {
+        if (f32) launch_one<C, inv::EPI_SILU, inv::OUT_F32, SPLIT>(p, grid, block, s);
+        else launch_one<C, inv::EPI_SILU, inv::OUT_BF16, SPLIT>(p, grid, block, s);
+    } else if (epi == inv::EPI_GELU) {
+        if (f32) launch_one<C, inv::EPI_GELU, inv::OUT_F32, SPLIT>(p, grid, block, s);
+        else launch_one<C, inv::EPI_GELU, inv::OUT_BF16, SPLIT>(p, grid, block, s);
+    } else {
+        if (f32) launch_one<C, inv::EPI_NONE, inv::OUT_F32, SPLIT>(p, grid, block, s);
+        else launch_one<C, inv::EPI_NONE, inv::OUT_BF16, SPLIT>(p, grid, block, s);
+    }
+}
+
+template <class C>
+hipError_t launch_cfg(const inv::GemmParams &p, int epi, int out, bool split, hipStream_t s) {
+    dim3 block(C::NTHREADS);
+    dim3 grid((unsigned)(p.tiles_m * p.tiles_n * (split ? p.ksplit : 1)));
+    if (split)
+        launch_epi<C, true>(p, epi, out, grid, block, s);
+    else
+        launch_epi<C, false>(p, epi, out, grid, block, s);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+#define INV_DEFINE_LAUNCH_(id, params)                                                                      \
+    hipError_t inv_gemm_launch_##id(const inv::GemmParams &p, int epi, int out, bool split, hipStream_t s) { \
+        return launch_cfg<inv::TileCfg<params>>(p, epi, out, split, s);                                     \
+    }
+#define INV_DEFINE_LAUNCH(id) INV_DEFINE_LAUNCH_(id, INV_CFG_PARAMS_##id)
+#define INV_EXPAND_DEFINE(id) INV_DEFINE_LAUNCH(id)
+INV_EXPAND_DEFINE(INV_CFG_ID)

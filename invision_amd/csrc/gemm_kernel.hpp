@@ -13,12 +13,18 @@
 //  * Global -> LDS uses buffer_load_dwordx4 ... lds (no VGPR staging).  Each
 //    workgroup addresses its W and X row panels through a buffer resource whose
 //    size ends at the last valid row, so rows past M or N read as zero; chunks
-//    past K are given an out-of-range offset and also read as zero.  K must be
-//    a multiple of 8 and rows 16-byte aligned (the host pads otherwise).
-//  * LDS holds each tile as rows of 64 bf16 (8 chunks of 16 B); chunk c of row
-//    r is stored in slot c ^ key(r) (row_slot_key), so the rows read by
-//    consecutive lanes of a ds_read_b128 fall in different bank groups.
-//  * Two LDS stages: the loads of k-tile t+1 run while k-tile t is multiplied.
+//    past K get an out-of-range offset and also read as zero.  K must be a
+//    multiple of 8 and rows 16-byte aligned (the host pads otherwise).
+//  * LDS holds each k-tile as rows of BK bf16 (BK/8 chunks of 16 B); chunk c of
+//    row r sits in slot c ^ key(r), chosen so that the 16 rows read by any 16
+//    consecutive lanes of a ds_read_b128 cover all 64 banks (gfx950 serves a
+//    b128 read 16 lanes at a time).
+//  * An NST-stage LDS ring: k-tile t+NST-1 is copied while t is multiplied, so
+//    a copy has NST-2 k-tiles of MFMA time to land.  One barrier per k-tile.
+//  * Fragments are double-buffered in registers: the reads for the next
+//    16-wide substep (including the first substep of the next k-tile) are
+//    issued under the MFMAs of the current one, so the matrix cores do not wait
+//    for LDS after the barrier.
 //  * Workgroups are remapped so that the tiles resident on one XCD (hardware
 //    dispatches workgroup b to XCD b % 8) form a compact block of the output,
 //    which keeps the shared X and W panels in that XCD's L2.
@@ -30,6 +36,9 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
+#include <utility>
 
 namespace inv {
 
@@ -48,13 +57,12 @@ struct GemmParams {
     const float *bias;  // [N] or null
     const float *Cin;   // [M x ldc] f32, read when beta != 0
     int64_t ldw, ldx, ldy, ldc;
-    int M, N, K;  // K: the reduction length of X (and of W unless it wraps)
-    int w_seg_tiles, Kw;  // W wraps every w_seg_tiles k-tiles (0: no wrap); Kw: valid K of W
+    int M, N, K;          // K: the reduction length of X (and of W unless it wraps)
+    int w_seg_k, Kw;      // W wraps every w_seg_k columns (a multiple of 64; 0: no wrap); Kw: valid K of W
     int tiles_m, tiles_n, group_m;
     int ksplit, kt_per_split;  // K tiles per split
     float alpha, beta;
     int has_bias, vec_store;
-    int swizzle;  // LDS slot permutation: 0 -> row & 7, 1 -> (row + row/8) & 7
     float *partial;       // split-K workspace: [tiles][ksplit][threads][acc regs]
     unsigned *counters;   // split-K arrival counters, one per tile, zero between calls
 };
@@ -101,32 +109,64 @@ __device__ __forceinline__ void tile_coords(int bid, int ntiles, int tiles_m, in
     tn = r / gm;
 }
 
-template <int TN, int TM, int WN, int WM>
+// Tile configuration: TN x TM output tile (W rows x X rows), WN x WM waves,
+// BK-wide k-tiles, NST LDS stages.
+template <int TN_, int TM_, int WN_, int WM_, int BK_, int NST_>
 struct TileCfg {
-    static constexpr int BK = 64;
+    static constexpr int TN = TN_, TM = TM_, WN = WN_, WM = WM_, BK = BK_, NST = NST_;
     static constexpr int NWAVES = WN * WM;
     static constexpr int NTHREADS = NWAVES * 64;
     static constexpr int WTN = TN / WN;
     static constexpr int WTM = TM / WM;
     static constexpr int FN = WTN / 32;
     static constexpr int FM = WTM / 32;
-    static constexpr int A_BYTES = TN * BK * 2;
-    static constexpr int B_BYTES = TM * BK * 2;
+    static constexpr int SLOTS = BK / 8;      // 16-byte chunks per LDS row
+    static constexpr int ROWB = BK * 2;       // bytes per LDS row
+    static constexpr int KSUB = BK / 16;      // MFMA k-substeps per k-tile
+    static constexpr int A_BYTES = TN * ROWB;
+    static constexpr int B_BYTES = TM * ROWB;
     static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
-    static constexpr int LDS_BYTES = 2 * STAGE_BYTES;
-    static constexpr int A_LOADS = TN * 8 / NTHREADS;
-    static constexpr int B_LOADS = TM * 8 / NTHREADS;
+    static constexpr int LDS_BYTES = NST * STAGE_BYTES;
+    static constexpr int A_LOADS = TN * SLOTS / NTHREADS;
+    static constexpr int B_LOADS = TM * SLOTS / NTHREADS;
+    static constexpr int LOADS = A_LOADS + B_LOADS;  // buffer_load_dwordx4 per thread per k-tile
     static constexpr int ACC_REGS = FN * FM * 16;
+    static_assert(BK == 32 || BK == 64, "BK is 32 or 64");
+    static_assert(NST >= 3, "the ring needs the current, the next and one loading stage");
     static_assert(TN % (WN * 32) == 0 && TM % (WM * 32) == 0, "wave tile must be a multiple of 32");
-    static_assert((TN * 8) % NTHREADS == 0 && (TM * 8) % NTHREADS == 0, "loads must divide evenly");
+    static_assert((TN * SLOTS) % NTHREADS == 0 && (TM * SLOTS) % NTHREADS == 0, "copies must divide evenly");
+    static_assert((NTHREADS / SLOTS) % 16 == 0, "copy rows must advance in multiples of 16");
     static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
+    static_assert(KSUB % 2 == 0, "register double-buffering alternates over an even substep count");
 };
 
 #if defined(__HIP_DEVICE_COMPILE__)
+
+// LDS slot key of row r (depends on r mod 16 only, so the copy side and the
+// fragment side can both compute it from their low row bits).
+//  8 slots (128-byte rows): rows r and r+8 of an aligned 16-row window differ
+//    by one slot, and the 8 rows of each parity get 8 different slots;
+//  4 slots (64-byte rows): rows r, r+4, r+8, r+12 get 4 different slots.
+// Either way the 16 rows read by 16 consecutive lanes land on 16 different
+// 16-byte bank groups of the 256-byte bank window.
+template <int SLOTS>
+__device__ __forceinline__ int slot_key(int r) {
+    if constexpr (SLOTS == 8)
+        return (r + ((r >> 3) & 1)) & 7;
+    else
+        return (r >> 2) & 3;
+}
+
+// Byte offset of k-tile `ktile` within a row, or an offset past every buffer
+// (reads as zeros) when the chunk is not valid.
+template <int BK>
+__device__ __forceinline__ uint32_t k_byte_offset(bool valid, int ktile) {
+    return valid ? (uint32_t)(ktile * BK) * 2 : 0x80000000u;
+}
+
 // Global -> LDS copies of one k-tile: A_LOADS + B_LOADS buffer_load_dwordx4
 // ... lds per lane.  Lane l of wave w writes 16 bytes at LDS position
-// (i * NTHREADS + w * 64 + l) * 16 of the stage; `kadd` is the k offset in
-// bytes, or 0x80000000 to make every lane read out of range (zeros).
+// (i * NTHREADS + w * 64 + l) * 16 of the stage.
 template <class C>
 __device__ __forceinline__ void issue_tile_loads(__amdgpu_buffer_rsrc_t rsw, __amdgpu_buffer_rsrc_t rsx,
                                                  lds_char_t *stage, int wave, uint32_t a_base, uint32_t a_step,
@@ -144,29 +184,14 @@ __device__ __forceinline__ void issue_tile_loads(__amdgpu_buffer_rsrc_t rsw, __a
                                                  0, 0, 0);
 }
 
-// Per-row key of the LDS slot permutation: chunk c of row r lives in slot
-// c ^ key(r).  key = r & 7 spreads any 8 consecutive rows over the 8 16-byte
-// slots of a 128-byte row (conflict-free when 8 lanes share 32 banks); key =
-// (r + r/8) & 7 also spreads the even and the odd rows of any aligned 16-row
-// window (conflict-free when 16 lanes share 64 banks).  Depends on r mod 16 only.
-__device__ __forceinline__ int row_slot_key(int r, int mode) {
-    return mode ? ((r + (r >> 3)) & 7) : (r & 7);
-}
-
-// Byte offset of k-tile `ktile` in a row, or an offset past every buffer
-// (reads as zeros) when the chunk is not valid.
-__device__ __forceinline__ uint32_t k_byte_offset(bool valid, int ktile) {
-    return valid ? (uint32_t)(ktile * 64) * 2 : 0x80000000u;
-}
-
-// MFMA fragments of one 16-wide k substep: FN rows blocks of W, FM of X.
+// MFMA fragments of one 16-wide k substep: FN row blocks of W, FM of X.
 template <class C>
-__device__ __forceinline__ void load_frags(const lds_char_t *sbase, int a_frag, int b_frag, int coff,
+__device__ __forceinline__ void load_frags(const lds_char_t *stage, int a_frag, int b_frag, int coff,
                                            bf16x8_t (&fa)[C::FN], bf16x8_t (&fb)[C::FM]) {
 #pragma unroll
-    for (int i = 0; i < C::FN; ++i) fa[i] = *(const bf16x8_t *)(sbase + a_frag + i * 32 * C::BK * 2 + coff);
+    for (int i = 0; i < C::FN; ++i) fa[i] = *(const bf16x8_t *)(stage + a_frag + i * 32 * C::ROWB + coff);
 #pragma unroll
-    for (int j = 0; j < C::FM; ++j) fb[j] = *(const bf16x8_t *)(sbase + b_frag + j * 32 * C::BK * 2 + coff);
+    for (int j = 0; j < C::FM; ++j) fb[j] = *(const bf16x8_t *)(stage + b_frag + j * 32 * C::ROWB + coff);
 }
 
 template <class C>
@@ -179,22 +204,53 @@ __device__ __forceinline__ void mfma_block(f32x16_t (&acc)[C::FN][C::FM], const 
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
 }
 
+// Compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N-1.
+template <class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// One global->LDS copy (the idx-th of the LOADS copies of a k-tile).
+template <class C, int IDX>
+__device__ __forceinline__ void issue_copy(__amdgpu_buffer_rsrc_t rsw, __amdgpu_buffer_rsrc_t rsx, lds_char_t *dst,
+                                           uint32_t a_base, uint32_t a_step, uint32_t b_base, uint32_t b_step,
+                                           uint32_t kadd_a, uint32_t kadd_b) {
+    if constexpr (IDX < C::A_LOADS)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, dst + IDX * C::NTHREADS * 16, 16, a_base + IDX * a_step + kadd_a,
+                                                 0, 0, 0);
+    else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsx, dst + C::A_BYTES + (IDX - C::A_LOADS) * C::NTHREADS * 16, 16,
+                                                 b_base + (IDX - C::A_LOADS) * b_step + kadd_b, 0, 0, 0);
+}
+
+// Position (in MFMA steps of a k-tile) after which copy i is issued: the
+// LOADS copies are spread evenly, so they never queue up in the texture unit
+// ahead of the MFMAs of the same wave.
+template <class C>
+constexpr int copy_step(int i) {
+    constexpr int T = C::KSUB * C::FN * C::FM;
+    return ((2 * i + 1) * T) / (2 * C::LOADS);
+}
 #endif  // __HIP_DEVICE_COMPILE__
 
 // The body is compiled only in the device pass: the host pass needs just the
 // launch stub, and buffer-resource types do not exist for the host target.
-template <int TN, int TM, int WN, int WM, int EPI, int OUT, bool SPLIT>
-__global__ void __launch_bounds__(256, 1) gemm_nt_bf16_kernel(const GemmParams p) {
+template <class C, int EPI, int OUT, bool SPLIT>
+__global__ void __launch_bounds__(C::NTHREADS, 1) gemm_nt_bf16_kernel(const GemmParams p) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    using C = TileCfg<TN, TM, WN, WM>;
     constexpr int BK = C::BK;
+    constexpr int NST = C::NST;
     __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wn = wave / WM;
-    const int wm = wave % WM;
+    const int wn = wave / C::WM;
+    const int wm = wave % C::WM;
 
     const int ntiles = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
@@ -205,8 +261,8 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_bf16_kernel(const GemmParams p
     }
     int tm, tn;
     tile_coords(bid, ntiles, p.tiles_m, p.group_m, tm, tn);
-    const int m0 = tm * TM;
-    const int n0 = tn * TN;
+    const int m0 = tm * C::TM;
+    const int n0 = tn * C::TN;
 
     const int KT = (p.K + BK - 1) / BK;
     int kt_begin = 0, kt_end = KT;
@@ -216,21 +272,22 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_bf16_kernel(const GemmParams p
     }
 
     // Buffer resources covering exactly the valid rows of this tile's panels.
-    const int rows_w = min(TN, p.N - n0);
-    const int rows_x = min(TM, p.M - m0);
+    const int rows_w = min(C::TN, p.N - n0);
+    const int rows_x = min(C::TM, p.M - m0);
     const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(p.W + (int64_t)n0 * p.ldw), 0, (int)((int64_t)rows_w * p.ldw * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(p.X + (int64_t)m0 * p.ldx), 0, (int)((int64_t)rows_x * p.ldx * 2), 0x00020000);
 
-    // Per-lane global offsets.  Position q = i*NTHREADS + tid of the tile maps to
-    // row q/8 and LDS slot q%8; the chunk loaded there is slot ^ (row & 7).  With
-    // NTHREADS a multiple of 64 the chunk is the same for every i.
-    const int ld_chunk = (tid & 7) ^ row_slot_key(tid >> 3, p.swizzle);
-    const int ld_row = tid >> 3;
+    // Copy-side lane constants: position q = i*NTHREADS + tid of a tile is row
+    // q / SLOTS, slot q % SLOTS, and holds chunk slot ^ key(row); the row
+    // advances by NTHREADS/SLOTS (a multiple of 16) per i, so the chunk is the
+    // same for every i.
+    const int ld_row = tid / C::SLOTS;
+    const int ld_chunk = (tid % C::SLOTS) ^ slot_key<C::SLOTS>(ld_row);
     const uint32_t a_base = (uint32_t)(ld_row * p.ldw * 2 + ld_chunk * 16);
     const uint32_t b_base = (uint32_t)(ld_row * p.ldx * 2 + ld_chunk * 16);
-    constexpr int ROWS_PER_LOAD = C::NTHREADS / 8;
+    constexpr int ROWS_PER_LOAD = C::NTHREADS / C::SLOTS;
     const uint32_t a_step = (uint32_t)(ROWS_PER_LOAD * p.ldw * 2);
     const uint32_t b_step = (uint32_t)(ROWS_PER_LOAD * p.ldx * 2);
 
@@ -244,69 +301,101 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_bf16_kernel(const GemmParams p
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // Fragment addressing: lane reads row (lane & 31) of each 32-row block,
-    // logical chunk 2*kk + (lane >> 5), stored at slot chunk ^ (row & 7).
+    // Fragment-side lane constants: lane reads row (lane & 31) of each 32-row
+    // block, logical chunk 2*kk + (lane >> 5), stored at slot chunk ^ key(row).
     const int frow = lane & 31;
     const int fh = lane >> 5;
-    const int fsw = row_slot_key(frow, p.swizzle);
-    const int a_frag = (wn * C::WTN + frow) * (BK * 2);
-    const int b_frag = C::A_BYTES + (wm * C::WTM + frow) * (BK * 2);
-    int coff[4];
+    const int fkey = slot_key<C::SLOTS>(frow);
+    const int a_frag = (wn * C::WTN + frow) * C::ROWB;
+    const int b_frag = C::A_BYTES + (wm * C::WTM + frow) * C::ROWB;
+    int coff[C::KSUB];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) coff[kk] = (((2 * kk + fh) ^ fsw) * 16);
+    for (int kk = 0; kk < C::KSUB; ++kk) coff[kk] = ((2 * kk + fh) ^ fkey) * 16;
 
-    // A k-tile at or past kt_end gets out-of-range offsets for every lane, so
-    // its copy writes zeros and reads nothing; the prefetch of the next tile
-    // is then unconditional and the loop body stays one basic block.
+    // K-tile cursors.  The copy of a k-tile at or past kt_end gets out-of-range
+    // offsets for every lane: it writes zeros and reads nothing, which keeps the
+    // ring uniform (every iteration issues exactly one k-tile of copies).
     // W may wrap along K (split-precision passes reuse the resident weight):
-    // its k-tile index runs modulo w_seg_tiles, tracked incrementally.
-    int ktw = p.w_seg_tiles ? kt_begin % p.w_seg_tiles : kt_begin;
-    {
-        const bool in = kt_begin < kt_end;
-        issue_tile_loads<C>(rsw, rsx, lds, wave, a_base, a_step, b_base, b_step,
-                            k_byte_offset(in && ktw * BK + ld_chunk * 8 < p.Kw, ktw),
-                            k_byte_offset(in && kt_begin * BK + ld_chunk * 8 < p.K, kt_begin));
-    }
+    // its k-tile index runs modulo the segment length, tracked incrementally.
+    const int wseg = p.w_seg_k / BK;  // W k-tiles per wrap segment (0: no wrap)
+    int load_kt = kt_begin;
+    int load_ktw = wseg ? kt_begin % wseg : kt_begin;
+    auto issue_next = [&](int stage) {
+        const bool in = load_kt < kt_end;
+        issue_tile_loads<C>(rsw, rsx, lds + stage * C::STAGE_BYTES, wave, a_base, a_step, b_base, b_step,
+                            k_byte_offset<BK>(in && load_ktw * BK + ld_chunk * 8 < p.Kw, load_ktw),
+                            k_byte_offset<BK>(in && load_kt * BK + ld_chunk * 8 < p.K, load_kt));
+        ++load_kt;
+        load_ktw = (wseg && load_ktw + 1 == wseg) ? 0 : load_ktw + 1;
+    };
 
+    // Prologue: k-tiles 0 .. NST-2 in flight; wait for the first, read its
+    // first substep.
+#pragma unroll
+    for (int s = 0; s < NST - 1; ++s) issue_next(s);
+    wait_vmcnt<(NST - 2) * C::LOADS>();
+    __syncthreads();
+
+    bf16x8_t fa0[C::FN], fb0[C::FM], fa1[C::FN], fb1[C::FM];
+    load_frags<C>(lds, a_frag, b_frag, coff[0], fa0, fb0);
+
+    int stage = 0;
     for (int kt = kt_begin; kt < kt_end; ++kt) {
-        const int stage = (kt - kt_begin) & 1;
-        wait_vmcnt<0>();
+        // k-tiles t+1 .. t+NST-2 are in flight; t+1 must have landed, everywhere.
+        wait_vmcnt<(NST - 3) * C::LOADS>();
         __syncthreads();
-        {
-            const int kn = kt + 1;
-            ktw = (p.w_seg_tiles && ktw + 1 == p.w_seg_tiles) ? 0 : ktw + 1;
-            const bool in = kn < kt_end;
-            issue_tile_loads<C>(rsw, rsx, lds + (stage ^ 1) * C::STAGE_BYTES, wave, a_base, a_step, b_base, b_step,
-                                k_byte_offset(in && ktw * BK + ld_chunk * 8 < p.Kw, ktw),
-                                k_byte_offset(in && kn * BK + ld_chunk * 8 < p.K, kn));
-        }
+        // The stage of t-1 is free now (every wave passed the barrier after
+        // finishing t-1): this k-tile's copies fill it with k-tile t+NST-1.
+        const int load_stage = (stage == 0) ? NST - 1 : stage - 1;
+        lds_char_t *cdst = lds + load_stage * C::STAGE_BYTES + wave * 1024;
+        const bool in = load_kt < kt_end;
+        const uint32_t kadd_a = k_byte_offset<BK>(in && load_ktw * BK + ld_chunk * 8 < p.Kw, load_ktw);
+        const uint32_t kadd_b = k_byte_offset<BK>(in && load_kt * BK + ld_chunk * 8 < p.K, load_kt);
+        ++load_kt;
+        load_ktw = (wseg && load_ktw + 1 == wseg) ? 0 : load_ktw + 1;
+        const lds_char_t *cur = lds + stage * C::STAGE_BYTES;
+        const int next_stage = (stage + 1 == NST) ? 0 : stage + 1;
+        const lds_char_t *nxt = lds + next_stage * C::STAGE_BYTES;
 
-        const lds_char_t *sbase = lds + stage * C::STAGE_BYTES;
-        bf16x8_t fa0[C::FN], fb0[C::FM], fa1[C::FN], fb1[C::FM], fa2[C::FN], fb2[C::FM], fa3[C::FN], fb3[C::FM];
-        load_frags<C>(sbase, a_frag, b_frag, coff[0], fa0, fb0);
-        load_frags<C>(sbase, a_frag, b_frag, coff[1], fa1, fb1);
-        mfma_block<C>(acc, fa0, fb0);
-        load_frags<C>(sbase, a_frag, b_frag, coff[2], fa2, fb2);
-        mfma_block<C>(acc, fa1, fb1);
-        load_frags<C>(sbase, a_frag, b_frag, coff[3], fa3, fb3);
-        mfma_block<C>(acc, fa2, fb2);
-        mfma_block<C>(acc, fa3, fb3);
-        // Schedule: the fragments of substeps 0 and 1 first, then each group of
-        // MFMAs interleaved with the fragment reads two substeps ahead.
-        constexpr int NF = C::FN + C::FM;  // ds_reads per substep
-        constexpr int NM = C::FN * C::FM;  // MFMAs per substep
-        __builtin_amdgcn_sched_group_barrier(0x100, 2 * NF, 0);
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-#pragma unroll
-            for (int q = 0; q < NF; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x008, NM / NF > 0 ? NM / NF : 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            }
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 2 * NM, 0);
+        // The k-tile as a fixed instruction order: step q of substep ks is one
+        // MFMA of substep ks, one fragment read of substep ks+1 (or of substep 0
+        // of the next k-tile), and a copy if one is due; sched_barrier pins it.
+        static_for<C::KSUB>([&](auto ksc) {
+            constexpr int ks = decltype(ksc)::value;
+            bf16x8_t(&ca)[C::FN] = (ks % 2 == 0) ? fa0 : fa1;
+            bf16x8_t(&cb)[C::FM] = (ks % 2 == 0) ? fb0 : fb1;
+            bf16x8_t(&na)[C::FN] = (ks % 2 == 0) ? fa1 : fa0;
+            bf16x8_t(&nb)[C::FM] = (ks % 2 == 0) ? fb1 : fb0;
+            const lds_char_t *rs = (ks + 1 < C::KSUB) ? cur : nxt;
+            const int rc = coff[(ks + 1) % C::KSUB];
+            static_for<C::FN * C::FM>([&](auto qc) {
+                constexpr int q = decltype(qc)::value;
+                constexpr int i = q / C::FM, j = q % C::FM;
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ca[i], cb[j], acc[i][j], 0, 0, 0);
+                if constexpr (q < C::FN)
+                    na[q] = *(const bf16x8_t *)(rs + a_frag + q * 32 * C::ROWB + rc);
+                else if constexpr (q < C::FN + C::FM)
+                    nb[q - C::FN] = *(const bf16x8_t *)(rs + b_frag + (q - C::FN) * 32 * C::ROWB + rc);
+                // every copy whose slot is this step (several when LOADS exceeds the MFMA count)
+                static_for<C::LOADS>([&](auto cc) {
+                    constexpr int ci = decltype(cc)::value;
+                    if constexpr (copy_step<C>(ci) == ks * C::FN * C::FM + q)
+                        issue_copy<C, ci>(rsw, rsx, cdst, a_base, a_step, b_base, b_step, kadd_a, kadd_b);
+                });
+                __builtin_amdgcn_sched_barrier(0);
+            });
+            // reads left over when a substep has more fragments than MFMAs
+            static_for<(C::FN + C::FM > C::FN * C::FM) ? C::FN + C::FM - C::FN * C::FM : 0>([&](auto rc2) {
+                constexpr int q = C::FN * C::FM + decltype(rc2)::value;
+                if constexpr (q < C::FN)
+                    na[q] = *(const bf16x8_t *)(rs + a_frag + q * 32 * C::ROWB + rc);
+                else
+                    nb[q - C::FN] = *(const bf16x8_t *)(rs + b_frag + (q - C::FN) * 32 * C::ROWB + rc);
+            });
+        });
+        stage = next_stage;
     }
-    // The final (all out-of-range) prefetch still writes LDS; let it land
+    // The copies of the k-tiles past the end still write LDS; let them land
     // before the workgroup can retire.
     wait_vmcnt<0>();
 
@@ -322,15 +411,17 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_bf16_kernel(const GemmParams p
                     f32x4_t v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
                     *(f32x4_t *)(mine + ((((i * C::FM + j) * 4 + g) * C::NTHREADS + tid) * 4)) = v;
                 }
-        __shared__ unsigned s_last;
+        // The flag lives in the (now idle) ring: the barrier below completes
+        // every wave's LDS reads before thread 0 writes it.
+        volatile unsigned *s_last = (volatile unsigned *)smem;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         __syncthreads();
         if (tid == 0) {
             unsigned prev = __hip_atomic_fetch_add(&p.counters[bid], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            s_last = (prev == (unsigned)(p.ksplit - 1)) ? 1u : 0u;
+            *s_last = (prev == (unsigned)(p.ksplit - 1)) ? 1u : 0u;
         }
         __syncthreads();
-        if (!s_last) return;
+        if (!*s_last) return;
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         // Sum the partials in split order so the result does not depend on
         // which split arrived last.
@@ -371,7 +462,7 @@ __global__ void __launch_bounds__(256, 1) gemm_nt_bf16_kernel(const GemmParams p
             float bv[4] = {0.f, 0.f, 0.f, 0.f};
             if (p.has_bias) {
                 if (n + 3 < p.N) {
-                    f32x4_t t = *(const f32x4_t *)(p.bias + n);  // bias is 16-byte aligned, N % 4 == 0 here
+                    f32x4_t t = *(const f32x4_t *)(p.bias + n);  // bias is 16-byte aligned, n % 4 == 0
                     bv[0] = t[0]; bv[1] = t[1]; bv[2] = t[2]; bv[3] = t[3];
                 } else {
 #pragma unroll

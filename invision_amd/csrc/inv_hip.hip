@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "convert_kernels.hpp"
+#include "gemm_configs.hpp"
 #include "gemm_kernel.hpp"
 
 namespace {
@@ -200,54 +201,22 @@ int d2h_rows(void *host, const void *dev, int64_t rows, size_t width, size_t pit
 // ---------------------------------------------------------------------------
 
 struct TileChoice {
-    int cfg;     // index into the instantiated tile shapes
+    int cfg;     // index into the instantiated tile configurations
     int ksplit;  // 1 = no split
 };
 
-// Instantiated tile shapes (TN = W rows, TM = X rows, wave grid WN x WM).
-// 0: 256x256 2x2   1: 256x128 2x2   2: 128x128 2x2   3: 128x64 2x2   4: 128x32 4x1
-constexpr int kNumCfg = 5;
-constexpr int kCfgTN[kNumCfg] = {256, 256, 128, 128, 128};
-constexpr int kCfgTM[kNumCfg] = {256, 128, 128, 64, 32};
-
-template <int TN, int TM, int WN, int WM>
-int launch_tile(const inv::GemmParams &p, int epi, int out, bool split) {
-    dim3 block(WN * WM * 64);
-    dim3 grid((unsigned)(p.tiles_m * p.tiles_n * (split ? p.ksplit : 1)));
-#define INV_LAUNCH(E, O, S) \
-    hipLaunchKernelGGL((inv::gemm_nt_bf16_kernel<TN, TM, WN, WM, E, O, S>), grid, block, 0, g.stream, p)
-#define INV_LAUNCH_EO(S)                                                        \
-    do {                                                                        \
-        if (out == inv::OUT_F32) {                                              \
-            if (epi == inv::EPI_NONE) INV_LAUNCH(inv::EPI_NONE, inv::OUT_F32, S); \
-            else if (epi == inv::EPI_SILU) INV_LAUNCH(inv::EPI_SILU, inv::OUT_F32, S); \
-            else INV_LAUNCH(inv::EPI_GELU, inv::OUT_F32, S);                    \
-        } else {                                                                \
-            if (epi == inv::EPI_NONE) INV_LAUNCH(inv::EPI_NONE, inv::OUT_BF16, S); \
-            else if (epi == inv::EPI_SILU) INV_LAUNCH(inv::EPI_SILU, inv::OUT_BF16, S); \
-            else INV_LAUNCH(inv::EPI_GELU, inv::OUT_BF16, S);                   \
-        }                                                                       \
-    } while (0)
-    if (split)
-        INV_LAUNCH_EO(true);
-    else
-        INV_LAUNCH_EO(false);
-#undef INV_LAUNCH_EO
-#undef INV_LAUNCH
-    HIPCHK(hipGetLastError());
-    return INV_OK;
-}
-
-int launch_cfg(int cfg, const inv::GemmParams &p, int epi, int out, bool split) {
-    switch (cfg) {
-    case 0: return launch_tile<256, 256, 2, 2>(p, epi, out, split);
-    case 1: return launch_tile<256, 128, 2, 2>(p, epi, out, split);
-    case 2: return launch_tile<128, 128, 2, 2>(p, epi, out, split);
-    case 3: return launch_tile<128, 64, 2, 2>(p, epi, out, split);
-    case 4: return launch_tile<128, 32, 4, 1>(p, epi, out, split);
-    default: return fail(INV_ERR_ARG, "bad tile config %d", cfg);
-    }
-}
+// Instantiated tile configurations (gemm_configs.hpp).
+struct CfgMeta {
+    int tn, tm, threads, acc_regs, bk;
+    hipError_t (*launch)(const inv::GemmParams &, int, int, bool, hipStream_t);
+};
+#define INV_META(id)                                                                                 \
+    {inv::TileCfg<INV_CFG_PARAMS_##id>::TN, inv::TileCfg<INV_CFG_PARAMS_##id>::TM,                  \
+     inv::TileCfg<INV_CFG_PARAMS_##id>::NTHREADS, inv::TileCfg<INV_CFG_PARAMS_##id>::ACC_REGS,      \
+     inv::TileCfg<INV_CFG_PARAMS_##id>::BK, &inv_gemm_launch_##id},
+const CfgMeta kCfg[INV_GEMM_NUM_CONFIGS] = {INV_GEMM_CONFIG_IDS(INV_META)};
+#undef INV_META
+constexpr int kNumCfg = INV_GEMM_NUM_CONFIGS;
 
 int env_int(const char *name, int dflt) {
     const char *v = getenv(name);
@@ -261,32 +230,36 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
     TileChoice c{0, 1};
     const int cus = g.cu_count > 0 ? g.cu_count : 256;
     const int64_t KT = (K + 63) / 64;
-    if (M <= 32) c.cfg = 4;
-    else if (M <= 64) c.cfg = 3;
-    else {
-        // Among the three larger tiles, the one that wastes least of the last
-        // wave of workgroups, weighting smaller tiles by their lower MFMA
-        // efficiency per byte of LDS traffic.
-        const double eff[3] = {1.0, 0.9, 0.8};
+    if (M <= 32) {
+        c.cfg = 5;
+    } else if (M <= 64) {
+        c.cfg = 4;
+    } else {
+        // Among the larger tiles, the one that wastes least of the last wave
+        // of workgroups, weighting smaller tiles by their lower MFMA
+        // efficiency (more LDS traffic per MFMA).
+        const int cand[3] = {0, 2, 3};
+        const double eff[3] = {1.0, 0.85, 0.7};
         double best = -1.0;
-        for (int cfg = 0; cfg < 3; ++cfg) {
-            int64_t tiles = ((M + kCfgTM[cfg] - 1) / kCfgTM[cfg]) * ((N + kCfgTN[cfg] - 1) / kCfgTN[cfg]);
-            double useful = (double)M * N;
+        for (int q = 0; q < 3; ++q) {
+            const CfgMeta &m = kCfg[cand[q]];
+            int64_t tiles = ((M + m.tm - 1) / m.tm) * ((N + m.tn - 1) / m.tn);
             double waves = (double)((tiles + cus - 1) / cus);
-            double score = useful / (waves * cus * kCfgTM[cfg] * kCfgTN[cfg]) * eff[cfg];
+            double score = (double)M * N / (waves * cus * m.tm * m.tn) * eff[q];
             if (score > best) {
                 best = score;
-                c.cfg = cfg;
+                c.cfg = cand[q];
             }
         }
     }
-    const int64_t tiles = ((M + kCfgTM[c.cfg] - 1) / kCfgTM[c.cfg]) * ((N + kCfgTN[c.cfg] - 1) / kCfgTN[c.cfg]);
-    const int64_t target = (c.cfg >= 3) ? 2 * cus : cus;
+    const CfgMeta &m = kCfg[c.cfg];
+    const int64_t tiles = ((M + m.tm - 1) / m.tm) * ((N + m.tn - 1) / m.tn);
+    const int64_t target = (m.threads == 256 && m.tn * m.tm <= 128 * 128) ? 2 * cus : cus;
     if (tiles < target && KT >= 16) {
-        int64_t s = (target + tiles - 1) / tiles;
-        s = std::min<int64_t>(s, KT / 8);
-        s = std::min<int64_t>(s, 16);
-        c.ksplit = (int)std::max<int64_t>(s, 1);
+        int64_t sp = (target + tiles - 1) / tiles;
+        sp = std::min<int64_t>(sp, KT / 8);
+        sp = std::min<int64_t>(sp, 16);
+        c.ksplit = (int)std::max<int64_t>(sp, 1);
     }
     int ov = env_int("INV_HIP_TILE_CFG", -1);
     if (ov >= 0 && ov < kNumCfg) c.cfg = ov;
@@ -298,7 +271,7 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
 // W [N x ldw], X [M x ldx] bf16 device; K a multiple of 8 (zero padded).
 int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, void *Y, int64_t ldy, int out,
              const float *bias, const float *Cin, int64_t ldc, float alpha, float beta, int64_t M, int64_t N,
-             int64_t K, int epi, int w_seg_tiles = 0, int64_t Kw = -1) {
+             int64_t K, int epi, int64_t w_seg_k = 0, int64_t Kw = -1) {
     if (M == 0 || N == 0) return INV_OK;
     if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return fail(INV_ERR_ARG, "dimension too large");
     if (K % 8 || ldw % 8 || ldx % 8 || !aligned(W, 16) || !aligned(X, 16))
@@ -319,19 +292,19 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
     p.M = (int)M;
     p.N = (int)N;
     p.K = (int)K;
-    p.w_seg_tiles = w_seg_tiles;
+    p.w_seg_k = (int)w_seg_k;
     p.Kw = (int)(Kw < 0 ? K : Kw);
-    p.tiles_m = (int)((M + kCfgTM[tc.cfg] - 1) / kCfgTM[tc.cfg]);
-    p.tiles_n = (int)((N + kCfgTN[tc.cfg] - 1) / kCfgTN[tc.cfg]);
-    p.group_m = std::max(1, std::min(p.tiles_m, env_int("INV_HIP_GROUP_M", 4)));
-    p.swizzle = env_int("INV_HIP_SWZ", 1) ? 1 : 0;
+    const CfgMeta &cm = kCfg[tc.cfg];
+    p.tiles_m = (int)((M + cm.tm - 1) / cm.tm);
+    p.tiles_n = (int)((N + cm.tn - 1) / cm.tn);
+    p.group_m = std::max(1, std::min(p.tiles_m, env_int("INV_HIP_GROUP_M", 8)));
     p.alpha = alpha;
     p.beta = beta;
     p.has_bias = bias != nullptr;
     const size_t esz = (out == inv::OUT_F32) ? 4 : 2;
     p.vec_store = (ldy % 4 == 0) && aligned(Y, 4 * esz) && (bias == nullptr || aligned(bias, 16));
     if (bias && !aligned(bias, 16)) return fail(INV_ERR_ARG, "internal: bias not 16-byte aligned");
-    const int64_t KT = (K + 63) / 64;
+    const int64_t KT = (K + cm.bk - 1) / cm.bk;  // the kernel's k-tiles
     bool split = tc.ksplit > 1 && KT > 1;
     if (split) {
         p.kt_per_split = (int)((KT + tc.ksplit - 1) / tc.ksplit);
@@ -343,9 +316,7 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
         p.kt_per_split = (int)KT;
     } else {
         const int64_t ntiles = (int64_t)p.tiles_m * p.tiles_n;
-        const int nthreads = (tc.cfg == 4) ? 256 : 256;
-        const int64_t acc_regs = (int64_t)kCfgTN[tc.cfg] * kCfgTM[tc.cfg] / nthreads;
-        TRY(ensure(g.partial, (size_t)(ntiles * p.ksplit * nthreads * acc_regs) * sizeof(float)));
+        TRY(ensure(g.partial, (size_t)(ntiles * p.ksplit * cm.threads * cm.acc_regs) * sizeof(float)));
         size_t cbytes = (size_t)ntiles * sizeof(unsigned);
         if (g.counters.cap < cbytes) {
             TRY(ensure(g.counters, cbytes));
@@ -355,7 +326,7 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
         p.counters = (unsigned *)g.counters.p;
     }
     if (g.stats) HIPCHK(hipEventRecord(g.st0, g.stream));
-    TRY(launch_cfg(tc.cfg, p, epi, out, split));
+    HIPCHK(cm.launch(p, epi, out, split, g.stream));
     if (g.stats) {
         HIPCHK(hipEventRecord(g.st1, g.stream));
         HIPCHK(hipEventSynchronize(g.st1));
@@ -785,7 +756,7 @@ int inv_hip_linear(const void *X, int x_dtype, inv_weight_t W, const float *bias
     }
     if (precise)
         TRY(run_gemm(W->w, W->ldw, Xd, ldx, Yd, N, out, bd, nullptr, 0, 1.0f, 0.0f, M, N, 2 * kseg, epilogue,
-                     (int)(kseg / 64), W->ldw));
+                     kseg, W->ldw));
     else
         TRY(run_gemm(W->w, W->ldw, Xd, ldx, Yd, N, out, bd, nullptr, 0, 1.0f, 0.0f, M, N, W->ldw, epilogue));
     g.calls++;

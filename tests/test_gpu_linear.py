@@ -157,7 +157,7 @@ def test_weight_upload_from_fp32_rounds_rne(hiplib):
 
 # ------------------------------------------------------------ tiles, split-K
 
-@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4, 5, 6, 7])
 @pytest.mark.parametrize("ksplit", [1, 3])
 def test_every_tile_shape_and_split(hiplib, monkeypatch, cfg, ksplit):
     monkeypatch.setenv("INV_HIP_TILE_CFG", str(cfg))
@@ -178,7 +178,7 @@ def test_split_k_result_independent_of_split_count(hiplib, monkeypatch):
     with q.Weight(W, b) as w:
         for ks in (1, 2, 4, 8):
             monkeypatch.setenv("INV_HIP_KSPLIT", str(ks))
-            monkeypatch.setenv("INV_HIP_TILE_CFG", "2")
+            monkeypatch.setenv("INV_HIP_TILE_CFG", "3")
             outs.append(q.linear(X, w))
     for o in outs[1:]:
         assert oracle.normwise_err(o, outs[0]) < 1e-6
