@@ -26,6 +26,6 @@ struct GemmParams;
 }
 
 #define INV_DECLARE_LAUNCH(id) \
-    hipError_t inv_gemm_launch_##id(const inv::GemmParams &p, int epi, int out, bool split, hipStream_t s);
+    hipError_t inv_gemm_launch_##id(const inv::GemmParams &p, int epi, int out, int mode, hipStream_t s);
 INV_GEMM_CONFIG_IDS(INV_DECLARE_LAUNCH)
 #undef INV_DECLARE_LAUNCH

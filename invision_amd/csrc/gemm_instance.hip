@@ -11,42 +11,46 @@
 
 namespace {
 
-template <class C, int EPI, int OUT, bool SPLIT>
+template <class C, int EPI, int OUT, int MODE>
 void launch_one(const inv::GemmParams &p, dim3 grid, dim3 block, hipStream_t s) {
-    hipLaunchKernelGGL((inv::gemm_nt_bf16_kernel<C, EPI, OUT, SPLIT>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((inv::gemm_nt_bf16_kernel<C, EPI, OUT, MODE>), grid, block, 0, s, p);
 }
 
-template <class C, bool SPLIT>
+template <class C, int MODE>
 void launch_epi(const inv::GemmParams &p, int epi, int out, dim3 grid, dim3 block, hipStream_t s) {
     const bool f32 = out == inv::OUT_F32;
     if (epi == inv::EPI_SILU) {
-        if (f32) launch_one<C, inv::EPI_SILU, inv::OUT_F32, SPLIT>(p, grid, block, s);
-        else launch_one<C, inv::EPI_SILU, inv::OUT_BF16, SPLIT>(p, grid, block, s);
+        if (f32) launch_one<C, inv::EPI_SILU, inv::OUT_F32, MODE>(p, grid, block, s);
+        else launch_one<C, inv::EPI_SILU, inv::OUT_BF16, MODE>(p, grid, block, s);
     } else if (epi == inv::EPI_GELU) {
-        if (f32) launch_one<C, inv::EPI_GELU, inv::OUT_F32, SPLIT>(p, grid, block, s);
-        else launch_one<C, inv::EPI_GELU, inv::OUT_BF16, SPLIT>(p, grid, block, s);
+        if (f32) launch_one<C, inv::EPI_GELU, inv::OUT_F32, MODE>(p, grid, block, s);
+        else launch_one<C, inv::EPI_GELU, inv::OUT_BF16, MODE>(p, grid, block, s);
     } else {
-        if (f32) launch_one<C, inv::EPI_NONE, inv::OUT_F32, SPLIT>(p, grid, block, s);
-        else launch_one<C, inv::EPI_NONE, inv::OUT_BF16, SPLIT>(p, grid, block, s);
+        if (f32) launch_one<C, inv::EPI_NONE, inv::OUT_F32, MODE>(p, grid, block, s);
+        else launch_one<C, inv::EPI_NONE, inv::OUT_BF16, MODE>(p, grid, block, s);
     }
 }
 
+// mode: inv::GRID_TILES (one workgroup per tile), GRID_SPLITK (tiles x ksplit
+// workgroups) or GRID_STREAMK (p.ksplit is then the persistent grid size).
 template <class C>
-hipError_t launch_cfg(const inv::GemmParams &p, int epi, int out, bool split, hipStream_t s) {
+hipError_t launch_cfg(const inv::GemmParams &p, int epi, int out, int mode, hipStream_t s) {
     dim3 block(C::NTHREADS);
-    dim3 grid((unsigned)(p.tiles_m * p.tiles_n * (split ? p.ksplit : 1)));
-    if (split)
-        launch_epi<C, true>(p, epi, out, grid, block, s);
+    const unsigned ntiles = (unsigned)(p.tiles_m * p.tiles_n);
+    if (mode == inv::GRID_SPLITK)
+        launch_epi<C, inv::GRID_SPLITK>(p, epi, out, dim3(ntiles * p.ksplit), block, s);
+    else if (mode == inv::GRID_STREAMK)
+        launch_epi<C, inv::GRID_STREAMK>(p, epi, out, dim3((unsigned)p.ksplit), block, s);
     else
-        launch_epi<C, false>(p, epi, out, grid, block, s);
+        launch_epi<C, inv::GRID_TILES>(p, epi, out, dim3(ntiles), block, s);
     return hipGetLastError();
 }
 
 }  // namespace
 
 #define INV_DEFINE_LAUNCH_(id, params)                                                                      \
-    hipError_t inv_gemm_launch_##id(const inv::GemmParams &p, int epi, int out, bool split, hipStream_t s) { \
-        return launch_cfg<inv::TileCfg<params>>(p, epi, out, split, s);                                     \
+    hipError_t inv_gemm_launch_##id(const inv::GemmParams &p, int epi, int out, int mode, hipStream_t s) {   \
+        return launch_cfg<inv::TileCfg<params>>(p, epi, out, mode, s);                                      \
     }
 #define INV_DEFINE_LAUNCH(id) INV_DEFINE_LAUNCH_(id, INV_CFG_PARAMS_##id)
 #define INV_EXPAND_DEFINE(id) INV_DEFINE_LAUNCH(id)

@@ -60,11 +60,12 @@ struct GemmParams {
     int M, N, K;          // K: the reduction length of X (and of W unless it wraps)
     int w_seg_k, Kw;      // W wraps every w_seg_k columns (a multiple of 64; 0: no wrap); Kw: valid K of W
     int tiles_m, tiles_n, group_m;
-    int ksplit, kt_per_split;  // K tiles per split
+    int ksplit, kt_per_split;  // split-K: splits, K tiles per split; stream-K: ksplit = persistent grid size
+    int sk_dp_tiles;           // stream-K: tiles done one per workgroup (whole rounds) before the balanced phase
     float alpha, beta;
     int has_bias, vec_store;
-    float *partial;       // split-K workspace: [tiles][ksplit][threads][acc regs]
-    unsigned *counters;   // split-K arrival counters, one per tile, zero between calls
+    float *partial;       // split/stream-K partial sums (uncached device memory)
+    unsigned *counters;   // arrival counters, one per tile, zero between calls (uncached)
 };
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
@@ -92,14 +93,17 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
 }
 
-// Workgroup id -> output tile, XCD-aware and grouped along m.
-__device__ __forceinline__ void tile_coords(int bid, int ntiles, int tiles_m, int group_m, int &tm, int &tn) {
-    // Undo the round-robin XCD dispatch: consecutive logical ids share an XCD.
-    const int per = ntiles >> 3, rem = ntiles & 7;
+// Hardware dispatches workgroup b to XCD b % 8.  xcd_remap turns the
+// dispatch index into a logical index whose consecutive values share an XCD,
+// so that neighbouring tiles (which share X and W panels) meet in one L2.
+__device__ __forceinline__ int xcd_remap(int bid, int count) {
+    const int per = count >> 3, rem = count & 7;
     const int xcd = bid & 7, local = bid >> 3;
-    int L = (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
-    // Grouped order: group_m tile rows, walked column by column.
-    const int tiles_n = ntiles / tiles_m;
+    return (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+}
+
+// Logical tile index -> (tm, tn): group_m tile rows, walked column by column.
+__device__ __forceinline__ void grouped_tile(int L, int tiles_m, int tiles_n, int group_m, int &tm, int &tn) {
     const int group_size = group_m * tiles_n;
     const int g = L / group_size;
     const int first_m = g * group_m;
@@ -237,39 +241,55 @@ constexpr int copy_step(int i) {
 }
 #endif  // __HIP_DEVICE_COMPILE__
 
-// The body is compiled only in the device pass: the host pass needs just the
-// launch stub, and buffer-resource types do not exist for the host target.
-template <class C, int EPI, int OUT, bool SPLIT>
-__global__ void __launch_bounds__(C::NTHREADS, 1) gemm_nt_bf16_kernel(const GemmParams p) {
+enum GridMode { GRID_TILES = 0, GRID_SPLITK = 1, GRID_STREAMK = 2 };
+
 #if defined(__HIP_DEVICE_COMPILE__)
+
+// How a work unit's accumulators become output: directly (the unit is a whole
+// tile), or through the partial-sum workspace when several units share a tile
+// (split-K: ksplit equal K ranges; stream-K: the ranges cut by the persistent
+// workgroups' shares of the global k-iteration space).
+struct UnitFix {
+    int tile;     // tile id (counter index)
+    int rel_tile; // stream-K: tile index within the balanced phase
+    int nseg;     // units sharing the tile (1: direct)
+    int my_seg;   // this unit's position among them, in K order
+    int g_first;  // stream-K: workgroup owning segment 0
+    int G, KT;    // stream-K: grid size, k-tiles per tile
+    int64_t I;    // stream-K: total k-iterations
+};
+
+// Start of stream-K workgroup g's share of [0, I).
+__device__ __forceinline__ int64_t sk_start(int64_t g, int64_t I, int64_t G) { return g * I / G; }
+
+// Workspace slot of segment `seg` of a shared tile.  Split-K: one slot per
+// (tile, split).  Stream-K: each workgroup owns two slots, one for the first
+// and one for the last unit of its share (only those two can be partial).
+template <int MODE, class C>
+__device__ __forceinline__ float *unit_slot(const GemmParams &p, const UnitFix &f, int seg) {
+    constexpr int64_t SZ = (int64_t)C::NTHREADS * C::ACC_REGS;
+    if constexpr (MODE == GRID_SPLITK) {
+        return p.partial + ((int64_t)f.tile * f.nseg + seg) * SZ;
+    } else {
+        const int64_t g = f.g_first + seg;
+        const bool starts_before = sk_start(g, f.I, f.G) < (int64_t)f.rel_tile * f.KT;
+        return p.partial + (2 * g + (starts_before ? 1 : 0)) * SZ;
+    }
+}
+
+// One work unit: output tile (tm, tn), k-tiles [kt_begin, kt_end).
+template <class C, int EPI, int OUT, int MODE>
+__device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int tm, int tn, int kt_begin, int kt_end,
+                                          const UnitFix &fix) {
     constexpr int BK = C::BK;
     constexpr int NST = C::NST;
-    __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
-
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wn = wave / C::WM;
     const int wm = wave % C::WM;
-
-    const int ntiles = p.tiles_m * p.tiles_n;
-    int bid = blockIdx.x;
-    int split = 0;
-    if constexpr (SPLIT) {
-        split = bid % p.ksplit;
-        bid = bid / p.ksplit;
-    }
-    int tm, tn;
-    tile_coords(bid, ntiles, p.tiles_m, p.group_m, tm, tn);
     const int m0 = tm * C::TM;
     const int n0 = tn * C::TN;
-
-    const int KT = (p.K + BK - 1) / BK;
-    int kt_begin = 0, kt_end = KT;
-    if constexpr (SPLIT) {
-        kt_begin = split * p.kt_per_split;
-        kt_end = min(KT, kt_begin + p.kt_per_split);
-    }
 
     // Buffer resources covering exactly the valid rows of this tile's panels.
     const int rows_w = min(C::TN, p.N - n0);
@@ -320,19 +340,18 @@ __global__ void __launch_bounds__(C::NTHREADS, 1) gemm_nt_bf16_kernel(const Gemm
     const int wseg = p.w_seg_k / BK;  // W k-tiles per wrap segment (0: no wrap)
     int load_kt = kt_begin;
     int load_ktw = wseg ? kt_begin % wseg : kt_begin;
-    auto issue_next = [&](int stage) {
-        const bool in = load_kt < kt_end;
-        issue_tile_loads<C>(rsw, rsx, lds + stage * C::STAGE_BYTES, wave, a_base, a_step, b_base, b_step,
-                            k_byte_offset<BK>(in && load_ktw * BK + ld_chunk * 8 < p.Kw, load_ktw),
-                            k_byte_offset<BK>(in && load_kt * BK + ld_chunk * 8 < p.K, load_kt));
-        ++load_kt;
-        load_ktw = (wseg && load_ktw + 1 == wseg) ? 0 : load_ktw + 1;
-    };
 
     // Prologue: k-tiles 0 .. NST-2 in flight; wait for the first, read its
     // first substep.
 #pragma unroll
-    for (int s = 0; s < NST - 1; ++s) issue_next(s);
+    for (int s = 0; s < NST - 1; ++s) {
+        const bool in = load_kt < kt_end;
+        issue_tile_loads<C>(rsw, rsx, lds + s * C::STAGE_BYTES, wave, a_base, a_step, b_base, b_step,
+                            k_byte_offset<BK>(in && load_ktw * BK + ld_chunk * 8 < p.Kw, load_ktw),
+                            k_byte_offset<BK>(in && load_kt * BK + ld_chunk * 8 < p.K, load_kt));
+        ++load_kt;
+        load_ktw = (wseg && load_ktw + 1 == wseg) ? 0 : load_ktw + 1;
+    }
     wait_vmcnt<(NST - 2) * C::LOADS>();
     __syncthreads();
 
@@ -396,61 +415,70 @@ __global__ void __launch_bounds__(C::NTHREADS, 1) gemm_nt_bf16_kernel(const Gemm
         stage = next_stage;
     }
     // The copies of the k-tiles past the end still write LDS; let them land
-    // before the workgroup can retire.
+    // before the ring is reused or the workgroup retires.
     wait_vmcnt<0>();
 
-    if constexpr (SPLIT) {
-        // Park this split's partial sums, then let the last arriving split finish.
-        float *mine = p.partial + ((int64_t)bid * p.ksplit + split) * (C::NTHREADS * C::ACC_REGS);
+    if constexpr (MODE != GRID_TILES) {
+        if (fix.nseg > 1) {
+            // Park this unit's partial sums, then let the last arriving unit of
+            // the tile finish it.
+            float *mine = unit_slot<MODE, C>(p, fix, fix.my_seg);
 #pragma unroll
-        for (int i = 0; i < C::FN; ++i)
+            for (int i = 0; i < C::FN; ++i)
 #pragma unroll
-            for (int j = 0; j < C::FM; ++j)
+                for (int j = 0; j < C::FM; ++j)
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    f32x4_t v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-                    *(f32x4_t *)(mine + ((((i * C::FM + j) * 4 + g) * C::NTHREADS + tid) * 4)) = v;
-                }
-        // The flag lives in the (now idle) ring: the barrier below completes
-        // every wave's LDS reads before thread 0 writes it.
-        volatile unsigned *s_last = (volatile unsigned *)smem;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __syncthreads();
-        if (tid == 0) {
-            unsigned prev = __hip_atomic_fetch_add(&p.counters[bid], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            *s_last = (prev == (unsigned)(p.ksplit - 1)) ? 1u : 0u;
-        }
-        __syncthreads();
-        if (!*s_last) return;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        // Sum the partials in split order so the result does not depend on
-        // which split arrived last.
-        const float *base = p.partial + (int64_t)bid * p.ksplit * (C::NTHREADS * C::ACC_REGS);
-#pragma unroll
-        for (int i = 0; i < C::FN; ++i)
-#pragma unroll
-            for (int j = 0; j < C::FM; ++j)
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    f32x4_t s = {0.f, 0.f, 0.f, 0.f};
-                    for (int sp = 0; sp < p.ksplit; ++sp) {
-                        f32x4_t v;
-                        if (sp == split) {
-                            v = f32x4_t{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                                        acc[i][j][4 * g + 3]};
-                        } else {
-                            v = __builtin_nontemporal_load(
-                                (const f32x4_t *)(base + (int64_t)sp * (C::NTHREADS * C::ACC_REGS) +
-                                                  ((((i * C::FM + j) * 4 + g) * C::NTHREADS + tid) * 4)));
-                        }
-                        s += v;
+                    for (int g = 0; g < 4; ++g) {
+                        f32x4_t v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                     acc[i][j][4 * g + 3]};
+                        *(f32x4_t *)(mine + ((((i * C::FM + j) * 4 + g) * C::NTHREADS + tid) * 4)) = v;
                     }
-                    acc[i][j][4 * g] = s[0];
-                    acc[i][j][4 * g + 1] = s[1];
-                    acc[i][j][4 * g + 2] = s[2];
-                    acc[i][j][4 * g + 3] = s[3];
+            // The workspace and counters are uncached device memory: stores,
+            // loads and atomics go to memory, so they are coherent across XCDs
+            // without agent-scope fences (which would write back and
+            // invalidate this XCD's whole L2).  Publishing the partial needs
+            // only its stores to be acknowledged before the counter moves.
+            wait_vmcnt<0>();
+            // The flag lives in the (now idle) ring: the barrier below completes
+            // every wave's LDS reads and partial stores before thread 0 acts.
+            volatile __attribute__((address_space(3))) unsigned *s_last =
+                (volatile __attribute__((address_space(3))) unsigned *)lds;
+            __syncthreads();
+            if (tid == 0) {
+                unsigned prev =
+                    __hip_atomic_fetch_add(&p.counters[fix.tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                *s_last = (prev == (unsigned)(fix.nseg - 1)) ? 1u : 0u;
+            }
+            __syncthreads();
+            const bool last = *s_last != 0;
+            __syncthreads();  // everyone has read the flag before the ring is reused
+            if (!last) return;
+            // Sum the partials in K order (this unit's own included, read back)
+            // so the result does not depend on which unit arrived last.  The
+            // segment loop is outermost so each segment's loads issue together.
+            // Plain loads: the barrier above orders them after the counter, and
+            // each slot is uncached and written once per launch.
+            for (int sp = 0; sp < fix.nseg; ++sp) {
+                const float *src = unit_slot<MODE, C>(p, fix, sp);
+#pragma unroll
+                for (int i = 0; i < C::FN; ++i) {
+                    // one fragment row at a time: FM*4 loads in flight, then the adds
+                    f32x4_t v[C::FM * 4];
+#pragma unroll
+                    for (int q = 0; q < C::FM * 4; ++q)
+                        v[q] = __builtin_nontemporal_load(
+                            (const f32x4_t *)(src + (((i * C::FM * 4 + q) * C::NTHREADS + tid) * 4)));
+#pragma unroll
+                    for (int q = 0; q < C::FM * 4; ++q)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            acc[i][q >> 2][4 * (q & 3) + e] =
+                                (sp == 0) ? v[q][e] : acc[i][q >> 2][4 * (q & 3) + e] + v[q][e];
                 }
-        if (tid == 0) p.counters[bid] = 0u;  // ready for the next call
+            }
+            if (tid == 0)  // ready for the next call
+                __hip_atomic_store(&p.counters[fix.tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 
     // Epilogue: lane holds D[n = 8g + 4h + e][m = lane & 31] of each 32x32 block.
@@ -506,6 +534,90 @@ __global__ void __launch_bounds__(C::NTHREADS, 1) gemm_nt_bf16_kernel(const Gemm
                     }
                 }
             }
+        }
+    }
+}
+
+#endif  // __HIP_DEVICE_COMPILE__
+
+// The body is compiled only in the device pass: the host pass needs just the
+// launch stub, and buffer-resource types do not exist for the host target.
+//  GRID_TILES:   one workgroup per output tile.
+//  GRID_SPLITK:  ksplit workgroups per tile, equal K ranges.
+//  GRID_STREAMK: a persistent grid of G workgroups.  The first sk_dp_tiles
+//                tiles (whole rounds) go one per workgroup; then workgroup g
+//                takes k-iterations [g*I/G, (g+1)*I/G) of the I = (remaining
+//                tiles) * KT, in tile order, so every workgroup ends together.
+template <class C, int EPI, int OUT, int MODE>
+__global__ void __launch_bounds__(C::NTHREADS, 1) gemm_nt_bf16_kernel(const GemmParams p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+    const int ntiles = p.tiles_m * p.tiles_n;
+    const int KT = (p.K + C::BK - 1) / C::BK;
+    int tm, tn;
+    if constexpr (MODE == GRID_TILES) {
+        grouped_tile(xcd_remap(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+        UnitFix fix{};
+        fix.nseg = 1;
+        gemm_unit<C, EPI, OUT, MODE>(p, smem, tm, tn, 0, KT, fix);
+    } else if constexpr (MODE == GRID_SPLITK) {
+        const int split = blockIdx.x % p.ksplit;
+        const int tile = blockIdx.x / p.ksplit;
+        grouped_tile(xcd_remap(tile, ntiles), p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+        UnitFix fix{};
+        fix.tile = tile;
+        fix.nseg = p.ksplit;
+        fix.my_seg = split;
+        const int kt_begin = split * p.kt_per_split;
+        gemm_unit<C, EPI, OUT, MODE>(p, smem, tm, tn, kt_begin, min(KT, kt_begin + p.kt_per_split), fix);
+    } else {
+        const int G = gridDim.x;
+        const int g = xcd_remap(blockIdx.x, G);
+        // Whole rounds first, one tile per workgroup (compact in L2, no
+        // partial sums), then the remaining tiles' k-iterations in equal
+        // shares.  One loop with one call site keeps a single copy of the unit
+        // body (two copies spill registers).
+        const int t0 = p.sk_dp_tiles;
+        const int64_t I = (int64_t)(ntiles - t0) * KT;
+        int dp_tile = g;
+        int64_t it = sk_start(g, I, G);
+        const int64_t end = sk_start(g + 1, I, G);
+        while (true) {
+            UnitFix fix{};
+            int tile, klo, khi;
+            if (dp_tile < t0) {
+                tile = dp_tile;
+                klo = 0;
+                khi = KT;
+                fix.nseg = 1;
+                dp_tile += G;
+            } else if (it < end) {
+                const int rt = (int)(it / KT);  // tile index within the balanced phase
+                tile = t0 + rt;
+                klo = (int)(it - (int64_t)rt * KT);
+                khi = (int)min((int64_t)KT, (int64_t)klo + (end - it));
+                it += khi - klo;
+                fix.tile = tile;
+                fix.rel_tile = rt;
+                fix.G = G;
+                fix.KT = KT;
+                fix.I = I;
+                // Workgroups whose shares meet this tile: the first is the one
+                // whose share contains iteration rt*KT, the last the one
+                // containing (rt+1)*KT - 1 (largest g with g*I/G <= x is
+                // ceil((x+1)G/I) - 1).
+                const int64_t x0 = (int64_t)rt * KT, x1 = (int64_t)(rt + 1) * KT - 1;
+                const int g_first = (int)(((x0 + 1) * G + I - 1) / I - 1);
+                const int g_last = (int)(((x1 + 1) * G + I - 1) / I - 1);
+                fix.g_first = g_first;
+                fix.nseg = g_last - g_first + 1;
+                fix.my_seg = g - g_first;
+            } else {
+                break;
+            }
+            grouped_tile(tile, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+            gemm_unit<C, EPI, OUT, MODE>(p, smem, tm, tn, klo, khi, fix);
+            __syncthreads();  // the next unit's prologue overwrites the ring
         }
     }
 #endif  // __HIP_DEVICE_COMPILE__

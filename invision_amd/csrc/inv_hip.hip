@@ -68,7 +68,12 @@ struct State {
     void *pin[2] = {nullptr, nullptr};
     int cu_count = 0, clock_khz = 0;
     char name[256] = {0};
-    Buf xin, x16, w16, win, yout, cin, bias, partial, counters;
+    Buf xin, x16, w16, win, yout, cin, bias;
+    // Split/stream-K partial sums and arrival counters: uncached device memory
+    // (coherent across XCDs without L2 maintenance).  Such memory is never
+    // freed once a kernel has read it: outgrown buffers are retired, not freed.
+    Buf partial, counters;
+    std::vector<void *> retired_uncached;
     int sgemm_prec = INV_PREC_SPLIT_AB;
     bool stats = false;
     int64_t calls = 0;
@@ -107,6 +112,22 @@ int ensure(Buf &b, size_t bytes) {
         b.p = nullptr;
         return fail(INV_ERR_OOM, "device allocation of %zu bytes failed", nb);
     }
+    b.cap = nb;
+    return INV_OK;
+}
+
+// Grow-only uncached buffer; the old one is retired (kept until process exit).
+int ensure_uncached(Buf &b, size_t bytes, bool zero) {
+    if (b.cap >= bytes) return INV_OK;
+    size_t nb = (size_t)round_up((int64_t)std::max<size_t>(bytes, 1), 2 << 20);
+    void *p = nullptr;
+    if (hipExtMallocWithFlags(&p, nb, hipDeviceMallocUncached) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(INV_ERR_OOM, "uncached device allocation of %zu bytes failed", nb);
+    }
+    if (zero) HIPCHK(hipMemsetAsync(p, 0, nb, g.stream));
+    if (b.p) g.retired_uncached.push_back(b.p);
+    b.p = p;
     b.cap = nb;
     return INV_OK;
 }
@@ -201,19 +222,21 @@ int d2h_rows(void *host, const void *dev, int64_t rows, size_t width, size_t pit
 // ---------------------------------------------------------------------------
 
 struct TileChoice {
-    int cfg;     // index into the instantiated tile configurations
-    int ksplit;  // 1 = no split
+    int cfg;    // index into the instantiated tile configurations
+    int mode;   // inv::GRID_TILES, GRID_SPLITK or GRID_STREAMK
+    int count;  // split-K: splits per tile; stream-K: persistent workgroups
 };
 
 // Instantiated tile configurations (gemm_configs.hpp).
 struct CfgMeta {
-    int tn, tm, threads, acc_regs, bk;
-    hipError_t (*launch)(const inv::GemmParams &, int, int, bool, hipStream_t);
+    int tn, tm, threads, acc_regs, bk, lds;
+    hipError_t (*launch)(const inv::GemmParams &, int, int, int, hipStream_t);
 };
 #define INV_META(id)                                                                                 \
     {inv::TileCfg<INV_CFG_PARAMS_##id>::TN, inv::TileCfg<INV_CFG_PARAMS_##id>::TM,                  \
      inv::TileCfg<INV_CFG_PARAMS_##id>::NTHREADS, inv::TileCfg<INV_CFG_PARAMS_##id>::ACC_REGS,      \
-     inv::TileCfg<INV_CFG_PARAMS_##id>::BK, &inv_gemm_launch_##id},
+     inv::TileCfg<INV_CFG_PARAMS_##id>::BK, inv::TileCfg<INV_CFG_PARAMS_##id>::LDS_BYTES,           \
+     &inv_gemm_launch_##id},
 const CfgMeta kCfg[INV_GEMM_NUM_CONFIGS] = {INV_GEMM_CONFIG_IDS(INV_META)};
 #undef INV_META
 constexpr int kNumCfg = INV_GEMM_NUM_CONFIGS;
@@ -223,48 +246,70 @@ int env_int(const char *name, int dflt) {
     return (v && *v) ? atoi(v) : dflt;
 }
 
-// Pick a tile shape and split-K factor.  Large problems take the 256x256 tile;
-// skinny ones stream W with a short X tile and split K until the grid covers
-// the chip at least twice.
+// Workgroups of configuration m resident per CU (LDS is the binding limit).
+int cfg_occupancy(const CfgMeta &m) { return std::max(1, std::min(2, (160 * 1024) / m.lds)); }
+
+// Pick a tile shape and how the grid covers it.  Large problems take the
+// 256x256 tile; skinny ones stream W with a short X tile.  When the tile count
+// does not fill the chip in whole rounds (or is below one round and K is
+// long), a persistent stream-K grid gives every workgroup the same share of
+// k-iterations instead of leaving CUs idle in the last round.
 TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
-    TileChoice c{0, 1};
+    TileChoice c{0, inv::GRID_TILES, 1};
     const int cus = g.cu_count > 0 ? g.cu_count : 256;
-    const int64_t KT = (K + 63) / 64;
     if (M <= 32) {
         c.cfg = 5;
     } else if (M <= 64) {
         c.cfg = 4;
     } else {
-        // Among the larger tiles, the one that wastes least of the last wave
-        // of workgroups, weighting smaller tiles by their lower MFMA
-        // efficiency (more LDS traffic per MFMA).
+        // Among the larger tiles, the one with the least MFMA-feeding cost:
+        // the 256x256 tile loads and reads the fewest bytes per MFMA; smaller
+        // tiles only when the problem cannot fill the chip with it.
         const int cand[3] = {0, 2, 3};
-        const double eff[3] = {1.0, 0.85, 0.7};
+        const double eff[3] = {1.0, 0.8, 0.65};
         double best = -1.0;
         for (int q = 0; q < 3; ++q) {
             const CfgMeta &m = kCfg[cand[q]];
-            int64_t tiles = ((M + m.tm - 1) / m.tm) * ((N + m.tn - 1) / m.tn);
-            double waves = (double)((tiles + cus - 1) / cus);
-            double score = (double)M * N / (waves * cus * m.tm * m.tn) * eff[q];
+            const int64_t tiles = ((M + m.tm - 1) / m.tm) * ((N + m.tn - 1) / m.tn);
+            const double slots = (double)cus * cfg_occupancy(m);
+            // stream-K evens out the last round, so only under-filled chips pay
+            const double fill = std::min(1.0, (double)tiles / slots);
+            const double score = fill * eff[q] * ((double)M * N) / ((double)tiles * m.tm * m.tn);
             if (score > best) {
                 best = score;
                 c.cfg = cand[q];
             }
         }
     }
-    const CfgMeta &m = kCfg[c.cfg];
-    const int64_t tiles = ((M + m.tm - 1) / m.tm) * ((N + m.tn - 1) / m.tn);
-    const int64_t target = (m.threads == 256 && m.tn * m.tm <= 128 * 128) ? 2 * cus : cus;
-    if (tiles < target && KT >= 16) {
-        int64_t sp = (target + tiles - 1) / tiles;
-        sp = std::min<int64_t>(sp, KT / 8);
-        sp = std::min<int64_t>(sp, 16);
-        c.ksplit = (int)std::max<int64_t>(sp, 1);
-    }
     int ov = env_int("INV_HIP_TILE_CFG", -1);
     if (ov >= 0 && ov < kNumCfg) c.cfg = ov;
-    int ks = env_int("INV_HIP_KSPLIT", -1);
-    if (ks >= 1) c.ksplit = ks;
+    const CfgMeta &m = kCfg[c.cfg];
+    const int64_t KT = (K + m.bk - 1) / m.bk;
+    const int64_t tiles = ((M + m.tm - 1) / m.tm) * ((N + m.tn - 1) / m.tn);
+    const int64_t slots = (int64_t)cus * cfg_occupancy(m);
+    // Share of the slot-rounds left idle by one workgroup per tile.
+    const int64_t rounds = (tiles + slots - 1) / slots;
+    const double idle = 1.0 - (double)tiles / (double)(rounds * slots);
+    if (m.tm >= 128 && ((tiles * 2 <= slots && KT >= 32) || (idle >= 0.25 && KT >= 128))) {
+        // A persistent stream-K grid spreads the k-iterations over all slots
+        // (at least 8 k-tiles per workgroup so the pipeline fill stays cheap).
+        // It pays when the last round would leave many slots idle and K is
+        // deep enough to amortise the partial-sum handoff; measured: better
+        // at 512x2560x9728-down and 9216x3840x15360-down, worse at
+        // 4608x9216x3072 (16% idle) and for the bandwidth-bound small-M tiles.
+        c.mode = inv::GRID_STREAMK;
+        c.count = (int)std::max<int64_t>(1, std::min<int64_t>(slots, tiles * KT / 8));
+    }
+    const int mode = env_int("INV_HIP_MODE", -1);
+    if (mode == inv::GRID_TILES) {
+        c.mode = inv::GRID_TILES;
+    } else if (mode == inv::GRID_SPLITK) {
+        c.mode = inv::GRID_SPLITK;
+        c.count = std::max(1, env_int("INV_HIP_KSPLIT", 2));
+    } else if (mode == inv::GRID_STREAMK) {
+        c.mode = inv::GRID_STREAMK;
+        c.count = std::max(1, env_int("INV_HIP_SK_GRID", (int)slots));
+    }
     return c;
 }
 
@@ -305,28 +350,39 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
     p.vec_store = (ldy % 4 == 0) && aligned(Y, 4 * esz) && (bias == nullptr || aligned(bias, 16));
     if (bias && !aligned(bias, 16)) return fail(INV_ERR_ARG, "internal: bias not 16-byte aligned");
     const int64_t KT = (K + cm.bk - 1) / cm.bk;  // the kernel's k-tiles
-    bool split = tc.ksplit > 1 && KT > 1;
-    if (split) {
-        p.kt_per_split = (int)((KT + tc.ksplit - 1) / tc.ksplit);
+    const int64_t ntiles = (int64_t)p.tiles_m * p.tiles_n;
+    int mode = tc.mode;
+    p.ksplit = 1;
+    p.kt_per_split = (int)KT;
+    if (mode == inv::GRID_SPLITK) {
+        p.kt_per_split = (int)((KT + tc.count - 1) / tc.count);
         p.ksplit = (int)((KT + p.kt_per_split - 1) / p.kt_per_split);
-        split = p.ksplit > 1;
-    }
-    if (!split) {
-        p.ksplit = 1;
-        p.kt_per_split = (int)KT;
-    } else {
-        const int64_t ntiles = (int64_t)p.tiles_m * p.tiles_n;
-        TRY(ensure(g.partial, (size_t)(ntiles * p.ksplit * cm.threads * cm.acc_regs) * sizeof(float)));
-        size_t cbytes = (size_t)ntiles * sizeof(unsigned);
-        if (g.counters.cap < cbytes) {
-            TRY(ensure(g.counters, cbytes));
-            HIPCHK(hipMemsetAsync(g.counters.p, 0, g.counters.cap, g.stream));
+        if (p.ksplit <= 1) {
+            mode = inv::GRID_TILES;
+            p.ksplit = 1;
+            p.kt_per_split = (int)KT;
         }
+    } else if (mode == inv::GRID_STREAMK) {
+        // Whole rounds except the last full one go one tile per workgroup;
+        // the last full round plus the remainder are balanced, so each
+        // workgroup's balanced share is at least one tile's K loop.
+        const int64_t G = std::min<int64_t>(tc.count, ntiles * KT);
+        int64_t dp_rounds = std::max<int64_t>(0, ntiles / G - 1);
+        const int ov_rounds = env_int("INV_HIP_SK_DP_ROUNDS", -1);
+        if (ov_rounds >= 0) dp_rounds = std::min<int64_t>(ov_rounds, ntiles / G);
+        const int64_t rest = (ntiles - dp_rounds * G) * KT;  // k-iterations of the balanced phase
+        p.ksplit = (int)(rest > 0 ? std::min<int64_t>(G, rest) : G);  // persistent grid size
+        p.sk_dp_tiles = (int)(dp_rounds * G);
+    }
+    if (mode != inv::GRID_TILES) {
+        const int64_t slots = (mode == inv::GRID_SPLITK) ? ntiles * p.ksplit : 2 * (int64_t)p.ksplit;
+        TRY(ensure_uncached(g.partial, (size_t)(slots * cm.threads * cm.acc_regs) * sizeof(float), false));
+        TRY(ensure_uncached(g.counters, (size_t)ntiles * sizeof(unsigned), true));
         p.partial = (float *)g.partial.p;
         p.counters = (unsigned *)g.counters.p;
     }
     if (g.stats) HIPCHK(hipEventRecord(g.st0, g.stream));
-    HIPCHK(cm.launch(p, epi, out, split, g.stream));
+    HIPCHK(cm.launch(p, epi, out, mode, g.stream));
     if (g.stats) {
         HIPCHK(hipEventRecord(g.st1, g.stream));
         HIPCHK(hipEventSynchronize(g.st1));
@@ -640,7 +696,8 @@ int inv_hip_shutdown(void) {
     (void)hipStreamSynchronize(g.stream);
     for (auto *w : g.weights) free_weight(w);
     g.weights.clear();
-    for (Buf *b : {&g.xin, &g.x16, &g.w16, &g.win, &g.yout, &g.cin, &g.bias, &g.partial, &g.counters}) release(*b);
+    for (Buf *b : {&g.xin, &g.x16, &g.w16, &g.win, &g.yout, &g.cin, &g.bias}) release(*b);
+    // g.partial / g.counters (uncached) stay allocated until the process ends.
     for (int k = 0; k < 2; ++k) {
         if (g.pin[k]) (void)hipHostFree(g.pin[k]);
         if (g.pin_ev[k]) (void)hipEventDestroy(g.pin_ev[k]);

@@ -157,11 +157,20 @@ def test_weight_upload_from_fp32_rounds_rne(hiplib):
 
 # ------------------------------------------------------------ tiles, split-K
 
+GRID_MODES = {  # INV_HIP_MODE / INV_HIP_KSPLIT / INV_HIP_SK_GRID
+    "tiles": {"INV_HIP_MODE": "0"},
+    "splitk3": {"INV_HIP_MODE": "1", "INV_HIP_KSPLIT": "3"},
+    "streamk256": {"INV_HIP_MODE": "2", "INV_HIP_SK_GRID": "256"},
+    "streamk37": {"INV_HIP_MODE": "2", "INV_HIP_SK_GRID": "37"},
+}
+
+
 @pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4, 5, 6, 7])
-@pytest.mark.parametrize("ksplit", [1, 3])
-def test_every_tile_shape_and_split(hiplib, monkeypatch, cfg, ksplit):
+@pytest.mark.parametrize("grid", sorted(GRID_MODES))
+def test_every_tile_shape_and_grid_mode(hiplib, monkeypatch, cfg, grid):
     monkeypatch.setenv("INV_HIP_TILE_CFG", str(cfg))
-    monkeypatch.setenv("INV_HIP_KSPLIT", str(ksplit))
+    for k, v in GRID_MODES[grid].items():
+        monkeypatch.setenv(k, v)
     M, K, N = 300, 1000, 520
     X, W, b = gen(10, M, K, N)
     with q.Weight(W, b) as w:
@@ -171,12 +180,27 @@ def test_every_tile_shape_and_split(hiplib, monkeypatch, cfg, ksplit):
     np.testing.assert_array_equal(y, y2)  # deterministic, counters reset
 
 
+@pytest.mark.parametrize("M,K,N", [(4608, 3072, 9216), (512, 9728, 2560), (777, 1304, 1000)])
+def test_stream_k_matches_one_workgroup_per_tile(hiplib, monkeypatch, M, K, N):
+    X, W, b = gen(15, M, K, N)
+    Xb = as_bf16_bits(X)
+    with q.Weight(W, b) as w:
+        monkeypatch.setenv("INV_HIP_MODE", "0")
+        y0 = q.linear(Xb, w)
+        monkeypatch.setenv("INV_HIP_MODE", "2")
+        y1 = q.linear(Xb, w)
+    # same products, different association across the K split: rounding-level
+    assert oracle.normwise_err(y1, y0) < 5e-6
+    check(y1, X, W, b, rows=sample_rows(M, 24))
+
+
 def test_split_k_result_independent_of_split_count(hiplib, monkeypatch):
     M, K, N = 256, 2048, 384
     X, W, b = gen(11, M, K, N)
     outs = []
     with q.Weight(W, b) as w:
         for ks in (1, 2, 4, 8):
+            monkeypatch.setenv("INV_HIP_MODE", "1")
             monkeypatch.setenv("INV_HIP_KSPLIT", str(ks))
             monkeypatch.setenv("INV_HIP_TILE_CFG", "3")
             outs.append(q.linear(X, w))
@@ -231,14 +255,17 @@ def test_c3_mlp_up_silu_then_down(hiplib):
     Xr = round_bf16(X[rows])
     H_ref = oracle.linear_bf16w(Xr, Wu, bu, oracle.EPI_SILU)
     e_h = oracle.normwise_err(bf16_bits_to_f32(H[rows]), H_ref)
-    Y_ref = oracle.linear_bf16w(round_bf16(H_ref), Wd, bd)
+    # The down projection on the device's own bf16 H (an H element whose fp32
+    # sum sits near a bf16 tie may round one ulp apart from the oracle's).
+    Y_ref = oracle.linear_bf16w(bf16_bits_to_f32(H[rows]), Wd, bd)
     e_y = oracle.normwise_err(y[rows], Y_ref)
-    # fp32-activation reference chain: H kept fp32 between the GEMMs
+    # The reference's chain keeps X and H in fp32; this one rounds both to bf16,
+    # and each rounded activation contributes up to TOL_REF.
     H_f = oracle.linear_bf16w(X[rows], Wu, bu, oracle.EPI_SILU)
     Y_f = oracle.linear_bf16w(H_f, Wd, bd)
     e_ref = oracle.normwise_err(y[rows], Y_f)
-    print(f"  H err {e_h:.3e}, Y err (bf16 chain) {e_y:.3e}, Y err vs fp32 reference chain {e_ref:.3e}", flush=True)
-    assert e_h <= TOL_BF16_OUT and e_y <= 1e-4 and e_ref <= TOL_REF
+    print(f"  H err {e_h:.3e}, Y err (on device H) {e_y:.3e}, Y err vs fp32 reference chain {e_ref:.3e}", flush=True)
+    assert e_h <= TOL_BF16_OUT and e_y <= TOL_TIGHT and e_ref <= 2 * TOL_REF
 
 
 @pytest.mark.parametrize("which", ["gate_up", "down"])
