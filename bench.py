@@ -69,7 +69,7 @@ def algorithmic_bytes(M, K, N, bias, xdt, ydt):
     return M * K * xs + N * K * 2 + M * N * ys + (4 * N if bias else 0)
 
 
-def run_workload(name, steps, warmup, check=True):
+def run_workload(name, steps, warmup, check=True, host_path=False):
     from invision_amd import hip
     from invision_amd import quicknn_hip as q
     from invision_amd.bf16 import as_bf16_bits, bf16_bits_to_f32
@@ -97,11 +97,33 @@ def run_workload(name, steps, warmup, check=True):
     t1 = time.perf_counter()
     wall_ms = (t1 - t0) * 1e3 / steps
     gpu_ms = ms.value / steps
+    # Per-launch spread: each launch bracketed by its own events (outside the timed region).
+    per = []
+    for _ in range(min(steps, 30)):
+        hip.call("inv_hip_timer_start")
+        q.linear_device(xd, w, yd, M, epilogue=epi, asynchronous=True)
+        hip.call("inv_hip_timer_stop", ctypes.byref(ms))
+        per.append(ms.value)
+    p10, p50, p90 = (float(v) for v in np.percentile(per, [10, 50, 90]))
     flops = 2.0 * M * N * K
     res = {"name": name, "M": M, "K": K, "N": N, "wall_ms": wall_ms, "kernel_ms": gpu_ms,
            "tflops_wall": flops / (wall_ms * 1e-3) / 1e12, "tflops_kernel": flops / (gpu_ms * 1e-3) / 1e12,
            "bytes": algorithmic_bytes(M, K, N, has_bias, xdt, ydt)}
     res["gbs_kernel"] = res["bytes"] / (gpu_ms * 1e-3) / 1e9
+    res["launch_ms_p10_p50_p90"] = [round(p10, 5), round(p50, 5), round(p90, 5)]
+    if host_path:
+        # The reference's own calling convention: fp32 X and Y in host memory,
+        # copied over PCIe on every call (pinned bounce buffers), X rounded on
+        # the device.  Reported beside the device-resident rate, never as it.
+        Xh = np.ascontiguousarray(X if xdt == "f32" else bf16_bits_to_f32(Xin))
+        q.linear(Xh, w, epilogue=epi)
+        reps, th = 0, time.perf_counter()
+        while reps < 3 or time.perf_counter() - th < 1.0:
+            q.linear(Xh, w, epilogue=epi)
+            reps += 1
+        host_ms = (time.perf_counter() - th) * 1e3 / reps
+        res["host_fp32_io_ms"] = host_ms
+        res["host_fp32_io_tflops"] = flops / (host_ms * 1e-3) / 1e12
     if check:
         # Spot parity on a few rows with numpy float64 (independent of the oracle).
         Y = yd.to_host()
@@ -156,6 +178,17 @@ def cpu_baseline(name):
             if dt2 >= 3.0:
                 break
         out["reference_sgemm2_tflops"] = reps2 * 2.0 * M * N * K / dt2 / 1e12
+    # numpy's bundled OpenBLAS sgemm: the library family the reference binds by
+    # default on Linux (its own libopenblas is not installed here).
+    A @ B.T
+    reps3, t = 0, time.perf_counter()
+    while True:
+        A @ B.T
+        reps3 += 1
+        dt3 = time.perf_counter() - t
+        if dt3 >= 2.0:
+            break
+    out["numpy_openblas_sgemm_tflops"] = reps3 * 2.0 * M * N * K / dt3 / 1e12
     try:
         out["cpu_model"] = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if "model name" in l)
     except Exception:
@@ -293,7 +326,7 @@ def main():
     if args.profile_run:
         return profile_run(args)
 
-    res = run_workload(args.workload, args.steps, args.warmup)
+    res = run_workload(args.workload, args.steps, args.warmup, host_path=True)
     log(f"[bench] {json.dumps(res)}")
     if args.all:
         for name in WORKLOADS:
@@ -330,6 +363,8 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic},
         "parity_normwise_sampled_rows": res.get("parity_normwise_sampled_rows"),
+        "launch_ms_p10_p50_p90": res["launch_ms_p10_p50_p90"],
+        "host_fp32_io_tflops": round(res["host_fp32_io_tflops"], 2),
         "device": info["name"],
     }
     if not args.no_cpu_baseline:

@@ -280,3 +280,7 @@ def test_checks_catch_planted_mistakes():
     Xs = X.copy()
     Xs[:, 3] *= -1.0  # a sign error in one column of K
     assert oracle.normwise_err(oracle.linear_bf16w(Xs, W, b), good) > 1e-3
+    Xo = np.ascontiguousarray(np.roll(X, 1, axis=1))  # k index off by one
+    assert oracle.normwise_err(oracle.linear_bf16w(Xo, W, b), good) > 1e-2
+    Wr = np.ascontiguousarray(np.roll(W, 1, axis=0))  # output row n off by one
+    assert oracle.normwise_err(oracle.linear_bf16w(X, Wr, b), good) > 1e-2
