@@ -1,12 +1,18 @@
 #!/usr/bin/env python3
 """Benchmark: dense bf16 linear layer on one MI355X through libinvision_hip.so.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload c2] [--all] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--warmup-seconds S] [--gpus 1] [--workload c2] [--all]
+                    [--no-cpu-baseline]
 
 A step is one Y = X . W^T + bias over the workload's full shape, with X, W,
 bias and Y resident in HBM (device pointers through the C ABI).  The default
 workload is the FLUX2-Klein-4B fused QKV projection, M x K x N = 4608 x 3072 x
 9216, bf16 X and W, fp32 bias and output, fp32 accumulation.
+
+Warm-up runs at least W steps and at least S seconds of back-to-back steps
+(default 1.5 s): the GPU's clock needs on the order of a second of sustained
+load to reach its steady state, and a short warm-up times the ramp instead of
+the kernel.  The line reports the warm-up steps actually run.
 
 Prints ONE JSON line on stdout.  `roofline` uses the dense bf16 MFMA peak;
 `achieved` is 2*M*N*K per launch over the average launch time measured with
@@ -69,7 +75,7 @@ def algorithmic_bytes(M, K, N, bias, xdt, ydt):
     return M * K * xs + N * K * 2 + M * N * ys + (4 * N if bias else 0)
 
 
-def run_workload(name, steps, warmup, check=True, host_path=False):
+def run_workload(name, steps, warmup, check=True, host_path=False, warmup_seconds=0.0):
     from invision_amd import hip
     from invision_amd import quicknn_hip as q
     from invision_amd.bf16 import as_bf16_bits, bf16_bits_to_f32
@@ -81,9 +87,12 @@ def run_workload(name, steps, warmup, check=True, host_path=False):
     w = q.Weight(W, b if has_bias else None)
     xd = q.DeviceArray.from_host(Xin, xdt)
     yd = q.DeviceArray((M, N), ydt)
-    for _ in range(warmup):
-        q.linear_device(xd, w, yd, M, epilogue=epi, asynchronous=True)
-    hip.call("inv_hip_synchronize")
+    warm_steps, tw = 0, time.perf_counter()
+    while warm_steps < warmup or time.perf_counter() - tw < warmup_seconds:
+        for _ in range(25):
+            q.linear_device(xd, w, yd, M, epilogue=epi, asynchronous=True)
+        warm_steps += 25
+        hip.call("inv_hip_synchronize")
     # Timed region: host wall clock bracketed by synchronizations, and HIP
     # events on the library stream around the same launches.
     t0 = time.perf_counter()
@@ -106,7 +115,7 @@ def run_workload(name, steps, warmup, check=True, host_path=False):
         per.append(ms.value)
     p10, p50, p90 = (float(v) for v in np.percentile(per, [10, 50, 90]))
     flops = 2.0 * M * N * K
-    res = {"name": name, "M": M, "K": K, "N": N, "wall_ms": wall_ms, "kernel_ms": gpu_ms,
+    res = {"name": name, "M": M, "K": K, "N": N, "warmup_steps": warm_steps, "wall_ms": wall_ms, "kernel_ms": gpu_ms,
            "tflops_wall": flops / (wall_ms * 1e-3) / 1e12, "tflops_kernel": flops / (gpu_ms * 1e-3) / 1e12,
            "bytes": algorithmic_bytes(M, K, N, has_bias, xdt, ydt)}
     res["gbs_kernel"] = res["bytes"] / (gpu_ms * 1e-3) / 1e9
@@ -210,7 +219,7 @@ def profile_run(args):
     a.free()
     b.free()
     log(f"[profile] copy calibration: 5 x copy_words16 of {n} bytes")
-    res = run_workload(args.workload, args.steps, args.warmup, check=False)
+    res = run_workload(args.workload, args.steps, args.warmup, check=False, warmup_seconds=args.warmup_seconds)
     log(f"[profile] {json.dumps(res)}")
     print(json.dumps({"profile_run": args.workload, "copy_bytes": n, **res}), flush=True)
     q.shutdown()
@@ -223,15 +232,15 @@ def profile_commands(workload, trace_dir, fetch_dir, write_dir):
     run = f"python3 {bench} --profile-run --workload {workload}"
     return {
         "trace": f"cd /tmp && export TMPDIR=/tmp && rocprofv3 --kernel-trace --stats -d {trace_dir} -o {workload} "
-                 f"--output-format csv -- {run} --steps 20 --warmup 5",
+                 f"--output-format csv -- {run} --steps 50 --warmup 5",
         "fetch": f"cd /tmp && export TMPDIR=/tmp && timeout -s KILL 60 rocprofv3 --pmc FETCH_SIZE -d {fetch_dir} "
-                 f"-o {workload} --output-format csv -- {run} --steps 5 --warmup 1",
+                 f"-o {workload} --output-format csv -- {run} --steps 5 --warmup 1 --warmup-seconds 0",
         "write": f"cd /tmp && export TMPDIR=/tmp && timeout -s KILL 60 rocprofv3 --pmc WRITE_SIZE -d {write_dir} "
-                 f"-o {workload} --output-format csv -- {run} --steps 5 --warmup 1",
+                 f"-o {workload} --output-format csv -- {run} --steps 5 --warmup 1 --warmup-seconds 0",
     }
 
 
-def summarize_profile(workload, trace_dir, fetch_dir, write_dir, kernel="gemm_nt_bf16_kernel"):
+def summarize_profile(workload, trace_dir, fetch_dir, write_dir, kernel="gemm_nt_bf16_kernel", steps=50):
     """Turn the three rocprofv3 runs of profile_commands() into profiles/gemm_<workload>_<MxKxN>.md and
     profiles/gemm_<workload>_traffic.json (HBM bytes per launch, read by the bench line's roofline).
 
@@ -266,7 +275,14 @@ def summarize_profile(workload, trace_dir, fetch_dir, write_dir, kernel="gemm_nt
     g_fetch = statistics.median(fe[gk]) * 1024 * f_scale
     g_write = statistics.median(wr[gk]) * 1024 * w_scale
     srow = next(r for r in stats if kernel in r["Name"])
-    avg_ns = float(srow["AverageNs"])
+    # Steady state: the timed launches of run_workload, i.e. the `steps` GEMM
+    # dispatches before its final 30 isolated ones (the warm-up before them
+    # includes the clock ramp, which the stats table averages in).
+    trace = [r for r in csv.DictReader(open(find(trace_dir, "kernel_trace.csv"))) if kernel in r["Kernel_Name"]]
+    trace.sort(key=lambda r: int(r["Start_Timestamp"]))
+    durs = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in trace]
+    timed = durs[-(steps + 30):-30] if len(durs) > steps + 30 else durs
+    avg_ns = float(sum(timed)) / len(timed)
     cmds = profile_commands(workload, trace_dir, fetch_dir, write_dir)
     tfl = flops / avg_ns / 1e3
     lines = [f"# {workload}: {desc}, Y[{M}x{N}] = X[{M}x{K}] . W[{N}x{K}]^T (rocprofv3)", "",
@@ -275,8 +291,9 @@ def summarize_profile(workload, trace_dir, fetch_dir, write_dir, kernel="gemm_nt
     for r in stats:
         lines.append(f"| `{r['Name'][:110]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
                      f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} |")
-    lines += ["", f"GEMM average {avg_ns / 1e3:.1f} us -> {tfl:.1f} TFLOP/s ({tfl / PEAK_BF16_TFLOPS * 100:.1f}% "
-                  f"of the {PEAK_BF16_TFLOPS} TFLOP/s bf16 dense MFMA peak).", "",
+    lines += ["", f"GEMM average over the {len(timed)} timed launches (after the warm-up): {avg_ns / 1e3:.1f} us -> "
+                  f"{tfl:.1f} TFLOP/s ({tfl / PEAK_BF16_TFLOPS * 100:.1f}% of the {PEAK_BF16_TFLOPS} TFLOP/s bf16 "
+                  f"dense MFMA peak).  The table's averages include the warm-up launches.", "",
               "Counter passes (one counter per run):", "", "```", cmds["fetch"], cmds["write"], "```", "",
               "| Kernel | FETCH_SIZE (KiB, median) | WRITE_SIZE (KiB, median) |", "|---|---|---|",
               f"| copy_words16, 512 MiB read + 512 MiB written | {statistics.median(fe[copyk]):.0f} | "
@@ -303,8 +320,10 @@ def summarize_profile(workload, trace_dir, fetch_dir, write_dir, kernel="gemm_nt
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10, help="minimum warm-up steps")
+    ap.add_argument("--warmup-seconds", type=float, default=1.5,
+                    help="minimum seconds of back-to-back warm-up steps before timing")
     ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
     ap.add_argument("--all", action="store_true", help="also time every workload shape (stderr)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -326,12 +345,12 @@ def main():
     if args.profile_run:
         return profile_run(args)
 
-    res = run_workload(args.workload, args.steps, args.warmup, host_path=True)
+    res = run_workload(args.workload, args.steps, args.warmup, host_path=True, warmup_seconds=args.warmup_seconds)
     log(f"[bench] {json.dumps(res)}")
     if args.all:
         for name in WORKLOADS:
             if name != args.workload:
-                r = run_workload(name, max(5, args.steps // 2), 3)
+                r = run_workload(name, max(5, args.steps // 2), 3, warmup_seconds=min(args.warmup_seconds, 0.5))
                 log(f"[bench] {json.dumps(r)}")
 
     desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[args.workload]
@@ -349,7 +368,7 @@ def main():
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": res["warmup_steps"],
         "ms_per_step": round(res["wall_ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",

@@ -1,25 +1,31 @@
 // gemm_configs.hpp -- the instantiated GEMM tile configurations.
 //
-// INV_CFG_PARAMS_<id> = TN, TM, WN, WM, BK, NST: a TN x TM output tile (W rows
-// x X rows), WN x WM waves of 64 threads, BK-wide k-tiles, NST LDS stages.
+// INV_CFG_<id> is the configuration type:
+//  inv::TileCfg<TN, TM, WN, WM, BK, NST>: a TN x TM output tile (W rows x X
+//    rows), WN x WM waves of 64 threads, BK-wide k-tiles, NST-stage LDS ring
+//    filled by direct global->LDS copies;
+//  inv::RsCfg<TN, TM, WN, WM>: 64-wide k-tiles, two LDS buffers filled from
+//    two register stages of global prefetch.
 // Each configuration is compiled in its own translation unit
 // (gemm_instance.hip with -DINV_CFG_ID=<id>) and reached through
-// inv_gemm_launch_<id>.
+// inv_gemm_launch_<id>.  The types are defined in gemm_kernel.hpp.
 #pragma once
 
 #include <hip/hip_runtime.h>
 
-#define INV_CFG_PARAMS_0 256, 256, 2, 4, 32, 4  /* 8 waves of 128x64, 4-stage ring (128 KiB) */
-#define INV_CFG_PARAMS_1 256, 256, 2, 4, 32, 5  /* same, 5 stages (160 KiB) */
-#define INV_CFG_PARAMS_2 256, 128, 2, 2, 64, 3  /* 4 waves of 128x64 */
-#define INV_CFG_PARAMS_3 128, 128, 2, 2, 64, 4  /* 4 waves of 64x64 */
-#define INV_CFG_PARAMS_4 128, 64, 2, 2, 64, 4   /* 4 waves of 64x32 */
-#define INV_CFG_PARAMS_5 128, 32, 4, 1, 64, 4   /* 4 waves of 32x32: W streaming for M <= 32 */
-#define INV_CFG_PARAMS_6 256, 256, 4, 2, 32, 4  /* 8 waves of 64x128 */
-#define INV_CFG_PARAMS_7 256, 256, 2, 2, 32, 4  /* 4 waves of 128x128 */
+#define INV_CFG_0 inv::TileCfg<256, 256, 2, 4, 32, 4> /* 8 waves of 128x64, 4-stage ring (128 KiB) */
+#define INV_CFG_1 inv::TileCfg<256, 256, 2, 4, 32, 5> /* same, 5 stages (160 KiB) */
+#define INV_CFG_2 inv::TileCfg<256, 128, 2, 2, 64, 3> /* 4 waves of 128x64 */
+#define INV_CFG_3 inv::TileCfg<128, 128, 2, 2, 64, 4> /* 4 waves of 64x64 */
+#define INV_CFG_4 inv::TileCfg<128, 64, 2, 2, 64, 4> /* 4 waves of 64x32 */
+#define INV_CFG_5 inv::TileCfg<128, 32, 4, 1, 64, 4> /* 4 waves of 32x32: W streaming for M <= 32 */
+#define INV_CFG_6 inv::TileCfg<256, 256, 4, 2, 32, 4> /* 8 waves of 64x128 */
+#define INV_CFG_7 inv::TileCfg<256, 256, 2, 2, 32, 4> /* 4 waves of 128x128 */
 
-#define INV_GEMM_CONFIG_IDS(X) X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7)
-#define INV_GEMM_NUM_CONFIGS 8
+#define INV_CFG_8 inv::RsCfg<256, 256, 2, 2> /* 4 waves of 128x128, register-staged prefetch */
+
+#define INV_GEMM_CONFIG_IDS(X) X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
+#define INV_GEMM_NUM_CONFIGS 9
 
 namespace inv {
 struct GemmParams;

@@ -48,10 +48,9 @@ hipError_t launch_cfg(const inv::GemmParams &p, int epi, int out, int mode, hipS
 
 }  // namespace
 
-#define INV_DEFINE_LAUNCH_(id, params)                                                                      \
+#define INV_DEFINE_LAUNCH(id)                                                                               \
     hipError_t inv_gemm_launch_##id(const inv::GemmParams &p, int epi, int out, int mode, hipStream_t s) {   \
-        return launch_cfg<inv::TileCfg<params>>(p, epi, out, mode, s);                                      \
+        return launch_cfg<INV_CFG_##id>(p, epi, out, mode, s);                                               \
     }
-#define INV_DEFINE_LAUNCH(id) INV_DEFINE_LAUNCH_(id, INV_CFG_PARAMS_##id)
 #define INV_EXPAND_DEFINE(id) INV_DEFINE_LAUNCH(id)
 INV_EXPAND_DEFINE(INV_CFG_ID)

@@ -45,6 +45,7 @@ namespace inv {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) char lds_char_t;
 
 enum EpiKind { EPI_NONE = 0, EPI_SILU = 1, EPI_GELU = 2 };
@@ -117,6 +118,7 @@ __device__ __forceinline__ void grouped_tile(int L, int tiles_m, int tiles_n, in
 // BK-wide k-tiles, NST LDS stages.
 template <int TN_, int TM_, int WN_, int WM_, int BK_, int NST_>
 struct TileCfg {
+    static constexpr bool REG_STAGED = false;
     static constexpr int TN = TN_, TM = TM_, WN = WN_, WM = WM_, BK = BK_, NST = NST_;
     static constexpr int NWAVES = WN * WM;
     static constexpr int NTHREADS = NWAVES * 64;
@@ -142,6 +144,37 @@ struct TileCfg {
     static_assert((NTHREADS / SLOTS) % 16 == 0, "copy rows must advance in multiples of 16");
     static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
     static_assert(KSUB % 2 == 0, "register double-buffering alternates over an even substep count");
+};
+
+// Register-staged configuration: TN x TM tile, WN x WM waves, 64-wide k-tiles
+// in two LDS buffers filled by ds_write from two register stages of global
+// prefetch (see mainloop_rs).
+template <int TN_, int TM_, int WN_, int WM_>
+struct RsCfg {
+    static constexpr bool REG_STAGED = true;
+    static constexpr int TN = TN_, TM = TM_, WN = WN_, WM = WM_, BK = 64, NST = 2;
+    static constexpr int NWAVES = WN * WM;
+    static constexpr int NTHREADS = NWAVES * 64;
+    static constexpr int WTN = TN / WN;
+    static constexpr int WTM = TM / WM;
+    static constexpr int FN = WTN / 32;
+    static constexpr int FM = WTM / 32;
+    static constexpr int SLOTS = 8;
+    static constexpr int ROWB = 128;
+    static constexpr int KSUB = 4;
+    static constexpr int A_BYTES = TN * ROWB;
+    static constexpr int B_BYTES = TM * ROWB;
+    static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+    static constexpr int LDS_BYTES = 2 * STAGE_BYTES;
+    static constexpr int A_LOADS = TN * SLOTS / NTHREADS;
+    static constexpr int B_LOADS = TM * SLOTS / NTHREADS;
+    static constexpr int LOADS = A_LOADS + B_LOADS;
+    static constexpr int ACC_REGS = FN * FM * 16;
+    static_assert(TN % (WN * 32) == 0 && TM % (WM * 32) == 0, "wave tile must be a multiple of 32");
+    static_assert((TN * SLOTS) % NTHREADS == 0 && (TM * SLOTS) % NTHREADS == 0, "copies must divide evenly");
+    static_assert((NTHREADS / SLOTS) % 16 == 0, "copy rows must advance in multiples of 16");
+    static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
+    static_assert(2 * LOADS - 1 < 64, "vmcnt holds at most 63 outstanding loads");
 };
 
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -232,12 +265,32 @@ __device__ __forceinline__ void issue_copy(__amdgpu_buffer_rsrc_t rsw, __amdgpu_
 }
 
 // Position (in MFMA steps of a k-tile) after which copy i is issued: the
-// LOADS copies are spread evenly, so they never queue up in the texture unit
-// ahead of the MFMAs of the same wave.
+// The fragment read issued at step r of a substep, for the next substep: A
+// fragment i as i >= 0, B fragment j as -1 - j.  Reads go in the order the next
+// substep's MFMAs (i-major) first use them -- A0, B0 .. B(FM-1), A1 .. A(FN-1) --
+// so each has most of a substep of MFMAs to land before it is needed.
+#ifndef INV_READ_FIRST_USE
+#define INV_READ_FIRST_USE 1
+#endif
+template <class C>
+constexpr int frag_read(int r) {
+    if constexpr (!INV_READ_FIRST_USE) return r < C::FN ? r : -1 - (r - C::FN);
+    if (r == 0) return 0;
+    if (r <= C::FM) return -r;  // B fragment r - 1
+    return r - C::FM;
+}
+
+// The MFMA step after which copy i of a k-tile is issued.  Early issue (one
+// copy per MFMA from the first step) gives each load the full NST-2 k-tiles
+// to land; the spread form distributes them evenly over the k-tile.
+#ifndef INV_COPY_SPREAD
+#define INV_COPY_SPREAD 0
+#endif
 template <class C>
 constexpr int copy_step(int i) {
     constexpr int T = C::KSUB * C::FN * C::FM;
-    return ((2 * i + 1) * T) / (2 * C::LOADS);
+    if constexpr (INV_COPY_SPREAD) return ((2 * i + 1) * T) / (2 * C::LOADS);
+    return C::LOADS <= T ? i : (i * T) / C::LOADS;
 }
 #endif  // __HIP_DEVICE_COMPILE__
 
@@ -277,10 +330,12 @@ __device__ __forceinline__ float *unit_slot(const GemmParams &p, const UnitFix &
     }
 }
 
-// One work unit: output tile (tm, tn), k-tiles [kt_begin, kt_end).
-template <class C, int EPI, int OUT, int MODE>
-__device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int tm, int tn, int kt_begin, int kt_end,
-                                          const UnitFix &fix) {
+// The LDS-ring main loop: direct global->LDS copies into an NST-stage ring,
+// k-tiles [kt_begin, kt_end) accumulated into acc.
+template <class C>
+__device__ __forceinline__ void mainloop_ring(const GemmParams &p, lds_char_t *lds, __amdgpu_buffer_rsrc_t rsw,
+                                              __amdgpu_buffer_rsrc_t rsx, int kt_begin, int kt_end,
+                                              f32x16_t (&acc)[C::FN][C::FM]) {
     constexpr int BK = C::BK;
     constexpr int NST = C::NST;
     const int tid = threadIdx.x;
@@ -288,16 +343,6 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
     const int wave = tid >> 6;
     const int wn = wave / C::WM;
     const int wm = wave % C::WM;
-    const int m0 = tm * C::TM;
-    const int n0 = tn * C::TN;
-
-    // Buffer resources covering exactly the valid rows of this tile's panels.
-    const int rows_w = min(C::TN, p.N - n0);
-    const int rows_x = min(C::TM, p.M - m0);
-    const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.W + (int64_t)n0 * p.ldw), 0, (int)((int64_t)rows_w * p.ldw * 2), 0x00020000);
-    const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.X + (int64_t)m0 * p.ldx), 0, (int)((int64_t)rows_x * p.ldx * 2), 0x00020000);
 
     // Copy-side lane constants: position q = i*NTHREADS + tid of a tile is row
     // q / SLOTS, slot q % SLOTS, and holds chunk slot ^ key(row); the row
@@ -310,16 +355,6 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
     constexpr int ROWS_PER_LOAD = C::NTHREADS / C::SLOTS;
     const uint32_t a_step = (uint32_t)(ROWS_PER_LOAD * p.ldw * 2);
     const uint32_t b_step = (uint32_t)(ROWS_PER_LOAD * p.ldx * 2);
-
-    lds_char_t *lds = (lds_char_t *)smem;
-
-    f32x16_t acc[C::FN][C::FM];
-#pragma unroll
-    for (int i = 0; i < C::FN; ++i)
-#pragma unroll
-        for (int j = 0; j < C::FM; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     // Fragment-side lane constants: lane reads row (lane & 31) of each 32-row
     // block, logical chunk 2*kk + (lane >> 5), stored at slot chunk ^ key(row).
@@ -391,10 +426,13 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
                 constexpr int q = decltype(qc)::value;
                 constexpr int i = q / C::FM, j = q % C::FM;
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ca[i], cb[j], acc[i][j], 0, 0, 0);
-                if constexpr (q < C::FN)
-                    na[q] = *(const bf16x8_t *)(rs + a_frag + q * 32 * C::ROWB + rc);
-                else if constexpr (q < C::FN + C::FM)
-                    nb[q - C::FN] = *(const bf16x8_t *)(rs + b_frag + (q - C::FN) * 32 * C::ROWB + rc);
+                if constexpr (q < C::FN + C::FM) {
+                    constexpr int fr = frag_read<C>(q);
+                    if constexpr (fr >= 0)
+                        na[fr] = *(const bf16x8_t *)(rs + a_frag + fr * 32 * C::ROWB + rc);
+                    else
+                        nb[-1 - fr] = *(const bf16x8_t *)(rs + b_frag + (-1 - fr) * 32 * C::ROWB + rc);
+                }
                 // every copy whose slot is this step (several when LOADS exceeds the MFMA count)
                 static_for<C::LOADS>([&](auto cc) {
                     constexpr int ci = decltype(cc)::value;
@@ -405,11 +443,11 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
             });
             // reads left over when a substep has more fragments than MFMAs
             static_for<(C::FN + C::FM > C::FN * C::FM) ? C::FN + C::FM - C::FN * C::FM : 0>([&](auto rc2) {
-                constexpr int q = C::FN * C::FM + decltype(rc2)::value;
-                if constexpr (q < C::FN)
-                    na[q] = *(const bf16x8_t *)(rs + a_frag + q * 32 * C::ROWB + rc);
+                constexpr int fr = frag_read<C>(C::FN * C::FM + decltype(rc2)::value);
+                if constexpr (fr >= 0)
+                    na[fr] = *(const bf16x8_t *)(rs + a_frag + fr * 32 * C::ROWB + rc);
                 else
-                    nb[q - C::FN] = *(const bf16x8_t *)(rs + b_frag + (q - C::FN) * 32 * C::ROWB + rc);
+                    nb[-1 - fr] = *(const bf16x8_t *)(rs + b_frag + (-1 - fr) * 32 * C::ROWB + rc);
             });
         });
         stage = next_stage;
@@ -417,6 +455,196 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
     // The copies of the k-tiles past the end still write LDS; let them land
     // before the ring is reused or the workgroup retires.
     wait_vmcnt<0>();
+}
+
+// The register-staged main loop (RsCfg): 64-wide k-tiles, two LDS buffers.
+// K-tile t (counted from kt_begin) is loaded into register stage t % 2 during
+// iteration t-2, written to LDS buffer t % 2 during iteration t-1 and
+// multiplied in iteration t, so each global load has two k-tiles of MFMA time
+// to land and each wave's loads cover whole 128-byte lines (8 lanes per row).
+// Per iteration, for every copy chunk c: wait until chunk c of tile t+1 has
+// landed (31 younger loads may be outstanding), ds_write it, and reuse its
+// registers for chunk c of tile t+3.  One barrier per iteration, early in the
+// last substep: it publishes tile t+1's LDS buffer and retires every read of
+// tile t's, so the next iteration may overwrite it.
+template <class C>
+__device__ __forceinline__ void mainloop_rs(const GemmParams &p, lds_char_t *lds, __amdgpu_buffer_rsrc_t rsw,
+                                            __amdgpu_buffer_rsrc_t rsx, int kt_begin, int kt_end,
+                                            f32x16_t (&acc)[C::FN][C::FM]) {
+    typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+    constexpr int BK = C::BK, ROWB = C::ROWB, SLOTS = C::SLOTS;
+    constexpr int AL = C::A_LOADS, L = C::LOADS;
+    constexpr int RPL = C::NTHREADS / SLOTS;  // rows covered by one copy chunk
+    constexpr int T = C::FN * C::FM;         // MFMAs per 16-wide substep
+    constexpr int NR = C::FN + C::FM;        // fragment reads per substep
+    constexpr int BAR = 1;                   // MFMA step of the last substep after which the barrier sits
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wn = wave / C::WM;
+    const int wm = wave % C::WM;
+
+    // Copy side: lane reads global chunk ld_chunk (k offset 8 * ld_chunk) of
+    // rows ld_row + RPL*i and stores it at slot ld_chunk ^ key(row); the key
+    // depends on the row mod 16 only, so it is the same for every i.
+    const int ld_row = tid / SLOTS;
+    const int ld_chunk = tid % SLOTS;
+    const int wr_off = ld_row * ROWB + ((ld_chunk ^ slot_key<SLOTS>(ld_row)) * 16);
+    const uint32_t a_base = (uint32_t)(ld_row * p.ldw * 2 + ld_chunk * 16);
+    const uint32_t b_base = (uint32_t)(ld_row * p.ldx * 2 + ld_chunk * 16);
+    const uint32_t a_step = (uint32_t)(RPL * p.ldw * 2);
+    const uint32_t b_step = (uint32_t)(RPL * p.ldx * 2);
+
+    // Fragment side (as in the ring loop).
+    const int frow = lane & 31;
+    const int fh = lane >> 5;
+    const int fkey = slot_key<SLOTS>(frow);
+    const int a_frag = (wn * C::WTN + frow) * ROWB;
+    const int b_frag = C::A_BYTES + (wm * C::WTM + frow) * ROWB;
+    int coff[C::KSUB];
+#pragma unroll
+    for (int kk = 0; kk < C::KSUB; ++kk) coff[kk] = ((2 * kk + fh) ^ fkey) * 16;
+
+    const int wseg = p.w_seg_k / BK;
+    int load_kt = kt_begin;
+    int load_ktw = wseg ? kt_begin % wseg : kt_begin;
+    // Offsets of the next k-tile to load (out of range, i.e. zeros, past kt_end or K).
+    auto next_kadd = [&](uint32_t &ka, uint32_t &kb) {
+        const bool in = load_kt < kt_end;
+        ka = k_byte_offset<BK>(in && load_ktw * BK + ld_chunk * 8 < p.Kw, load_ktw);
+        kb = k_byte_offset<BK>(in && load_kt * BK + ld_chunk * 8 < p.K, load_kt);
+        ++load_kt;
+        load_ktw = (wseg && load_ktw + 1 == wseg) ? 0 : load_ktw + 1;
+    };
+    auto gload = [&](int cidx, uint32_t ka, uint32_t kb) -> u32x4_t {
+        if (cidx < AL)
+            return __builtin_amdgcn_raw_buffer_load_b128(rsw, a_base + cidx * a_step + ka, 0, 0);
+        return __builtin_amdgcn_raw_buffer_load_b128(rsx, b_base + (cidx - AL) * b_step + kb, 0, 0);
+    };
+    auto lds_chunk = [&](lds_char_t *buf, int cidx) -> u32x4_t * {
+        return (u32x4_t *)(buf + (cidx < AL ? 0 : C::A_BYTES) + wr_off + (cidx % AL) * RPL * ROWB);
+    };
+
+    u32x4_t R0[L], R1[L];
+    lds_char_t *buf0 = lds;
+    lds_char_t *buf1 = lds + C::STAGE_BYTES;
+
+    // Prologue: tiles 0 and 1 into R0 and R1, tile 0 to LDS buffer 0, tile 2 into R0.
+    {
+        uint32_t ka, kb;
+        next_kadd(ka, kb);
+#pragma unroll
+        for (int c = 0; c < L; ++c) R0[c] = gload(c, ka, kb);
+        next_kadd(ka, kb);
+#pragma unroll
+        for (int c = 0; c < L; ++c) R1[c] = gload(c, ka, kb);
+        next_kadd(ka, kb);
+#pragma unroll
+        for (int c = 0; c < L; ++c) {
+            *lds_chunk(buf0, c) = R0[c];
+            R0[c] = gload(c, ka, kb);
+        }
+    }
+    __syncthreads();
+
+    bf16x8_t fa0[C::FN], fb0[C::FM], fa1[C::FN], fb1[C::FM];
+    load_frags<C>(buf0, a_frag, b_frag, coff[0], fa0, fb0);
+
+    // One iteration: multiply the tile in `cur` while moving register stage R
+    // (tile t+1) into `nxt` and refilling R with tile t+3.
+    auto iteration = [&](const lds_char_t *cur, lds_char_t *nxt, u32x4_t(&R)[L]) {
+        uint32_t ka, kb;
+        next_kadd(ka, kb);
+        static_for<C::KSUB>([&](auto ksc) {
+            constexpr int ks = decltype(ksc)::value;
+            bf16x8_t(&ca)[C::FN] = (ks % 2 == 0) ? fa0 : fa1;
+            bf16x8_t(&cb)[C::FM] = (ks % 2 == 0) ? fb0 : fb1;
+            bf16x8_t(&na)[C::FN] = (ks % 2 == 0) ? fa1 : fa0;
+            bf16x8_t(&nb)[C::FM] = (ks % 2 == 0) ? fb1 : fb0;
+            const lds_char_t *rs = (ks + 1 < C::KSUB) ? cur : nxt;
+            const int rc = coff[(ks + 1) % C::KSUB];
+            static_for<T>([&](auto qc) {
+                constexpr int q = decltype(qc)::value;
+                constexpr int i = q / C::FM, j = q % C::FM;
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ca[i], cb[j], acc[i][j], 0, 0, 0);
+                if constexpr (ks == C::KSUB - 1 && q == BAR) __syncthreads();
+                // fragment reads for the next substep
+                static_for<NR>([&](auto rc2) {
+                    constexpr int r = decltype(rc2)::value;
+                    constexpr int at = (ks == C::KSUB - 1) ? BAR + 1 + (r * (T - BAR - 1)) / NR : (r * T) / NR;
+                    if constexpr (at == q) {
+                        constexpr int fr = frag_read<C>(r);
+                        if constexpr (fr >= 0)
+                            na[fr] = *(const bf16x8_t *)(rs + a_frag + fr * 32 * ROWB + rc);
+                        else
+                            nb[-1 - fr] = *(const bf16x8_t *)(rs + b_frag + (-1 - fr) * 32 * ROWB + rc);
+                    }
+                });
+                // copy chunks: ds_write tile t+1, reload with tile t+3
+                if constexpr (ks < C::KSUB - 1) {
+                    static_for<L>([&](auto cc) {
+                        constexpr int cidx = decltype(cc)::value;
+                        constexpr int at = ((2 * cidx + 1) * (C::KSUB - 1) * T) / (2 * L);
+                        if constexpr (at == ks * T + q) {
+                            wait_vmcnt<2 * L - 1>();
+                            *lds_chunk(nxt, cidx) = R[cidx];
+                            R[cidx] = gload(cidx, ka, kb);
+                        }
+                    });
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        });
+    };
+
+    const int n = kt_end - kt_begin;
+    int t = 0;
+    for (; t + 1 < n; t += 2) {
+        iteration(buf0, buf1, R1);
+        iteration(buf1, buf0, R0);
+    }
+    if (t < n) iteration(buf0, buf1, R1);
+    wait_vmcnt<0>();
+}
+
+// One work unit: output tile (tm, tn), k-tiles [kt_begin, kt_end).
+template <class C, int EPI, int OUT, int MODE>
+__device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int tm, int tn, int kt_begin, int kt_end,
+                                          const UnitFix &fix) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wn = wave / C::WM;
+    const int wm = wave % C::WM;
+    const int m0 = tm * C::TM;
+    const int n0 = tn * C::TN;
+
+    // Buffer resources covering exactly the valid rows of this tile's panels.
+    const int rows_w = min(C::TN, p.N - n0);
+    const int rows_x = min(C::TM, p.M - m0);
+    const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.W + (int64_t)n0 * p.ldw), 0, (int)((int64_t)rows_w * p.ldw * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.X + (int64_t)m0 * p.ldx), 0, (int)((int64_t)rows_x * p.ldx * 2), 0x00020000);
+
+    lds_char_t *lds = (lds_char_t *)smem;
+
+    f32x16_t acc[C::FN][C::FM];
+#pragma unroll
+    for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FM; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    if constexpr (C::REG_STAGED)
+        mainloop_rs<C>(p, lds, rsw, rsx, kt_begin, kt_end, acc);
+    else
+        mainloop_ring<C>(p, lds, rsw, rsx, kt_begin, kt_end, acc);
+    // Accumulator layout: lane holds D[n = 8g + 4*fh + e][m = frow] of each 32x32 block.
+    const int frow = lane & 31;
+    const int fh = lane >> 5;
+
 
     if constexpr (MODE != GRID_TILES) {
         if (fix.nseg > 1) {
@@ -481,26 +709,37 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
         }
     }
 
-    // Epilogue: lane holds D[n = 8g + 4h + e][m = lane & 31] of each 32x32 block.
+    // Epilogue: lane holds D[n = 8g + 4*fh + e][m = frow] of each 32x32 block.
+    // For each (i, j) a lane's four g stores cover 32 bytes of row m and the
+    // two lane halves together the row's whole 128-byte segment; they are
+    // issued back to back so the L2 merges them into full lines.
 #pragma unroll
     for (int i = 0; i < C::FN; ++i) {
+        const int nb = n0 + wn * C::WTN + i * 32 + 4 * fh;
+        float bv[4][4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const int n = n0 + wn * C::WTN + i * 32 + 8 * g + 4 * fh;
-            float bv[4] = {0.f, 0.f, 0.f, 0.f};
+            const int n = nb + 8 * g;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bv[g][e] = 0.f;
             if (p.has_bias) {
                 if (n + 3 < p.N) {
                     f32x4_t t = *(const f32x4_t *)(p.bias + n);  // bias is 16-byte aligned, n % 4 == 0
-                    bv[0] = t[0]; bv[1] = t[1]; bv[2] = t[2]; bv[3] = t[3];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) bv[g][e] = t[e];
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) bv[e] = (n + e < p.N) ? p.bias[n + e] : 0.f;
+                    for (int e = 0; e < 4; ++e) bv[g][e] = (n + e < p.N) ? p.bias[n + e] : 0.f;
                 }
             }
+        }
 #pragma unroll
-            for (int j = 0; j < C::FM; ++j) {
-                const int m = m0 + wm * C::WTM + j * 32 + frow;
-                if (m >= p.M) continue;
+        for (int j = 0; j < C::FM; ++j) {
+            const int m = m0 + wm * C::WTM + j * 32 + frow;
+            if (m >= p.M) continue;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int n = nb + 8 * g;
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[e] = p.alpha * acc[i][j][4 * g + e];
@@ -510,11 +749,11 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
                         if (n + e < p.N) v[e] += p.beta * p.Cin[(int64_t)m * p.ldc + n + e];
                 }
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = epilogue_op<EPI>(v[e] + bv[e]);
+                for (int e = 0; e < 4; ++e) v[e] = epilogue_op<EPI>(v[e] + bv[g][e]);
                 if constexpr (OUT == OUT_F32) {
                     float *y = (float *)p.Y + (int64_t)m * p.ldy + n;
                     if (p.vec_store && n + 3 < p.N) {
-                        *(f32x4_t *)y = f32x4_t{v[0], v[1], v[2], v[3]};
+                        *reinterpret_cast<f32x4_t *>(y) = f32x4_t{v[0], v[1], v[2], v[3]};
                     } else {
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
@@ -523,10 +762,10 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
                 } else {
                     uint16_t *y = (uint16_t *)p.Y + (int64_t)m * p.ldy + n;
                     if (p.vec_store && n + 3 < p.N) {
-                        uint2 packed;
-                        packed.x = (uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16);
-                        packed.y = (uint32_t)f32_to_bf16_rne(v[2]) | ((uint32_t)f32_to_bf16_rne(v[3]) << 16);
-                        *(uint2 *)y = packed;
+                        u32x2_t packed;
+                        packed[0] = (uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16);
+                        packed[1] = (uint32_t)f32_to_bf16_rne(v[2]) | ((uint32_t)f32_to_bf16_rne(v[3]) << 16);
+                        *reinterpret_cast<u32x2_t *>(y) = packed;
                     } else {
 #pragma unroll
                         for (int e = 0; e < 4; ++e)

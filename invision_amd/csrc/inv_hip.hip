@@ -230,13 +230,12 @@ struct TileChoice {
 // Instantiated tile configurations (gemm_configs.hpp).
 struct CfgMeta {
     int tn, tm, threads, acc_regs, bk, lds;
+    bool reg_staged;  // RsCfg: no stream-K / split-K (its fixup path spills registers)
     hipError_t (*launch)(const inv::GemmParams &, int, int, int, hipStream_t);
 };
-#define INV_META(id)                                                                                 \
-    {inv::TileCfg<INV_CFG_PARAMS_##id>::TN, inv::TileCfg<INV_CFG_PARAMS_##id>::TM,                  \
-     inv::TileCfg<INV_CFG_PARAMS_##id>::NTHREADS, inv::TileCfg<INV_CFG_PARAMS_##id>::ACC_REGS,      \
-     inv::TileCfg<INV_CFG_PARAMS_##id>::BK, inv::TileCfg<INV_CFG_PARAMS_##id>::LDS_BYTES,           \
-     &inv_gemm_launch_##id},
+#define INV_META(id)                                                                        \
+    {INV_CFG_##id::TN,       INV_CFG_##id::TM,  INV_CFG_##id::NTHREADS, INV_CFG_##id::ACC_REGS, \
+     INV_CFG_##id::BK,       INV_CFG_##id::LDS_BYTES, INV_CFG_##id::REG_STAGED, &inv_gemm_launch_##id},
 const CfgMeta kCfg[INV_GEMM_NUM_CONFIGS] = {INV_GEMM_CONFIG_IDS(INV_META)};
 #undef INV_META
 constexpr int kNumCfg = INV_GEMM_NUM_CONFIGS;
@@ -263,9 +262,10 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
         c.cfg = 4;
     } else {
         // Among the larger tiles, the one with the least MFMA-feeding cost:
-        // the 256x256 tile loads and reads the fewest bytes per MFMA; smaller
-        // tiles only when the problem cannot fill the chip with it.
-        const int cand[3] = {0, 2, 3};
+        // the 256x256 register-staged tile loads and reads the fewest bytes
+        // per MFMA; smaller tiles only when the problem cannot fill the chip
+        // with it.
+        const int cand[3] = {8, 2, 3};
         const double eff[3] = {1.0, 0.8, 0.65};
         double best = -1.0;
         for (int q = 0; q < 3; ++q) {
@@ -290,7 +290,7 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
     // Share of the slot-rounds left idle by one workgroup per tile.
     const int64_t rounds = (tiles + slots - 1) / slots;
     const double idle = 1.0 - (double)tiles / (double)(rounds * slots);
-    if (m.tm >= 128 && ((tiles * 2 <= slots && KT >= 32) || (idle >= 0.25 && KT >= 128))) {
+    if (!m.reg_staged && m.tm >= 128 && ((tiles * 2 <= slots && KT >= 32) || (idle >= 0.25 && KT >= 128))) {
         // A persistent stream-K grid spreads the k-iterations over all slots
         // (at least 8 k-tiles per workgroup so the pipeline fill stays cheap).
         // It pays when the last round would leave many slots idle and K is

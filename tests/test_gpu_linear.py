@@ -165,7 +165,11 @@ GRID_MODES = {  # INV_HIP_MODE / INV_HIP_KSPLIT / INV_HIP_SK_GRID
 }
 
 
-@pytest.mark.parametrize("cfg", [0, 1, 2, 3, 4, 5, 6, 7])
+ALL_CFGS = list(range(9))  # INV_GEMM_NUM_CONFIGS in invision_amd/csrc/gemm_configs.hpp
+REG_STAGED_CFGS = [8]
+
+
+@pytest.mark.parametrize("cfg", ALL_CFGS)
 @pytest.mark.parametrize("grid", sorted(GRID_MODES))
 def test_every_tile_shape_and_grid_mode(hiplib, monkeypatch, cfg, grid):
     monkeypatch.setenv("INV_HIP_TILE_CFG", str(cfg))
@@ -178,6 +182,20 @@ def test_every_tile_shape_and_grid_mode(hiplib, monkeypatch, cfg, grid):
         y2 = q.linear(X, w, epilogue="silu")
     check(y, X, W, b, "silu")
     np.testing.assert_array_equal(y, y2)  # deterministic, counters reset
+
+
+@pytest.mark.parametrize("cfg", REG_STAGED_CFGS)
+@pytest.mark.parametrize("K", [8, 64, 128, 200, 576, 1000, 3072])
+def test_register_staged_k_tile_counts(hiplib, monkeypatch, cfg, K):
+    """One, two, odd, even and ragged numbers of 64-wide k-tiles (the main loop
+    runs two k-tiles per trip and a single one for an odd remainder)."""
+    monkeypatch.setenv("INV_HIP_TILE_CFG", str(cfg))
+    monkeypatch.setenv("INV_HIP_MODE", "0")
+    M, N = 300, 520
+    X, W, b = gen(16, M, K, N)
+    with q.Weight(W, b) as w:
+        y = q.linear(as_bf16_bits(X), w)
+    check(y, X, W, b)
 
 
 @pytest.mark.parametrize("M,K,N", [(4608, 3072, 9216), (512, 9728, 2560), (777, 1304, 1000)])
