@@ -4,8 +4,9 @@
 //  inv::TileCfg<TN, TM, WN, WM, BK, NST>: a TN x TM output tile (W rows x X
 //    rows), WN x WM waves of 64 threads, BK-wide k-tiles, NST-stage LDS ring
 //    filled by direct global->LDS copies;
-//  inv::RsCfg<TN, TM, WN, WM>: 64-wide k-tiles, two LDS buffers filled from
-//    two register stages of global prefetch.
+//  inv::RsCfg<TN, TM, WN, WM, NREG, PF>: 64-wide k-tiles, two LDS buffers
+//    filled from NREG register stages of global prefetch, MFMA fragments read
+//    PF 16-wide substeps ahead.
 // Each configuration is compiled in its own translation unit
 // (gemm_instance.hip with -DINV_CFG_ID=<id>) and reached through
 // inv_gemm_launch_<id>.  The types are defined in gemm_kernel.hpp.
@@ -22,10 +23,12 @@
 #define INV_CFG_6 inv::TileCfg<256, 256, 4, 2, 32, 4> /* 8 waves of 64x128 */
 #define INV_CFG_7 inv::TileCfg<256, 256, 2, 2, 32, 4> /* 4 waves of 128x128 */
 
-#define INV_CFG_8 inv::RsCfg<256, 256, 2, 2> /* 4 waves of 128x128, register-staged prefetch */
+#define INV_CFG_8 inv::RsCfg<256, 256, 2, 2, 2> /* 4 waves of 128x128, two register stages */
+#define INV_CFG_9 inv::RsCfg<256, 256, 2, 2, 1> /* same, one register stage */
+#define INV_CFG_10 inv::RsCfg<256, 256, 2, 2, 1, 2> /* one register stage, fragments two substeps ahead */
 
-#define INV_GEMM_CONFIG_IDS(X) X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
-#define INV_GEMM_NUM_CONFIGS 9
+#define INV_GEMM_CONFIG_IDS(X) X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10)
+#define INV_GEMM_NUM_CONFIGS 11
 
 namespace inv {
 struct GemmParams;

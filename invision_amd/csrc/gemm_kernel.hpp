@@ -76,6 +76,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     return (uint16_t)(u >> 16);
 }
 
+// Two fp32 values to packed bf16 (low half = a) with v_cvt_pk_bf16_f32:
+// round to nearest, ties to even -- bit-identical to f32_to_bf16_rne on every
+// bf16 value combined with the low halves 0x0000/0x7FFF/0x8000/0x8001/0xFFFF,
+// NaNs and denormals included (checked on gfx950).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+
 template <int EPI>
 __device__ __forceinline__ float epilogue_op(float v) {
     if constexpr (EPI == EPI_SILU) {
@@ -144,15 +154,17 @@ struct TileCfg {
     static_assert((NTHREADS / SLOTS) % 16 == 0, "copy rows must advance in multiples of 16");
     static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
     static_assert(KSUB % 2 == 0, "register double-buffering alternates over an even substep count");
+    static constexpr bool STAGED_EPI = NWAVES * 32 * (WTN + 4) * 4 <= LDS_BYTES;
 };
 
 // Register-staged configuration: TN x TM tile, WN x WM waves, 64-wide k-tiles
-// in two LDS buffers filled by ds_write from two register stages of global
-// prefetch (see mainloop_rs).
-template <int TN_, int TM_, int WN_, int WM_>
+// in two LDS buffers filled by ds_write from NREG (1 or 2) register stages of
+// global prefetch (see mainloop_rs); MFMA fragments are read PF substeps ahead.
+template <int TN_, int TM_, int WN_, int WM_, int NREG_ = 2, int PF_ = 1>
 struct RsCfg {
     static constexpr bool REG_STAGED = true;
-    static constexpr int TN = TN_, TM = TM_, WN = WN_, WM = WM_, BK = 64, NST = 2;
+    static constexpr int TN = TN_, TM = TM_, WN = WN_, WM = WM_, BK = 64, NST = 2, NREG = NREG_;
+    static constexpr int PF = PF_;  // fragment reads run PF 16-wide substeps ahead of the MFMAs
     static constexpr int NWAVES = WN * WM;
     static constexpr int NTHREADS = NWAVES * 64;
     static constexpr int WTN = TN / WN;
@@ -174,7 +186,10 @@ struct RsCfg {
     static_assert((TN * SLOTS) % NTHREADS == 0 && (TM * SLOTS) % NTHREADS == 0, "copies must divide evenly");
     static_assert((NTHREADS / SLOTS) % 16 == 0, "copy rows must advance in multiples of 16");
     static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
-    static_assert(2 * LOADS - 1 < 64, "vmcnt holds at most 63 outstanding loads");
+    static_assert(NREG == 1 || NREG == 2, "one or two register stages");
+    static_assert(PF == 1 || PF == 2, "fragment prefetch distance 1 or 2 substeps");
+    static constexpr bool STAGED_EPI = NWAVES * 32 * (WTN + 4) * 4 <= LDS_BYTES;
+    static_assert(NREG * LOADS - 1 < 64, "vmcnt holds at most 63 outstanding loads");
 };
 
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -458,15 +473,15 @@ __device__ __forceinline__ void mainloop_ring(const GemmParams &p, lds_char_t *l
 }
 
 // The register-staged main loop (RsCfg): 64-wide k-tiles, two LDS buffers.
-// K-tile t (counted from kt_begin) is loaded into register stage t % 2 during
-// iteration t-2, written to LDS buffer t % 2 during iteration t-1 and
-// multiplied in iteration t, so each global load has two k-tiles of MFMA time
-// to land and each wave's loads cover whole 128-byte lines (8 lanes per row).
-// Per iteration, for every copy chunk c: wait until chunk c of tile t+1 has
-// landed (31 younger loads may be outstanding), ds_write it, and reuse its
-// registers for chunk c of tile t+3.  One barrier per iteration, early in the
-// last substep: it publishes tile t+1's LDS buffer and retires every read of
-// tile t's, so the next iteration may overwrite it.
+// K-tile t (counted from kt_begin) is loaded into registers during iteration
+// t-1-NREG, written to LDS buffer t % 2 during iteration t-1 and multiplied in
+// iteration t, so each global load has NREG k-tiles of MFMA time to land; each
+// wave's loads cover whole 128-byte lines (8 lanes per row).  Per iteration,
+// for every copy chunk c: wait until chunk c of tile t+1 has landed
+// (NREG*LOADS-1 younger loads may be outstanding), ds_write it, and reuse its
+// registers for chunk c of tile t+1+NREG.  One barrier per iteration, early in
+// the last substep: it publishes tile t+1's LDS buffer and retires every read
+// of tile t's, so the next iteration may overwrite it.
 template <class C>
 __device__ __forceinline__ void mainloop_rs(const GemmParams &p, lds_char_t *lds, __amdgpu_buffer_rsrc_t rsw,
                                             __amdgpu_buffer_rsrc_t rsx, int kt_begin, int kt_end,
@@ -525,19 +540,22 @@ __device__ __forceinline__ void mainloop_rs(const GemmParams &p, lds_char_t *lds
         return (u32x4_t *)(buf + (cidx < AL ? 0 : C::A_BYTES) + wr_off + (cidx % AL) * RPL * ROWB);
     };
 
-    u32x4_t R0[L], R1[L];
+    u32x4_t R0[L], R1[C::NREG == 2 ? L : 1];
     lds_char_t *buf0 = lds;
     lds_char_t *buf1 = lds + C::STAGE_BYTES;
 
-    // Prologue: tiles 0 and 1 into R0 and R1, tile 0 to LDS buffer 0, tile 2 into R0.
+    // Prologue: tile 0 to LDS buffer 0; the next NREG tiles in registers
+    // (tile 1 in R1 and tile 2 in R0 with two stages, tile 1 in R0 with one).
     {
         uint32_t ka, kb;
         next_kadd(ka, kb);
 #pragma unroll
         for (int c = 0; c < L; ++c) R0[c] = gload(c, ka, kb);
-        next_kadd(ka, kb);
+        if constexpr (C::NREG == 2) {
+            next_kadd(ka, kb);
 #pragma unroll
-        for (int c = 0; c < L; ++c) R1[c] = gload(c, ka, kb);
+            for (int c = 0; c < L; ++c) R1[c] = gload(c, ka, kb);
+        }
         next_kadd(ka, kb);
 #pragma unroll
         for (int c = 0; c < L; ++c) {
@@ -547,46 +565,55 @@ __device__ __forceinline__ void mainloop_rs(const GemmParams &p, lds_char_t *lds
     }
     __syncthreads();
 
-    bf16x8_t fa0[C::FN], fb0[C::FM], fa1[C::FN], fb1[C::FM];
-    load_frags<C>(buf0, a_frag, b_frag, coff[0], fa0, fb0);
+    // Fragment buffers: the reads for substep s+PF are issued under the MFMAs
+    // of substep s (PF = 1: two buffers alternating; PF = 2: one per substep).
+    constexpr int PF = C::PF;
+    constexpr int NB = (PF == 1) ? 2 : C::KSUB;
+    bf16x8_t fa[NB][C::FN], fb[NB][C::FM];
+    static_for<PF>([&](auto sc) {
+        constexpr int s0 = decltype(sc)::value;
+        load_frags<C>(buf0, a_frag, b_frag, coff[s0], fa[s0], fb[s0]);
+    });
+    // The barrier precedes the first read of the next tile (substep KSUB-PF);
+    // the ds_writes of the next tile all come before it.
+    constexpr int BSUB = C::KSUB - PF;
 
     // One iteration: multiply the tile in `cur` while moving register stage R
-    // (tile t+1) into `nxt` and refilling R with tile t+3.
+    // (tile t+1) into `nxt` and refilling R with tile t+1+NREG.
     auto iteration = [&](const lds_char_t *cur, lds_char_t *nxt, u32x4_t(&R)[L]) {
         uint32_t ka, kb;
         next_kadd(ka, kb);
         static_for<C::KSUB>([&](auto ksc) {
             constexpr int ks = decltype(ksc)::value;
-            bf16x8_t(&ca)[C::FN] = (ks % 2 == 0) ? fa0 : fa1;
-            bf16x8_t(&cb)[C::FM] = (ks % 2 == 0) ? fb0 : fb1;
-            bf16x8_t(&na)[C::FN] = (ks % 2 == 0) ? fa1 : fa0;
-            bf16x8_t(&nb)[C::FM] = (ks % 2 == 0) ? fb1 : fb0;
-            const lds_char_t *rs = (ks + 1 < C::KSUB) ? cur : nxt;
-            const int rc = coff[(ks + 1) % C::KSUB];
+            constexpr int cb_i = ks % NB;               // buffer of this substep
+            constexpr int rd = ks + PF;                 // substep whose fragments are read now
+            constexpr int nb_i = rd % NB;
+            const lds_char_t *rs = (rd < C::KSUB) ? cur : nxt;
+            const int rc = coff[rd % C::KSUB];
             static_for<T>([&](auto qc) {
                 constexpr int q = decltype(qc)::value;
                 constexpr int i = q / C::FM, j = q % C::FM;
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ca[i], cb[j], acc[i][j], 0, 0, 0);
-                if constexpr (ks == C::KSUB - 1 && q == BAR) __syncthreads();
-                // fragment reads for the next substep
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cb_i][i], fb[cb_i][j], acc[i][j], 0, 0, 0);
+                if constexpr (ks == BSUB && q == BAR) __syncthreads();
+                // fragment reads for substep rd
                 static_for<NR>([&](auto rc2) {
                     constexpr int r = decltype(rc2)::value;
-                    constexpr int at = (ks == C::KSUB - 1) ? BAR + 1 + (r * (T - BAR - 1)) / NR : (r * T) / NR;
+                    constexpr int at = (ks == BSUB) ? BAR + 1 + (r * (T - BAR - 1)) / NR : (r * T) / NR;
                     if constexpr (at == q) {
                         constexpr int fr = frag_read<C>(r);
                         if constexpr (fr >= 0)
-                            na[fr] = *(const bf16x8_t *)(rs + a_frag + fr * 32 * ROWB + rc);
+                            fa[nb_i][fr] = *(const bf16x8_t *)(rs + a_frag + fr * 32 * ROWB + rc);
                         else
-                            nb[-1 - fr] = *(const bf16x8_t *)(rs + b_frag + (-1 - fr) * 32 * ROWB + rc);
+                            fb[nb_i][-1 - fr] = *(const bf16x8_t *)(rs + b_frag + (-1 - fr) * 32 * ROWB + rc);
                     }
                 });
-                // copy chunks: ds_write tile t+1, reload with tile t+3
-                if constexpr (ks < C::KSUB - 1) {
+                // copy chunks: ds_write tile t+1, reload the registers with tile t+1+NREG
+                if constexpr (ks < BSUB) {
                     static_for<L>([&](auto cc) {
                         constexpr int cidx = decltype(cc)::value;
-                        constexpr int at = ((2 * cidx + 1) * (C::KSUB - 1) * T) / (2 * L);
+                        constexpr int at = ((2 * cidx + 1) * BSUB * T) / (2 * L);
                         if constexpr (at == ks * T + q) {
-                            wait_vmcnt<2 * L - 1>();
+                            wait_vmcnt<C::NREG * L - 1>();
                             *lds_chunk(nxt, cidx) = R[cidx];
                             R[cidx] = gload(cidx, ka, kb);
                         }
@@ -598,13 +625,212 @@ __device__ __forceinline__ void mainloop_rs(const GemmParams &p, lds_char_t *lds
     };
 
     const int n = kt_end - kt_begin;
-    int t = 0;
-    for (; t + 1 < n; t += 2) {
-        iteration(buf0, buf1, R1);
-        iteration(buf1, buf0, R0);
+    if constexpr (C::NREG == 2) {
+        // The register stage alternates, so iterations go in pairs.
+        int t = 0;
+        for (; t + 1 < n; t += 2) {
+            iteration(buf0, buf1, R1);
+            iteration(buf1, buf0, R0);
+        }
+        if (t < n) iteration(buf0, buf1, R1);
+    } else {
+        lds_char_t *cur = buf0, *nxt = buf1;
+        for (int t = 0; t < n; ++t) {
+            iteration(cur, nxt, R0);
+            lds_char_t *tmp = cur;
+            cur = nxt;
+            nxt = tmp;
+        }
     }
-    if (t < n) iteration(buf0, buf1, R1);
     wait_vmcnt<0>();
+}
+
+// Epilogue through LDS.  The MFMA accumulator layout gives each lane 4
+// consecutive n of one row m, so direct stores write 32 bytes into each of 32
+// rows per instruction.  Instead, each wave writes one 32-row block of its
+// accumulators (times alpha) to its own LDS region, rows padded by 16 bytes
+// (conflict-free for the 16-lane phases of ds_write_b128), and reads them back
+// row-major: WTN/4 lanes per row, so every store covers whole row segments of
+// 4*WTN (fp32) or 2*WTN (bf16) bytes.  beta*C, bias and the activation are
+// applied on the row-major side, where their loads are contiguous too.
+// BETA is a template parameter so that the common beta == 0 path has no loads
+// among the stores: loads and stores share vmcnt, and a wait for a load that
+// may have been issued also waits for every store before it.
+// Requires the ring to be idle (a barrier first) and NWAVES*32*(WTN+4)*4 bytes.
+template <class C, int EPI, int OUT, bool BETA>
+__device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_t *lds,
+                                                  const f32x16_t (&acc)[C::FN][C::FM], int m0, int n0, int wn,
+                                                  int wm, int lane, int wave) {
+    typedef __attribute__((address_space(3))) float lds_float_t;
+    constexpr int SROW = C::WTN + 4;       // staged row pitch in floats
+    constexpr int LPR = C::WTN / 4;        // lanes per row on the read side
+    constexpr int RPI = 64 / LPR;          // rows per read instruction
+    const int frow = lane & 31;
+    const int fh = lane >> 5;
+    lds_float_t *st = (lds_float_t *)lds + wave * 32 * SROW;
+    const int col = (lane % LPR) * 4;
+    const int rsub = lane / LPR;
+    const int n = n0 + wn * C::WTN + col;
+    const bool nvec = p.vec_store && n + 3 < p.N;
+    float bv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (p.has_bias) {
+        if (n + 3 < p.N) {
+            const f32x4_t t = *(const f32x4_t *)(p.bias + n);  // bias is 16-byte aligned, n % 4 == 0
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bv[e] = t[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bv[e] = (n + e < p.N) ? p.bias[n + e] : 0.f;
+        }
+    }
+    // The bias has landed before the first store: a later wait for it would
+    // also wait for every store issued before it.
+    wait_vmcnt<0>();
+    __syncthreads();  // every wave has finished with the ring
+#pragma unroll
+    for (int j = 0; j < C::FM; ++j) {
+#pragma unroll
+        for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *(__attribute__((address_space(3))) f32x4_t *)(st + frow * SROW + i * 32 + 8 * g + 4 * fh) =
+                    f32x4_t{p.alpha * acc[i][j][4 * g], p.alpha * acc[i][j][4 * g + 1],
+                            p.alpha * acc[i][j][4 * g + 2], p.alpha * acc[i][j][4 * g + 3]};
+        // LDS operations of one wave execute in order: the reads below see the
+        // writes above, and the next block's writes follow these reads.  All
+        // reads (and C loads) of the block are issued before any store, so the
+        // stores are never behind a wait.
+        constexpr int NIT = 32 / RPI;
+        f32x4_t t[NIT];
+#pragma unroll
+        for (int it = 0; it < NIT; ++it)
+            t[it] = *(const __attribute__((address_space(3))) f32x4_t *)(st + (it * RPI + rsub) * SROW + col);
+        const int mrow = m0 + wm * C::WTM + j * 32 + rsub;  // row of it = 0; it adds RPI rows
+        if (nvec && mrow + (NIT - 1) * RPI < p.M) {
+            // every row of this lane in range, 16-byte aligned: no branches
+            if constexpr (BETA) {
+                f32x4_t cv[NIT];
+#pragma unroll
+                for (int it = 0; it < NIT; ++it)
+                    cv[it] = *(const f32x4_t *)(p.Cin + (int64_t)(mrow + it * RPI) * p.ldc + n);
+#pragma unroll
+                for (int it = 0; it < NIT; ++it) t[it] += p.beta * cv[it];
+            }
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = epilogue_op<EPI>(t[it][e] + bv[e]);
+                const int64_t off = (int64_t)(mrow + it * RPI) * p.ldy + n;
+                if constexpr (OUT == OUT_F32) {
+                    *reinterpret_cast<f32x4_t *>((float *)p.Y + off) = f32x4_t{v[0], v[1], v[2], v[3]};
+                } else {
+                    u32x2_t packed;
+                    packed[0] = pack_bf16x2(v[0], v[1]);
+                    packed[1] = pack_bf16x2(v[2], v[3]);
+                    *reinterpret_cast<u32x2_t *>((uint16_t *)p.Y + off) = packed;
+                }
+            }
+        } else {
+            // edge tiles and unaligned outputs: element-wise bounds
+            for (int it = 0; it < NIT; ++it) {
+                const int m = mrow + it * RPI;
+                if (m >= p.M) continue;
+                float v[4] = {t[it][0], t[it][1], t[it][2], t[it][3]};
+                if constexpr (BETA) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < p.N) v[e] += p.beta * p.Cin[(int64_t)m * p.ldc + n + e];
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = epilogue_op<EPI>(v[e] + bv[e]);
+                if constexpr (OUT == OUT_F32) {
+                    float *y = (float *)p.Y + (int64_t)m * p.ldy + n;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < p.N) y[e] = v[e];
+                } else {
+                    uint16_t *y = (uint16_t *)p.Y + (int64_t)m * p.ldy + n;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < p.N) y[e] = f32_to_bf16_rne(v[e]);
+                }
+            }
+        }
+    }
+}
+
+// Direct epilogue (configurations whose LDS cannot hold the staging area).
+// Lane holds D[n = 8g + 4*fh + e][m = frow] of each 32x32 block; for each (i, j)
+// a lane's four g stores cover 32 bytes of row m and the two lane halves the
+// row's whole 128-byte segment, issued back to back so the L2 merges them.
+template <class C, int EPI, int OUT, bool BETA>
+__device__ __forceinline__ void store_tile_direct(const GemmParams &p, const f32x16_t (&acc)[C::FN][C::FM], int m0,
+                                                  int n0, int wn, int wm, int lane) {
+    const int frow = lane & 31;
+    const int fh = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < C::FN; ++i) {
+        const int nb = n0 + wn * C::WTN + i * 32 + 4 * fh;
+        float bv[4][4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int n = nb + 8 * g;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bv[g][e] = 0.f;
+            if (p.has_bias) {
+                if (n + 3 < p.N) {
+                    f32x4_t t = *(const f32x4_t *)(p.bias + n);  // bias is 16-byte aligned, n % 4 == 0
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) bv[g][e] = t[e];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) bv[g][e] = (n + e < p.N) ? p.bias[n + e] : 0.f;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < C::FM; ++j) {
+            const int m = m0 + wm * C::WTM + j * 32 + frow;
+            if (m >= p.M) continue;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int n = nb + 8 * g;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = p.alpha * acc[i][j][4 * g + e];
+                if constexpr (BETA) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < p.N) v[e] += p.beta * p.Cin[(int64_t)m * p.ldc + n + e];
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = epilogue_op<EPI>(v[e] + bv[g][e]);
+                if constexpr (OUT == OUT_F32) {
+                    float *y = (float *)p.Y + (int64_t)m * p.ldy + n;
+                    if (p.vec_store && n + 3 < p.N) {
+                        *reinterpret_cast<f32x4_t *>(y) = f32x4_t{v[0], v[1], v[2], v[3]};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (n + e < p.N) y[e] = v[e];
+                    }
+                } else {
+                    uint16_t *y = (uint16_t *)p.Y + (int64_t)m * p.ldy + n;
+                    if (p.vec_store && n + 3 < p.N) {
+                        u32x2_t packed;
+                        packed[0] = pack_bf16x2(v[0], v[1]);
+                        packed[1] = pack_bf16x2(v[2], v[3]);
+                        *reinterpret_cast<u32x2_t *>(y) = packed;
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (n + e < p.N) y[e] = f32_to_bf16_rne(v[e]);
+                    }
+                }
+            }
+        }
+    }
 }
 
 // One work unit: output tile (tm, tn), k-tiles [kt_begin, kt_end).
@@ -641,9 +867,6 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
         mainloop_rs<C>(p, lds, rsw, rsx, kt_begin, kt_end, acc);
     else
         mainloop_ring<C>(p, lds, rsw, rsx, kt_begin, kt_end, acc);
-    // Accumulator layout: lane holds D[n = 8g + 4*fh + e][m = frow] of each 32x32 block.
-    const int frow = lane & 31;
-    const int fh = lane >> 5;
 
 
     if constexpr (MODE != GRID_TILES) {
@@ -709,71 +932,15 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
         }
     }
 
-    // Epilogue: lane holds D[n = 8g + 4*fh + e][m = frow] of each 32x32 block.
-    // For each (i, j) a lane's four g stores cover 32 bytes of row m and the
-    // two lane halves together the row's whole 128-byte segment; they are
-    // issued back to back so the L2 merges them into full lines.
-#pragma unroll
-    for (int i = 0; i < C::FN; ++i) {
-        const int nb = n0 + wn * C::WTN + i * 32 + 4 * fh;
-        float bv[4][4];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int n = nb + 8 * g;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) bv[g][e] = 0.f;
-            if (p.has_bias) {
-                if (n + 3 < p.N) {
-                    f32x4_t t = *(const f32x4_t *)(p.bias + n);  // bias is 16-byte aligned, n % 4 == 0
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) bv[g][e] = t[e];
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) bv[g][e] = (n + e < p.N) ? p.bias[n + e] : 0.f;
-                }
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < C::FM; ++j) {
-            const int m = m0 + wm * C::WTM + j * 32 + frow;
-            if (m >= p.M) continue;
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int n = nb + 8 * g;
-                float v[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = p.alpha * acc[i][j][4 * g + e];
-                if (p.beta != 0.0f) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (n + e < p.N) v[e] += p.beta * p.Cin[(int64_t)m * p.ldc + n + e];
-                }
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = epilogue_op<EPI>(v[e] + bv[g][e]);
-                if constexpr (OUT == OUT_F32) {
-                    float *y = (float *)p.Y + (int64_t)m * p.ldy + n;
-                    if (p.vec_store && n + 3 < p.N) {
-                        *reinterpret_cast<f32x4_t *>(y) = f32x4_t{v[0], v[1], v[2], v[3]};
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            if (n + e < p.N) y[e] = v[e];
-                    }
-                } else {
-                    uint16_t *y = (uint16_t *)p.Y + (int64_t)m * p.ldy + n;
-                    if (p.vec_store && n + 3 < p.N) {
-                        u32x2_t packed;
-                        packed[0] = (uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16);
-                        packed[1] = (uint32_t)f32_to_bf16_rne(v[2]) | ((uint32_t)f32_to_bf16_rne(v[3]) << 16);
-                        *reinterpret_cast<u32x2_t *>(y) = packed;
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            if (n + e < p.N) y[e] = f32_to_bf16_rne(v[e]);
-                    }
-                }
-            }
-        }
+    if constexpr (C::STAGED_EPI) {
+        if (p.beta != 0.0f)
+            store_tile_staged<C, EPI, OUT, true>(p, lds, acc, m0, n0, wn, wm, lane, wave);
+        else
+            store_tile_staged<C, EPI, OUT, false>(p, lds, acc, m0, n0, wn, wm, lane, wave);
+    } else if (p.beta != 0.0f) {
+        store_tile_direct<C, EPI, OUT, true>(p, acc, m0, n0, wn, wm, lane);
+    } else {
+        store_tile_direct<C, EPI, OUT, false>(p, acc, m0, n0, wn, wm, lane);
     }
 }
 

@@ -165,8 +165,8 @@ GRID_MODES = {  # INV_HIP_MODE / INV_HIP_KSPLIT / INV_HIP_SK_GRID
 }
 
 
-ALL_CFGS = list(range(9))  # INV_GEMM_NUM_CONFIGS in invision_amd/csrc/gemm_configs.hpp
-REG_STAGED_CFGS = [8]
+ALL_CFGS = list(range(11))  # INV_GEMM_NUM_CONFIGS in invision_amd/csrc/gemm_configs.hpp
+REG_STAGED_CFGS = [8, 9, 10]
 
 
 @pytest.mark.parametrize("cfg", ALL_CFGS)
