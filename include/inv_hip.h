@@ -43,7 +43,8 @@ extern "C" {
 #define INV_ERR_NOT_INIT     6  /* inv_hip_init has not succeeded                   */
 
 /* ---- element types: the reference's TQNNDataType values
- *      (src/quicknn_common.pas:77-98: dtBf16 = 2, dtF32 = 3) ---------------- */
+ *      (src/quicknn_common.pas:77-98: dtF16 = 1, dtBf16 = 2, dtF32 = 3) ------ */
+#define INV_DT_F16  1 /* safetensors weights only */
 #define INV_DT_BF16 2
 #define INV_DT_F32  3
 
@@ -99,6 +100,34 @@ int inv_hip_weight_upload(const uint16_t *w_bf16, int64_t N, int64_t K, const fl
 int inv_hip_weight_upload_f32(const float *w_f32, int64_t N, int64_t K, const float *bias,
                               inv_weight_t *out);
 int inv_hip_weight_free(inv_weight_t w);
+
+/* ---- weights from .safetensors files --------------------------------------
+ * The file format the reference reads its weights from (TSafeTensorFile,
+ * src/safetensor.pas:466-513): u64 little-endian header length, a JSON header
+ * {name: {dtype, shape, data_offsets [begin, end) from the data block}}, data.
+ * The same checks as the reference: header length below the file size, every
+ * tensor inside the file, and (in addition) byte size = product(shape) * dtype
+ * size for F32/BF16/F16. */
+#define INV_ST_MAX_DIMS 8
+#define INV_ST_TRUNCATE 0x1 /* F32/F16 -> bf16 by truncation (u16 = u32 >> 16), the
+                               reference's SingleToBF16 (src/quicknn_common.pas:
+                               2010-2027) as getTensorDataMemBlockBF16 applies it
+                               (src/safetensor.pas:675); default: ties to even */
+/* Metadata of tensor `name` (no device needed): dtype as INV_DT_* (-1 for
+ * other dtypes), rank, up to INV_ST_MAX_DIMS dimensions, and the byte offset
+ * of its data in the file.  Replaces TSafeTensorFile.find + the tensor record
+ * (src/safetensor.pas:491-507). */
+int inv_hip_safetensors_info(const char *path, const char *name, int *dtype, int *ndim, int64_t *shape,
+                             int64_t *data_offset);
+/* Upload the 2-D weight `name` ([N x K], PyTorch Linear layout) of a
+ * .safetensors file, with an optional 1-D bias `bias_name` (NULL: none; any
+ * of F32/BF16/F16, widened to fp32).  BF16 weights go from the read-only file
+ * mapping straight to the device, as getTensorDataMemBlockBF16 hands the mmap
+ * pointer over (src/safetensor.pas:650-683); F32 and F16 are rounded to bf16
+ * (ties to even, or truncated with INV_ST_TRUNCATE).  The file is unmapped on
+ * return. */
+int inv_hip_weight_load_safetensors(const char *path, const char *name, const char *bias_name, int flags,
+                                    inv_weight_t *out);
 /* N and K of a handle. */
 int inv_hip_weight_shape(inv_weight_t w, int64_t *N, int64_t *K);
 

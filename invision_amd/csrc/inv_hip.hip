@@ -39,6 +39,16 @@ int fail(int code, const char *fmt, ...) {
     return code;
 }
 
+}  // namespace
+
+// Error reporting for the library's other translation units (safetensors.cpp):
+// records the message for inv_hip_last_error on this thread.  Not exported.
+extern "C" __attribute__((visibility("hidden"))) int inv_hip_internal_fail(int code, const char *msg) {
+    return fail(code, "%s", msg);
+}
+
+namespace {
+
 #define HIPCHK(expr)                                                                         \
     do {                                                                                     \
         hipError_t e_ = (expr);                                                              \

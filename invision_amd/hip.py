@@ -22,6 +22,7 @@ INV_ERR_HIP = 5
 INV_ERR_NOT_INIT = 6
 
 # TQNNDataType values (src/quicknn_common.pas:77-98)
+INV_DT_F16 = 1
 INV_DT_BF16 = 2
 INV_DT_F32 = 3
 
@@ -39,6 +40,9 @@ INV_FLAG_DEVICE_PTRS = 0x1
 INV_FLAG_ASYNC = 0x2
 INV_FLAG_PRECISE = 0x4
 
+INV_ST_MAX_DIMS = 8
+INV_ST_TRUNCATE = 0x1
+
 INV_PREC_BF16 = 0
 INV_PREC_SPLIT_A = 1
 INV_PREC_SPLIT_AB = 2
@@ -54,6 +58,9 @@ _PROTOS = {
     "inv_hip_weight_upload_f32": (c_int, [c_void_p, c_int64, c_int64, c_void_p, POINTER(c_void_p)]),
     "inv_hip_weight_free": (c_int, [c_void_p]),
     "inv_hip_weight_shape": (c_int, [c_void_p, POINTER(c_int64), POINTER(c_int64)]),
+    "inv_hip_safetensors_info": (c_int, [c_char_p, c_char_p, POINTER(c_int), POINTER(c_int), POINTER(c_int64),
+                                         POINTER(c_int64)]),
+    "inv_hip_weight_load_safetensors": (c_int, [c_char_p, c_char_p, c_char_p, c_int, POINTER(c_void_p)]),
     "inv_hip_linear": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
                                c_int, c_int]),
     "inv_hip_sgemm": (c_int, [c_int, c_int, c_int, c_int64, c_int64, c_int64, c_float, c_void_p, c_int64, c_void_p,

@@ -11,6 +11,7 @@ arguments across the C ABI.
 from __future__ import annotations
 
 import ctypes
+import os
 from typing import Optional
 
 import numpy as np
@@ -143,6 +144,26 @@ class Weight:
             raise TypeError("weight must be bf16 bits (uint16) or float32")
         self.handle = h.value
         self.has_bias = b is not None
+
+    @classmethod
+    def from_safetensors(cls, path: str, name: str, bias_name: Optional[str] = None,
+                         truncate: bool = False) -> "Weight":
+        """Upload the [N x K] tensor `name` (and 1-D `bias_name`) of a .safetensors
+        file: the reference's getTensorDataMemBlockBF16 (src/safetensor.pas:650-683)
+        feeding the device once.  BF16 is copied as is; F32/F16 are rounded to bf16
+        (ties to even, or truncated like the reference's SingleToBF16 with truncate)."""
+        init()
+        h = ctypes.c_void_p()
+        hip.call("inv_hip_weight_load_safetensors", os.fsencode(path), name.encode(),
+                 bias_name.encode() if bias_name else None, hip.INV_ST_TRUNCATE if truncate else 0,
+                 ctypes.byref(h))
+        self = cls.__new__(cls)
+        self.handle = h.value
+        n, k = ctypes.c_int64(), ctypes.c_int64()
+        hip.call("inv_hip_weight_shape", self.handle, ctypes.byref(n), ctypes.byref(k))
+        self.N, self.K = n.value, k.value
+        self.has_bias = bool(bias_name)
+        return self
 
     def free(self) -> None:
         if self.handle:
@@ -323,3 +344,59 @@ def as_weight(w: np.ndarray, bias: Optional[np.ndarray] = None) -> Weight:
     if w.dtype not in (np.uint16, np.float32):
         w = as_bf16_bits(w)
     return Weight(w, bias)
+
+
+_ST_DTYPES = {hip.INV_DT_F16: "F16", hip.INV_DT_BF16: "BF16", hip.INV_DT_F32: "F32"}
+
+
+def safetensors_info(path: str, name: str) -> dict:
+    """dtype ("F32"/"BF16"/"F16", or None for other dtypes), shape and data byte
+    offset of tensor `name` (TSafeTensorFile.find, src/safetensor.pas:491-507).
+    Parses the header only: no device needed."""
+    dt, nd, off = ctypes.c_int(), ctypes.c_int(), ctypes.c_int64()
+    shape = (ctypes.c_int64 * hip.INV_ST_MAX_DIMS)()
+    hip.call("inv_hip_safetensors_info", os.fsencode(path), name.encode(), ctypes.byref(dt), ctypes.byref(nd),
+             shape, ctypes.byref(off))
+    return {"dtype": _ST_DTYPES.get(dt.value), "shape": tuple(shape[i] for i in range(nd.value)),
+            "data_offset": off.value}
+
+
+class SafeTensorFiles:
+    """The reference's TSafeTensorFilesHelper (src/safetensor.pas:584-683): a set
+    of .safetensors shards searched by tensor name.  Built from file paths, or
+    from a directory holding `model.safetensors.index.json` (its "weight_map",
+    as src/quicknn_transformers.pas:536-556 reads it) or *.safetensors files."""
+
+    def __init__(self, paths):
+        import glob
+        import json
+        if isinstance(paths, (str, os.PathLike)) and os.path.isdir(paths):
+            idx = os.path.join(paths, "model.safetensors.index.json")
+            if os.path.exists(idx):
+                wm = json.load(open(idx))["weight_map"]
+                self._where = {n: os.path.join(paths, f) for n, f in wm.items()}
+                self.paths = sorted(set(self._where.values()))
+                return
+            paths = sorted(glob.glob(os.path.join(paths, "*.safetensors")))
+        elif isinstance(paths, (str, os.PathLike)):
+            paths = [paths]
+        self.paths = [os.fspath(p) for p in paths]
+        self._where = None
+
+    def find(self, name: str) -> str:
+        """The shard that holds `name` (assert-style error if none does)."""
+        if self._where is not None:
+            if name not in self._where:
+                raise KeyError(f"cannot find tensor \"{name}\" in the index")
+            return self._where[name]
+        for p in self.paths:
+            try:
+                safetensors_info(p, name)
+                return p
+            except hip.HipError:
+                continue
+        raise KeyError(f"cannot find tensor \"{name}\" in {len(self.paths)} file(s)")
+
+    def linear_weight(self, name: str, bias_name: Optional[str] = None, truncate: bool = False) -> Weight:
+        """A device weight for a Linear layer (bias from the same shard)."""
+        return Weight.from_safetensors(self.find(name), name, bias_name, truncate)

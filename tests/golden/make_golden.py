@@ -13,6 +13,12 @@ Fixtures (data only: inputs and expected outputs):
                       Requires the reference tree; skipped otherwise.
   linear_small.npz    QNNLinear-shaped cases (bias, SiLU, GELU, ragged
                       shapes) with fp64 closed-form outputs.
+  linear_tiny.safetensors + linear_tiny_expected.npz
+                      a .safetensors file written byte by byte (u64 LE header
+                      length, JSON header, data; the layout TSafeTensorFile.open
+                      reads, src/safetensor.pas:466-513) holding BF16, F32 and
+                      F16 linear weights and biases plus a __metadata__ entry,
+                      and the same arrays with their data byte offsets.
 """
 from __future__ import annotations
 
@@ -99,11 +105,50 @@ def make_linear(path: str) -> None:
     np.savez_compressed(path, **arrays)
 
 
+def make_safetensors(path: str, expected_path: str) -> None:
+    """Tensors in file order; F32 weights include exact bf16 ties (low half
+    0x8000) and values whose truncation and rounding differ."""
+    oracle.rng_seed(77)
+    N, K = 12, 24
+    w_bf16 = oracle.f32_to_bf16_rne(oracle.randn_scaled((N, K), 0.02, False))
+    b_f32 = oracle.randn_scaled((N,), 0.01, False).astype(np.float32)
+    w32 = oracle.randn_scaled((N, K), 0.02, False).astype(np.float32)
+    bits = w32.view(np.uint32).copy()
+    bits[0, :8] = (bits[0, :8] & 0xFFFF0000) | 0x8000          # ties: even and odd upper halves
+    bits[1, :8] = (bits[1, :8] & 0xFFFF0000) | 0x7FFF          # just below a tie
+    bits[2, :8] = (bits[2, :8] & 0xFFFF0000) | 0x8001          # just above a tie
+    w32 = bits.view(np.float32)
+    w16 = (oracle.randn_scaled((N, K), 0.02, False)).astype(np.float16)
+    b_bf16 = oracle.f32_to_bf16_rne(oracle.randn_scaled((N,), 0.01, False))
+    tensors = [
+        ("blocks.0.attn.qkv.weight", "BF16", (N, K), w_bf16.astype("<u2").tobytes()),
+        ("blocks.0.attn.qkv.bias", "F32", (N,), b_f32.astype("<f4").tobytes()),
+        ("blocks.0.mlp.fc32.weight", "F32", (N, K), w32.astype("<f4").tobytes()),
+        ("blocks.0.mlp.fc16.weight", "F16", (N, K), w16.astype("<f2").tobytes()),
+        ("blocks.0.mlp.fc16.bias", "BF16", (N,), b_bf16.astype("<u2").tobytes()),
+        ("blocks.0.norm.scale", "F32", (K,), np.ones(K, "<f4").tobytes()),
+    ]
+    header, data, offsets = {"__metadata__": {"format": "pt"}}, b"", {}
+    for name, dt, shape, raw in tensors:
+        header[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [len(data), len(data) + len(raw)]}
+        offsets[name] = len(data)
+        data += raw
+    hj = json.dumps(header, separators=(",", ":")).encode()
+    hj += b" " * (-len(hj) % 8)
+    with open(path, "wb") as f:
+        f.write(len(hj).to_bytes(8, "little") + hj + data)
+    base = 8 + len(hj)
+    np.savez_compressed(expected_path, w_bf16=w_bf16, b_f32=b_f32, w32=w32, w16=w16, b_bf16=b_bf16,
+                        names=np.array([t[0] for t in tensors]),
+                        data_offsets=np.array([base + offsets[t[0]] for t in tensors], np.int64))
+
+
 def main() -> None:
     with open(os.path.join(HERE, "rng_seed0.json"), "w") as f:
         json.dump(make_rng(), f, indent=1)
     make_sgemm2(os.path.join(HERE, "sgemm2_ref.npz"))
     make_linear(os.path.join(HERE, "linear_small.npz"))
+    make_safetensors(os.path.join(HERE, "linear_tiny.safetensors"), os.path.join(HERE, "linear_tiny_expected.npz"))
     print("fixtures written to", HERE)
 
 
