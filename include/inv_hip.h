@@ -58,6 +58,11 @@ extern "C" {
 #define INV_EPI_NONE      0 /* Y = acc (+bias)                                            */
 #define INV_EPI_SILU      1 /* Y = silu(acc + bias), exact: v / (1 + exp(-v))              */
 #define INV_EPI_GELU_ERF  2 /* Y = 0.5 v (1 + erf(v / sqrt 2)); the reference has no GELU */
+#define INV_EPI_SWIGLU    3 /* gate/up weight only (inv_hip_weight_upload_gate_up):
+                               Y = silu(X.Wg^T + bg) * (X.Wu^T + bu), exact SiLU -- the two
+                               projections and QNNSiluMul of ffnSwigluForward
+                               (src/quicknn_transformers.pas:1331-1334, src/quicknncpu.pas:
+                               2404-2418) in one GEMM; Y has F columns */
 
 /* ---- flags for inv_hip_linear -------------------------------------------- */
 #define INV_FLAG_DEVICE_PTRS 0x1 /* X, Y and bias are device pointers (inv_hip_malloc) */
@@ -99,6 +104,13 @@ int inv_hip_weight_upload(const uint16_t *w_bf16, int64_t N, int64_t K, const fl
  * each value is rounded to bf16, ties to even (exact for widened bf16). */
 int inv_hip_weight_upload_f32(const float *w_f32, int64_t N, int64_t K, const float *bias,
                               inv_weight_t *out);
+/* A gate/up pair for INV_EPI_SWIGLU: gate and up are [F x K] bf16 (FLUX2's
+ * fused linear_in [2F x K] is gate = ptr, up = ptr + F*K, as
+ * src/quicknn_transformers.pas:595-597 splits it; Qwen3 and Z-Image hold them
+ * as separate tensors).  Biases optional (fp32 [F] each).  Stored interleaved
+ * in 128-row blocks so that one output tile holds matching gate and up rows. */
+int inv_hip_weight_upload_gate_up(const uint16_t *gate_bf16, const uint16_t *up_bf16, int64_t F, int64_t K,
+                                  const float *gate_bias, const float *up_bias, inv_weight_t *out);
 int inv_hip_weight_free(inv_weight_t w);
 
 /* ---- weights from .safetensors files --------------------------------------
@@ -109,6 +121,9 @@ int inv_hip_weight_free(inv_weight_t w);
  * tensor inside the file, and (in addition) byte size = product(shape) * dtype
  * size for F32/BF16/F16. */
 #define INV_ST_MAX_DIMS 8
+#define INV_ST_GATE_UP  0x2 /* the tensor is a fused [2F x K] gate|up weight (and the
+                               bias, if any, [2F]): load it as a gate/up pair for
+                               INV_EPI_SWIGLU (N of the handle = F) */
 #define INV_ST_TRUNCATE 0x1 /* F32/F16 -> bf16 by truncation (u16 = u32 >> 16), the
                                reference's SingleToBF16 (src/quicknn_common.pas:
                                2010-2027) as getTensorDataMemBlockBF16 applies it

@@ -17,7 +17,7 @@ void launch_one(const inv::GemmParams &p, dim3 grid, dim3 block, hipStream_t s) 
 }
 
 template <class C, int MODE>
-void launch_epi(const inv::GemmParams &p, int epi, int out, dim3 grid, dim3 block, hipStream_t s) {
+bool launch_epi(const inv::GemmParams &p, int epi, int out, dim3 grid, dim3 block, hipStream_t s) {
     const bool f32 = out == inv::OUT_F32;
     if (epi == inv::EPI_SILU) {
         if (f32) launch_one<C, inv::EPI_SILU, inv::OUT_F32, MODE>(p, grid, block, s);
@@ -25,10 +25,19 @@ void launch_epi(const inv::GemmParams &p, int epi, int out, dim3 grid, dim3 bloc
     } else if (epi == inv::EPI_GELU) {
         if (f32) launch_one<C, inv::EPI_GELU, inv::OUT_F32, MODE>(p, grid, block, s);
         else launch_one<C, inv::EPI_GELU, inv::OUT_BF16, MODE>(p, grid, block, s);
+    } else if (epi == inv::EPI_SWIGLU) {
+        // only one workgroup per tile, and only where the tile splits into gate | up wave columns
+        if constexpr (C::SWIGLU_OK && MODE == inv::GRID_TILES) {
+            if (f32) launch_one<C, inv::EPI_SWIGLU, inv::OUT_F32, MODE>(p, grid, block, s);
+            else launch_one<C, inv::EPI_SWIGLU, inv::OUT_BF16, MODE>(p, grid, block, s);
+            return true;
+        }
+        return false;
     } else {
         if (f32) launch_one<C, inv::EPI_NONE, inv::OUT_F32, MODE>(p, grid, block, s);
         else launch_one<C, inv::EPI_NONE, inv::OUT_BF16, MODE>(p, grid, block, s);
     }
+    return true;
 }
 
 // mode: inv::GRID_TILES (one workgroup per tile), GRID_SPLITK (tiles x ksplit
@@ -37,13 +46,14 @@ template <class C>
 hipError_t launch_cfg(const inv::GemmParams &p, int epi, int out, int mode, hipStream_t s) {
     dim3 block(C::NTHREADS);
     const unsigned ntiles = (unsigned)(p.tiles_m * p.tiles_n);
+    bool ok;
     if (mode == inv::GRID_SPLITK)
-        launch_epi<C, inv::GRID_SPLITK>(p, epi, out, dim3(ntiles * p.ksplit), block, s);
+        ok = launch_epi<C, inv::GRID_SPLITK>(p, epi, out, dim3(ntiles * p.ksplit), block, s);
     else if (mode == inv::GRID_STREAMK)
-        launch_epi<C, inv::GRID_STREAMK>(p, epi, out, dim3((unsigned)p.ksplit), block, s);
+        ok = launch_epi<C, inv::GRID_STREAMK>(p, epi, out, dim3((unsigned)p.ksplit), block, s);
     else
-        launch_epi<C, inv::GRID_TILES>(p, epi, out, dim3(ntiles), block, s);
-    return hipGetLastError();
+        ok = launch_epi<C, inv::GRID_TILES>(p, epi, out, dim3(ntiles), block, s);
+    return ok ? hipGetLastError() : hipErrorInvalidConfiguration;
 }
 
 }  // namespace

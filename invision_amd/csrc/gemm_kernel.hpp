@@ -48,7 +48,10 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) char lds_char_t;
 
-enum EpiKind { EPI_NONE = 0, EPI_SILU = 1, EPI_GELU = 2 };
+// EPI_SWIGLU: the weight holds gate and up rows interleaved in 128-row blocks
+// (a 256-row tile = 128 gate rows, then the 128 up rows of the same outputs);
+// Y[m][f] = silu(gate + bias) * (up + bias), Y is nout columns wide.
+enum EpiKind { EPI_NONE = 0, EPI_SILU = 1, EPI_GELU = 2, EPI_SWIGLU = 3 };
 enum OutKind { OUT_F32 = 0, OUT_BF16 = 1 };
 
 struct GemmParams {
@@ -65,6 +68,7 @@ struct GemmParams {
     int sk_dp_tiles;           // stream-K: tiles done one per workgroup (whole rounds) before the balanced phase
     float alpha, beta;
     int has_bias, vec_store;
+    int nout;             // EPI_SWIGLU: output columns (N = its padded gate+up row count)
     float *partial;       // split/stream-K partial sums (uncached device memory)
     unsigned *counters;   // arrival counters, one per tile, zero between calls (uncached)
 };
@@ -155,6 +159,7 @@ struct TileCfg {
     static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
     static_assert(KSUB % 2 == 0, "register double-buffering alternates over an even substep count");
     static constexpr bool STAGED_EPI = NWAVES * 32 * (WTN + 4) * 4 <= LDS_BYTES;
+    static constexpr bool SWIGLU_OK = STAGED_EPI && TN == 256 && WN == 2;  // wave columns = gate | up
 };
 
 // Register-staged configuration: TN x TM tile, WN x WM waves, 64-wide k-tiles
@@ -189,6 +194,7 @@ struct RsCfg {
     static_assert(NREG == 1 || NREG == 2, "one or two register stages");
     static_assert(PF == 1 || PF == 2, "fragment prefetch distance 1 or 2 substeps");
     static constexpr bool STAGED_EPI = NWAVES * 32 * (WTN + 4) * 4 <= LDS_BYTES;
+    static constexpr bool SWIGLU_OK = STAGED_EPI && TN == 256 && WN == 2;  // wave columns = gate | up
     static_assert(NREG * LOADS - 1 < 64, "vmcnt holds at most 63 outstanding loads");
 };
 
@@ -833,6 +839,93 @@ __device__ __forceinline__ void store_tile_direct(const GemmParams &p, const f32
     }
 }
 
+// SwiGLU epilogue (QNNSiluMul over two projections, src/quicknncpu.pas:2404-
+// 2418, fused).  Wave column wn = 0 holds the gate rows of the tile, wn = 1 the
+// up rows of the same outputs: both stage each 32-row block in LDS, then each
+// wave of the pair finishes half of the block's rows,
+//   Y[m][f] = silu(alpha*gate + bg) * (alpha*up + bu),  f = n0/2 + col,
+// with the exact SiLU v / (1 + exp(-v)).  Needs SWIGLU_OK and beta == 0.
+template <class C, int OUT>
+__device__ __forceinline__ void store_tile_swiglu(const GemmParams &p, lds_char_t *lds,
+                                                  const f32x16_t (&acc)[C::FN][C::FM], int m0, int n0, int wn,
+                                                  int wm, int lane, int wave) {
+    static_assert(C::SWIGLU_OK, "SwiGLU needs 256-row tiles split over two wave columns");
+    typedef __attribute__((address_space(3))) float lds_float_t;
+    constexpr int SROW = C::WTN + 4;
+    constexpr int LPR = C::WTN / 4;   // 32 lanes per staged row
+    constexpr int RPI = 64 / LPR;     // 2 rows per read instruction
+    constexpr int HALF = 16;          // rows of a 32-row block finished by each wave of the pair
+    constexpr int NIT = HALF / RPI;
+    const int frow = lane & 31;
+    const int fh = lane >> 5;
+    lds_float_t *own = (lds_float_t *)lds + wave * 32 * SROW;
+    const lds_float_t *gst = (const lds_float_t *)lds + (0 * C::WM + wm) * 32 * SROW;  // gate wave of this row band
+    const lds_float_t *ust = (const lds_float_t *)lds + (1 * C::WM + wm) * 32 * SROW;  // up wave
+    const int col = (lane % LPR) * 4;
+    const int rsub = lane / LPR;
+    const int f = n0 / 2 + col;  // output column
+    const bool fvec = p.vec_store && f + 3 < p.nout;
+    float bg[4] = {0.f, 0.f, 0.f, 0.f}, bu[4] = {0.f, 0.f, 0.f, 0.f};
+    if (p.has_bias) {  // interleaved like the rows: gate bias at n0 + col, up bias at n0 + 128 + col
+        const f32x4_t g4 = *(const f32x4_t *)(p.bias + n0 + col);
+        const f32x4_t u4 = *(const f32x4_t *)(p.bias + n0 + C::WTN + col);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            bg[e] = g4[e];
+            bu[e] = u4[e];
+        }
+    }
+    wait_vmcnt<0>();
+    __syncthreads();  // every wave has finished with the ring
+#pragma unroll
+    for (int j = 0; j < C::FM; ++j) {
+#pragma unroll
+        for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *(__attribute__((address_space(3))) f32x4_t *)(own + frow * SROW + i * 32 + 8 * g + 4 * fh) =
+                    f32x4_t{p.alpha * acc[i][j][4 * g], p.alpha * acc[i][j][4 * g + 1],
+                            p.alpha * acc[i][j][4 * g + 2], p.alpha * acc[i][j][4 * g + 3]};
+        __syncthreads();  // the pair's gate and up blocks are both staged
+        f32x4_t gv[NIT], uv[NIT];
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int r = wn * HALF + it * RPI + rsub;
+            gv[it] = *(const __attribute__((address_space(3))) f32x4_t *)(gst + r * SROW + col);
+            uv[it] = *(const __attribute__((address_space(3))) f32x4_t *)(ust + r * SROW + col);
+        }
+        const int mrow = m0 + wm * C::WTM + j * 32 + wn * HALF + rsub;
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int m = mrow + it * RPI;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float gt = gv[it][e] + bg[e];
+                v[e] = gt / (1.0f + expf(-gt)) * (uv[it][e] + bu[e]);
+            }
+            if (m >= p.M) continue;
+            const int64_t off = (int64_t)m * p.ldy + f;
+            if (fvec) {
+                if constexpr (OUT == OUT_F32)
+                    *reinterpret_cast<f32x4_t *>((float *)p.Y + off) = f32x4_t{v[0], v[1], v[2], v[3]};
+                else
+                    *reinterpret_cast<u32x2_t *>((uint16_t *)p.Y + off) =
+                        u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            } else {
+                for (int e = 0; e < 4; ++e) {
+                    if (f + e >= p.nout) break;
+                    if constexpr (OUT == OUT_F32)
+                        ((float *)p.Y)[off + e] = v[e];
+                    else
+                        ((uint16_t *)p.Y)[off + e] = f32_to_bf16_rne(v[e]);
+                }
+            }
+        }
+        __syncthreads();  // both waves have read the block before the next one is staged
+    }
+}
+
 // One work unit: output tile (tm, tn), k-tiles [kt_begin, kt_end).
 template <class C, int EPI, int OUT, int MODE>
 __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int tm, int tn, int kt_begin, int kt_end,
@@ -932,7 +1025,9 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
         }
     }
 
-    if constexpr (C::STAGED_EPI) {
+    if constexpr (EPI == EPI_SWIGLU) {
+        store_tile_swiglu<C, OUT>(p, lds, acc, m0, n0, wn, wm, lane, wave);
+    } else if constexpr (C::STAGED_EPI) {
         if (p.beta != 0.0f)
             store_tile_staged<C, EPI, OUT, true>(p, lds, acc, m0, n0, wn, wm, lane, wave);
         else

@@ -98,9 +98,12 @@ std::mutex g_mu;
 
 struct inv_weight_s {
     uint32_t magic;
-    uint16_t *w;   // [N x ldw] bf16, zero padded beyond K
-    float *bias;   // [N] or null
+    uint16_t *w;   // [rows x ldw] bf16, zero padded beyond K
+    float *bias;   // [rows] or null
     int64_t N, K, ldw;
+    int gated;     // gate/up pair for INV_EPI_SWIGLU: rows = 2 * N rounded up to 128 per half,
+                   // interleaved in 128-row blocks (gate block b at rows 256b, its up block at 256b + 128)
+    int64_t rows;  // device rows (N unless gated)
 };
 
 namespace {
@@ -241,11 +244,13 @@ struct TileChoice {
 struct CfgMeta {
     int tn, tm, threads, acc_regs, bk, lds;
     bool reg_staged;  // RsCfg: no stream-K / split-K (its fixup path spills registers)
+    bool swiglu_ok;   // 256-row tiles over two wave columns with a staged epilogue
     hipError_t (*launch)(const inv::GemmParams &, int, int, int, hipStream_t);
 };
 #define INV_META(id)                                                                        \
     {INV_CFG_##id::TN,       INV_CFG_##id::TM,  INV_CFG_##id::NTHREADS, INV_CFG_##id::ACC_REGS, \
-     INV_CFG_##id::BK,       INV_CFG_##id::LDS_BYTES, INV_CFG_##id::REG_STAGED, &inv_gemm_launch_##id},
+     INV_CFG_##id::BK,       INV_CFG_##id::LDS_BYTES, INV_CFG_##id::REG_STAGED, INV_CFG_##id::SWIGLU_OK,      \
+     &inv_gemm_launch_##id},
 const CfgMeta kCfg[INV_GEMM_NUM_CONFIGS] = {INV_GEMM_CONFIG_IDS(INV_META)};
 #undef INV_META
 constexpr int kNumCfg = INV_GEMM_NUM_CONFIGS;
@@ -326,7 +331,7 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
 // W [N x ldw], X [M x ldx] bf16 device; K a multiple of 8 (zero padded).
 int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, void *Y, int64_t ldy, int out,
              const float *bias, const float *Cin, int64_t ldc, float alpha, float beta, int64_t M, int64_t N,
-             int64_t K, int epi, int64_t w_seg_k = 0, int64_t Kw = -1) {
+             int64_t K, int epi, int64_t w_seg_k = 0, int64_t Kw = -1, int64_t nout = -1) {
     if (M == 0 || N == 0) return INV_OK;
     if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return fail(INV_ERR_ARG, "dimension too large");
     if (K % 8 || ldw % 8 || ldx % 8 || !aligned(W, 16) || !aligned(X, 16))
@@ -334,7 +339,14 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
     if ((int64_t)256 * ldw * 2 >= ((int64_t)1 << 31) || (int64_t)256 * ldx * 2 >= ((int64_t)1 << 31))
         return fail(INV_ERR_UNSUPPORTED, "leading dimension too large for 32-bit buffer offsets");
     TileChoice tc = choose_tiles(M, N, K);
+    if (epi == INV_EPI_SWIGLU) {
+        // gate | up wave columns over 256-row tiles, one workgroup per tile
+        if (!kCfg[tc.cfg].swiglu_ok) tc.cfg = (M > 128) ? 8 : 2;
+        tc.mode = inv::GRID_TILES;
+        if (beta != 0.0f) return fail(INV_ERR_UNSUPPORTED, "SwiGLU epilogue with beta != 0");
+    }
     inv::GemmParams p{};
+    p.nout = (int)(nout < 0 ? N : nout);
     p.W = W;
     p.X = X;
     p.Y = Y;
@@ -451,7 +463,9 @@ bool valid_weight(inv_weight_t w) {
     return false;
 }
 
-int epi_ok(int epi) { return epi == INV_EPI_NONE || epi == INV_EPI_SILU || epi == INV_EPI_GELU_ERF; }
+int epi_ok(int epi) {
+    return epi == INV_EPI_NONE || epi == INV_EPI_SILU || epi == INV_EPI_GELU_ERF || epi == INV_EPI_SWIGLU;
+}
 
 int upload_bias(const float *bias, int64_t N, float **out) {
     *out = nullptr;
@@ -506,7 +520,7 @@ int weight_upload_impl(const void *w, bool is_f32, int64_t N, int64_t K, const f
         if (db) (void)hipFree(db);
         return rc;
     }
-    auto *h = new inv_weight_s{kWeightMagic, dw, db, N, K, ldw};
+    auto *h = new inv_weight_s{kWeightMagic, dw, db, N, K, ldw, 0, N};
     g.weights.push_back(h);
     *out = h;
     return INV_OK;
@@ -747,6 +761,66 @@ int inv_hip_weight_upload_f32(const float *w_f32, int64_t N, int64_t K, const fl
     return weight_upload_impl(w_f32, true, N, K, bias, out);
 }
 
+int inv_hip_weight_upload_gate_up(const uint16_t *gate_bf16, const uint16_t *up_bf16, int64_t F, int64_t K,
+                                  const float *gate_bias, const float *up_bias, inv_weight_t *out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    TRY(check_init());
+    if (!out) return fail(INV_ERR_ARG, "out handle pointer is null");
+    *out = nullptr;
+    if (!gate_bf16 || !up_bf16 || F <= 0 || K <= 0)
+        return fail(INV_ERR_ARG, "gate/up weight: null pointer or non-positive shape (F=%lld K=%lld)", (long long)F,
+                    (long long)K);
+    if (F > INT32_MAX / 8 || K > INT32_MAX / 2) return fail(INV_ERR_ARG, "gate/up weight too large");
+    const int64_t ldw = round_up(K, 8), fpad = round_up(F, 128), rows = 2 * fpad;
+    uint16_t *dw = nullptr;
+    if (hipMalloc(&dw, (size_t)(rows * ldw) * 2) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(INV_ERR_OOM, "gate/up weight allocation of %lld bytes failed", (long long)(rows * ldw * 2));
+    }
+    int rc = INV_OK;
+    if (hipMemsetAsync(dw, 0, (size_t)(rows * ldw) * 2, g.stream) != hipSuccess)
+        rc = fail(INV_ERR_HIP, "gate/up weight: clearing failed");
+    // 128-row blocks: gate rows [128b, 128b+128) -> device rows 256b.., up -> 256b+128..
+    for (int half = 0; half < 2 && !rc; ++half) {
+        const uint16_t *src = half ? up_bf16 : gate_bf16;
+        for (int64_t f0 = 0; f0 < F && !rc; f0 += 128) {
+            const int64_t nr = std::min<int64_t>(128, F - f0);
+            uint16_t *dst = dw + ((f0 / 128) * 256 + half * 128) * ldw;
+            if (ldw == K) {
+                rc = h2d_rows(dst, src + f0 * K, nr, (size_t)K * 2, (size_t)K * 2);
+            } else {
+                rc = ensure(g.win, (size_t)(nr * K) * 2);
+                if (!rc) rc = h2d_rows(g.win.p, src + f0 * K, nr, (size_t)K * 2, (size_t)K * 2);
+                if (!rc) rc = launch_copy_rows_bf16((const uint16_t *)g.win.p, K, dst, ldw, nr, K, ldw);
+                if (!rc && hipStreamSynchronize(g.stream) != hipSuccess) rc = fail(INV_ERR_HIP, "gate/up copy failed");
+            }
+        }
+    }
+    float *db = nullptr;
+    if (!rc && (gate_bias || up_bias)) {
+        std::vector<float> bi((size_t)rows, 0.0f);
+        for (int64_t f = 0; f < F; ++f) {
+            const int64_t r = (f / 128) * 256 + f % 128;
+            if (gate_bias) bi[(size_t)r] = gate_bias[f];
+            if (up_bias) bi[(size_t)(r + 128)] = up_bias[f];
+        }
+        rc = upload_bias(bi.data(), rows, &db);
+    }
+    if (!rc) {
+        hipError_t e = hipStreamSynchronize(g.stream);
+        if (e != hipSuccess) rc = fail(INV_ERR_HIP, "gate/up weight upload: %s", hipGetErrorString(e));
+    }
+    if (rc) {
+        (void)hipFree(dw);
+        if (db) (void)hipFree(db);
+        return rc;
+    }
+    auto *h = new inv_weight_s{kWeightMagic, dw, db, F, K, ldw, 1, rows};
+    g.weights.push_back(h);
+    *out = h;
+    return INV_OK;
+}
+
 int inv_hip_weight_free(inv_weight_t w) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (!w) return INV_OK;
@@ -784,6 +858,10 @@ int inv_hip_linear(const void *X, int x_dtype, inv_weight_t W, const float *bias
     if (K != W->K || N != W->N)
         return fail(INV_ERR_ARG, "linear: shape mismatch: call K=%lld N=%lld, weight K=%lld N=%lld", (long long)K,
                     (long long)N, (long long)W->K, (long long)W->N);
+    if ((epilogue == INV_EPI_SWIGLU) != (W->gated != 0))
+        return fail(INV_ERR_ARG, W->gated ? "linear: a gate/up weight needs INV_EPI_SWIGLU"
+                                          : "linear: INV_EPI_SWIGLU needs a gate/up weight (inv_hip_weight_upload_gate_up)");
+    if (W->gated && bias) return fail(INV_ERR_ARG, "linear: a gate/up weight takes its biases at upload");
     if (M == 0) return INV_OK;
     if (!X || !Y) return fail(INV_ERR_ARG, "linear: X or Y is null");
     if (M > INT32_MAX / 2) return fail(INV_ERR_ARG, "linear: M too large");
@@ -821,11 +899,14 @@ int inv_hip_linear(const void *X, int x_dtype, inv_weight_t W, const float *bias
         TRY(ensure(g.yout, (size_t)(M * N) * ysz));
         Yd = g.yout.p;
     }
+    // The GEMM runs over the handle's device rows (2 x 128-padded N for a
+    // gate/up pair); Y has N columns either way.
     if (precise)
-        TRY(run_gemm(W->w, W->ldw, Xd, ldx, Yd, N, out, bd, nullptr, 0, 1.0f, 0.0f, M, N, 2 * kseg, epilogue,
-                     kseg, W->ldw));
+        TRY(run_gemm(W->w, W->ldw, Xd, ldx, Yd, N, out, bd, nullptr, 0, 1.0f, 0.0f, M, W->rows, 2 * kseg, epilogue,
+                     kseg, W->ldw, N));
     else
-        TRY(run_gemm(W->w, W->ldw, Xd, ldx, Yd, N, out, bd, nullptr, 0, 1.0f, 0.0f, M, N, W->ldw, epilogue));
+        TRY(run_gemm(W->w, W->ldw, Xd, ldx, Yd, N, out, bd, nullptr, 0, 1.0f, 0.0f, M, W->rows, W->ldw, epilogue,
+                     0, -1, N));
     g.calls++;
     if (!dev) {
         TRY(d2h_rows(Y, Yd, M, (size_t)N * ysz, (size_t)N * ysz));

@@ -398,6 +398,10 @@ extern "C" int inv_hip_weight_load_safetensors(const char *path, const char *nam
         return fail(INV_ERR_UNSUPPORTED, "safetensors: \"%s\" has dtype %s (supported: BF16, F32, F16)", name,
                     t->dtype.c_str());
     const int64_t N = t->shape[0], K = t->shape[1];
+    const bool gate_up = (flags & INV_ST_GATE_UP) != 0;
+    if (gate_up && (N % 2))
+        return fail(INV_ERR_ARG, "safetensors: \"%s\" has %lld rows, a fused gate|up weight needs an even count", name,
+                    (long long)N);
 
     std::vector<float> bias;
     if (bias_name && *bias_name) {
@@ -414,6 +418,27 @@ extern "C" int inv_hip_weight_load_safetensors(const char *path, const char *nam
     }
     const float *bp = bias.empty() ? nullptr : bias.data();
     const uint8_t *src = f.data(*t);
+    if (gate_up) {
+        // [2F x K]: gate rows first, up rows second (src/quicknn_transformers.pas:595-597)
+        const int64_t F = N / 2;
+        std::vector<uint16_t> wb;
+        const uint16_t *w16 = (const uint16_t *)src;
+        if (t->dtype != "BF16") {
+            std::vector<float> wf = to_f32(src, t->dtype, N * K);
+            wb.resize((size_t)(N * K));
+            for (int64_t i = 0; i < N * K; ++i) {
+                uint32_t u;
+                memcpy(&u, &wf[(size_t)i], 4);
+                if (!(flags & INV_ST_TRUNCATE)) {
+                    if ((u & 0x7fffffffu) > 0x7f800000u) u |= 0x00400000u;  // NaN stays NaN
+                    else u += 0x7fffu + ((u >> 16) & 1u);
+                }
+                wb[(size_t)i] = (uint16_t)(u >> 16);
+            }
+            w16 = wb.data();
+        }
+        return inv_hip_weight_upload_gate_up(w16, w16 + F * K, F, K, bp, bp ? bp + F : nullptr, out);
+    }
     if (t->dtype == "BF16") {
         // the mmap pointer straight into the upload, as getTensorDataMemBlockBF16
         // hands it to the reference (src/safetensor.pas:661-667)

@@ -35,6 +35,7 @@ CblasTrans = 112
 INV_EPI_NONE = 0
 INV_EPI_SILU = 1
 INV_EPI_GELU_ERF = 2
+INV_EPI_SWIGLU = 3
 
 INV_FLAG_DEVICE_PTRS = 0x1
 INV_FLAG_ASYNC = 0x2
@@ -42,6 +43,7 @@ INV_FLAG_PRECISE = 0x4
 
 INV_ST_MAX_DIMS = 8
 INV_ST_TRUNCATE = 0x1
+INV_ST_GATE_UP = 0x2
 
 INV_PREC_BF16 = 0
 INV_PREC_SPLIT_A = 1
@@ -56,6 +58,8 @@ _PROTOS = {
     "inv_hip_device_info": (c_int, [c_char_p, c_size_t, POINTER(c_int), POINTER(c_int)]),
     "inv_hip_weight_upload": (c_int, [c_void_p, c_int64, c_int64, c_void_p, POINTER(c_void_p)]),
     "inv_hip_weight_upload_f32": (c_int, [c_void_p, c_int64, c_int64, c_void_p, POINTER(c_void_p)]),
+    "inv_hip_weight_upload_gate_up": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p,
+                                              POINTER(c_void_p)]),
     "inv_hip_weight_free": (c_int, [c_void_p]),
     "inv_hip_weight_shape": (c_int, [c_void_p, POINTER(c_int64), POINTER(c_int64)]),
     "inv_hip_safetensors_info": (c_int, [c_char_p, c_char_p, POINTER(c_int), POINTER(c_int), POINTER(c_int64),

@@ -144,25 +144,53 @@ class Weight:
             raise TypeError("weight must be bf16 bits (uint16) or float32")
         self.handle = h.value
         self.has_bias = b is not None
+        self.gated = False
+
+    @classmethod
+    def gate_up(cls, gate: np.ndarray, up: np.ndarray, gate_bias: Optional[np.ndarray] = None,
+                up_bias: Optional[np.ndarray] = None) -> "Weight":
+        """A gate/up pair for epilogue="swiglu": Y = silu(x.Wg^T + bg) * (x.Wu^T + bu).
+        gate and up are [F x K] bf16 bits (FLUX2's fused [2F x K] linear_in splits as
+        gate = rows [0, F), up = rows [F, 2F), src/quicknn_transformers.pas:595-597)."""
+        init()
+        g = np.ascontiguousarray(gate, dtype=np.uint16)
+        u = np.ascontiguousarray(up, dtype=np.uint16)
+        if g.ndim != 2 or g.shape != u.shape:
+            raise ValueError("gate and up must be [F x K] of the same shape")
+        F, K = (int(x) for x in g.shape)
+        bg = None if gate_bias is None else np.ascontiguousarray(gate_bias, dtype=np.float32)
+        bu = None if up_bias is None else np.ascontiguousarray(up_bias, dtype=np.float32)
+        for b in (bg, bu):
+            if b is not None and b.shape != (F,):
+                raise ValueError("biases must have shape (F,)")
+        h = ctypes.c_void_p()
+        hip.call("inv_hip_weight_upload_gate_up", _ptr(g), _ptr(u), F, K, _ptr(bg) if bg is not None else None,
+                 _ptr(bu) if bu is not None else None, ctypes.byref(h))
+        self = cls.__new__(cls)
+        self.handle, self.N, self.K = h.value, F, K
+        self.has_bias = bg is not None or bu is not None
+        self.gated = True
+        return self
 
     @classmethod
     def from_safetensors(cls, path: str, name: str, bias_name: Optional[str] = None,
-                         truncate: bool = False) -> "Weight":
+                         truncate: bool = False, gate_up: bool = False) -> "Weight":
         """Upload the [N x K] tensor `name` (and 1-D `bias_name`) of a .safetensors
         file: the reference's getTensorDataMemBlockBF16 (src/safetensor.pas:650-683)
         feeding the device once.  BF16 is copied as is; F32/F16 are rounded to bf16
         (ties to even, or truncated like the reference's SingleToBF16 with truncate)."""
         init()
         h = ctypes.c_void_p()
+        flags = (hip.INV_ST_TRUNCATE if truncate else 0) | (hip.INV_ST_GATE_UP if gate_up else 0)
         hip.call("inv_hip_weight_load_safetensors", os.fsencode(path), name.encode(),
-                 bias_name.encode() if bias_name else None, hip.INV_ST_TRUNCATE if truncate else 0,
-                 ctypes.byref(h))
+                 bias_name.encode() if bias_name else None, flags, ctypes.byref(h))
         self = cls.__new__(cls)
         self.handle = h.value
         n, k = ctypes.c_int64(), ctypes.c_int64()
         hip.call("inv_hip_weight_shape", self.handle, ctypes.byref(n), ctypes.byref(k))
         self.N, self.K = n.value, k.value
         self.has_bias = bool(bias_name)
+        self.gated = gate_up
         return self
 
     def free(self) -> None:
@@ -177,7 +205,8 @@ class Weight:
         self.free()
 
 
-_EPI = {"none": hip.INV_EPI_NONE, "silu": hip.INV_EPI_SILU, "gelu": hip.INV_EPI_GELU_ERF}
+_EPI = {"none": hip.INV_EPI_NONE, "silu": hip.INV_EPI_SILU, "gelu": hip.INV_EPI_GELU_ERF,
+        "swiglu": hip.INV_EPI_SWIGLU}
 
 
 def linear_device(x: DeviceArray, W: Weight, y: DeviceArray, M: int, epilogue: str = "none",
