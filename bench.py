@@ -52,6 +52,11 @@ WORKLOADS = {
     "c5_up": ("Z-Image MLP up", 9216, 3840, 15360, True, "none", "bf16", "f32"),
     "c5_down": ("Z-Image MLP down", 9216, 15360, 3840, True, "none", "bf16", "f32"),
     "c5_adaln": ("Z-Image AdaLN modulation M=2", 2, 3840, 23040, True, "none", "bf16", "f32"),
+    # N is the SwiGLU output width F: the GEMM runs over the 2F gate/up rows
+    "flux2_swiglu": ("FLUX2 MLP gate/up with fused SiLU(gate)*up, bf16 H", 4608, 3072, 9216, True, "swiglu", "bf16",
+                     "bf16"),
+    "flux2_gated_out": ("FLUX2 attention out-projection into the gated fp32 residual", 4608, 3072, 3072, False,
+                        "gated_add", "bf16", "f32"),
 }
 
 
@@ -69,10 +74,19 @@ def make_inputs(M, K, N, seed=0):
     return X, W, b
 
 
-def algorithmic_bytes(M, K, N, bias, xdt, ydt):
+def gemm_rows(N, epi):
+    """Weight rows the GEMM runs over (a gate/up pair has two per output column)."""
+    return 2 * N if epi == "swiglu" else N
+
+
+def algorithmic_bytes(M, K, N, bias, xdt, ydt, epi="none"):
     xs = 2 if xdt == "bf16" else 4
     ys = 2 if ydt == "bf16" else 4
-    return M * K * xs + N * K * 2 + M * N * ys + (4 * N if bias else 0)
+    R = gemm_rows(N, epi)
+    b = M * K * xs + R * K * 2 + M * N * ys + (4 * R if bias else 0)
+    if epi == "gated_add":
+        b += M * N * ys + 4 * N  # the residual read back, and the gate
+    return b
 
 
 def run_workload(name, steps, warmup, check=True, host_path=False, warmup_seconds=0.0):
@@ -82,15 +96,38 @@ def run_workload(name, steps, warmup, check=True, host_path=False, warmup_second
 
     desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[name]
     log(f"[bench] {name}: {desc} M={M} K={K} N={N} epilogue={epi} x={xdt} y={ydt}")
-    X, W, b = make_inputs(M, K, N)
+    R = gemm_rows(N, epi)
+    X, W, b = make_inputs(M, K, R)
     Xin = as_bf16_bits(X) if xdt == "bf16" else X
-    w = q.Weight(W, b if has_bias else None)
+    if epi == "swiglu":
+        w = q.Weight.gate_up(W[:N], W[N:], b[:N] if has_bias else None, b[N:] if has_bias else None)
+    else:
+        w = q.Weight(W, b if has_bias else None)
     xd = q.DeviceArray.from_host(Xin, xdt)
     yd = q.DeviceArray((M, N), ydt)
+    gd = None
+    if epi == "gated_add":
+        rng = np.random.default_rng(1)
+        Y0 = rng.standard_normal((M, N), dtype=np.float32)
+        yd.copy_from(Y0)
+        gate = (rng.standard_normal(N, dtype=np.float32) * np.float32(0.5)).astype(np.float32)
+        gd = q.DeviceArray.from_host(gate, "f32")
+
+    def launch():
+        if epi == "gated_add":
+            q.linear_gated_add_device(xd, w, yd, M, gate=gd, asynchronous=True)
+        else:
+            q.linear_device(xd, w, yd, M, epilogue=epi, asynchronous=True)
+
+    if epi == "gated_add" and check:
+        # parity on the first call's update, before timing accumulates into Y
+        launch()
+        hip.call("inv_hip_synchronize")
+        Y1 = yd.to_host()
     warm_steps, tw = 0, time.perf_counter()
     while warm_steps < warmup or time.perf_counter() - tw < warmup_seconds:
         for _ in range(25):
-            q.linear_device(xd, w, yd, M, epilogue=epi, asynchronous=True)
+            launch()
         warm_steps += 25
         hip.call("inv_hip_synchronize")
     # Timed region: host wall clock bracketed by synchronizations, and HIP
@@ -98,7 +135,7 @@ def run_workload(name, steps, warmup, check=True, host_path=False, warmup_second
     t0 = time.perf_counter()
     hip.call("inv_hip_timer_start")
     for _ in range(steps):
-        q.linear_device(xd, w, yd, M, epilogue=epi, asynchronous=True)
+        launch()
     import ctypes
     ms = ctypes.c_float()
     hip.call("inv_hip_timer_stop", ctypes.byref(ms))
@@ -110,17 +147,18 @@ def run_workload(name, steps, warmup, check=True, host_path=False, warmup_second
     per = []
     for _ in range(min(steps, 30)):
         hip.call("inv_hip_timer_start")
-        q.linear_device(xd, w, yd, M, epilogue=epi, asynchronous=True)
+        launch()
         hip.call("inv_hip_timer_stop", ctypes.byref(ms))
         per.append(ms.value)
     p10, p50, p90 = (float(v) for v in np.percentile(per, [10, 50, 90]))
-    flops = 2.0 * M * N * K
-    res = {"name": name, "M": M, "K": K, "N": N, "warmup_steps": warm_steps, "wall_ms": wall_ms, "kernel_ms": gpu_ms,
-           "tflops_wall": flops / (wall_ms * 1e-3) / 1e12, "tflops_kernel": flops / (gpu_ms * 1e-3) / 1e12,
-           "bytes": algorithmic_bytes(M, K, N, has_bias, xdt, ydt)}
+    flops = 2.0 * M * R * K
+    res = {"name": name, "M": M, "K": K, "N": N, "gemm_rows": R, "warmup_steps": warm_steps, "wall_ms": wall_ms,
+           "kernel_ms": gpu_ms, "tflops_wall": flops / (wall_ms * 1e-3) / 1e12,
+           "tflops_kernel": flops / (gpu_ms * 1e-3) / 1e12,
+           "bytes": algorithmic_bytes(M, K, N, has_bias, xdt, ydt, epi)}
     res["gbs_kernel"] = res["bytes"] / (gpu_ms * 1e-3) / 1e9
     res["launch_ms_p10_p50_p90"] = [round(p10, 5), round(p50, 5), round(p90, 5)]
-    if host_path:
+    if host_path and epi in ("none", "silu", "gelu"):
         # The reference's own calling convention: fp32 X and Y in host memory,
         # copied over PCIe on every call (pinned bounce buffers), X rounded on
         # the device.  Reported beside the device-resident rate, never as it.
@@ -135,8 +173,8 @@ def run_workload(name, steps, warmup, check=True, host_path=False, warmup_second
         res["host_fp32_io_tflops"] = flops / (host_ms * 1e-3) / 1e12
     if check:
         # Spot parity on a few rows with numpy float64 (independent of the oracle).
-        Y = yd.to_host()
-        Yf = bf16_bits_to_f32(Y) if ydt == "bf16" else Y
+        Y = Y1 if epi == "gated_add" else yd.to_host()
+        Yf = bf16_bits_to_f32(Y) if ydt == "bf16" else Y.astype(np.float64)
         rows = np.unique(np.linspace(0, M - 1, num=min(M, 6)).astype(int))
         Xr = bf16_bits_to_f32(as_bf16_bits(X[rows])).astype(np.float64)
         ref = Xr @ bf16_bits_to_f32(W).astype(np.float64).T
@@ -144,11 +182,20 @@ def run_workload(name, steps, warmup, check=True, host_path=False, warmup_second
             ref += b.astype(np.float64)
         if epi == "silu":
             ref = ref / (1.0 + np.exp(-ref))
+        elif epi == "swiglu":
+            g, u = ref[:, :N], ref[:, N:]
+            ref = g / (1.0 + np.exp(-g)) * u
+        elif epi == "gated_add":
+            ref = gate.astype(np.float64) * ref  # compared on the update Y1 - Y0
+            Yf = Yf[rows] - Y0[rows]
+            rows = slice(None)
         err = float(np.max(np.abs(Yf[rows] - ref)) / np.max(np.abs(ref)))
         res["parity_normwise_sampled_rows"] = err
     xd.free()
     yd.free()
     w.free()
+    if gd is not None:
+        gd.free()
     return res
 
 
@@ -264,7 +311,7 @@ def summarize_profile(workload, trace_dir, fetch_dir, write_dir, kernel="gemm_nt
 
     desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[workload]
     flops = 2.0 * M * N * K
-    alg = algorithmic_bytes(M, K, N, has_bias, xdt, ydt)
+    alg = algorithmic_bytes(M, K, N, has_bias, xdt, ydt, epi)
     stats = list(csv.DictReader(open(find(trace_dir, "kernel_stats.csv"))))
     fe, wr = counters(fetch_dir), counters(write_dir)
     copyk = next(k for k in fe if "copy_words16" in k)
@@ -383,7 +430,7 @@ def main():
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic},
         "parity_normwise_sampled_rows": res.get("parity_normwise_sampled_rows"),
         "launch_ms_p10_p50_p90": res["launch_ms_p10_p50_p90"],
-        "host_fp32_io_tflops": round(res["host_fp32_io_tflops"], 2),
+        "host_fp32_io_tflops": round(res["host_fp32_io_tflops"], 2) if "host_fp32_io_tflops" in res else None,
         "device": info["name"],
     }
     if not args.no_cpu_baseline:

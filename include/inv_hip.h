@@ -156,6 +156,18 @@ int inv_hip_weight_shape(inv_weight_t w, int64_t *N, int64_t *K);
 int inv_hip_linear(const void *X, int x_dtype, inv_weight_t W, const float *bias, void *Y,
                    int y_dtype, int64_t M, int64_t K, int64_t N, int epilogue, int flags);
 
+/* Gated residual projection: Y[m][n] += gate[n] * (X . W^T + bias)[m][n].
+ * Replaces the QNNLINEAR_BF16_OR_F32 projection followed by QNNGatedAdd
+ * (src/quicknn_transformers.pas:1432-1438, 1447, 1456, 1528-1529;
+ * QNNGatedAdd src/quicknncpu.pas:853-859, QNNAccMul 1752-1758) with one GEMM
+ * whose epilogue scales each column by the gate and adds it into the fp32
+ * residual stream Y [M x N] in place; the projection is never stored.
+ * gate: [N] fp32, or NULL for a plain residual add (Y += X . W^T + bias).
+ * bias, X dtypes and flags as for inv_hip_linear; gate/up weights are
+ * rejected.  With host pointers Y is copied in, updated and copied back. */
+int inv_hip_linear_gated_add(const void *X, int x_dtype, inv_weight_t W, const float *bias,
+                             const float *gate, float *Y, int64_t M, int64_t K, int64_t N, int flags);
+
 /* ---- the CBLAS slots ------------------------------------------------------ */
 /* Exactly the signature of TQNNSingleOPS.cblas_sgemm (src/quicknncpu.pas:
  * 102-103): C = alpha * op(A) . op(B) + beta * C on host fp32 arrays, RowMajor

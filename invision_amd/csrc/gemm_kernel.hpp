@@ -1,6 +1,6 @@
 // gemm_kernel.hpp -- bf16 "NT" GEMM for gfx950 (CDNA4) on MFMA 32x32x16.
 //
-//   Y[m, n] = epilogue( alpha * sum_k X[m, k] * W[n, k]  (+ bias[n])  (+ beta * C[m, n]) )
+//   Y[m, n] = epilogue( alpha * sum_k X[m, k] * W[n, k]  (+ bias[n]) ) (* colscale[n])  (+ beta * C[m, n])
 //
 // X [M x K] and W [N x K] are bf16, row-major, K contiguous (the layout of the
 // reference's QNNLinear: cblas_gemm(RowMajor, NoTrans, Trans, ...),
@@ -69,6 +69,7 @@ struct GemmParams {
     float alpha, beta;
     int has_bias, vec_store;
     int nout;             // EPI_SWIGLU: output columns (N = its padded gate+up row count)
+    const float *colscale;  // [N] or null: Y = epi(alpha*acc + bias) * colscale[n] (+ beta*C)
     float *partial;       // split/stream-K partial sums (uncached device memory)
     unsigned *counters;   // arrival counters, one per tile, zero between calls (uncached)
 };
@@ -678,7 +679,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
     const int rsub = lane / LPR;
     const int n = n0 + wn * C::WTN + col;
     const bool nvec = p.vec_store && n + 3 < p.N;
-    float bv[4] = {0.f, 0.f, 0.f, 0.f};
+    float bv[4] = {0.f, 0.f, 0.f, 0.f}, sc[4] = {1.f, 1.f, 1.f, 1.f};
     if (p.has_bias) {
         if (n + 3 < p.N) {
             const f32x4_t t = *(const f32x4_t *)(p.bias + n);  // bias is 16-byte aligned, n % 4 == 0
@@ -688,6 +689,10 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
 #pragma unroll
             for (int e = 0; e < 4; ++e) bv[e] = (n + e < p.N) ? p.bias[n + e] : 0.f;
         }
+    }
+    if (p.colscale) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[e] = (n + e < p.N) ? p.colscale[n + e] : 0.f;
     }
     // The bias has landed before the first store: a later wait for it would
     // also wait for every store issued before it.
@@ -714,19 +719,20 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
         const int mrow = m0 + wm * C::WTM + j * 32 + rsub;  // row of it = 0; it adds RPI rows
         if (nvec && mrow + (NIT - 1) * RPI < p.M) {
             // every row of this lane in range, 16-byte aligned: no branches
+            f32x4_t cv[BETA ? NIT : 1];
             if constexpr (BETA) {
-                f32x4_t cv[NIT];
 #pragma unroll
                 for (int it = 0; it < NIT; ++it)
                     cv[it] = *(const f32x4_t *)(p.Cin + (int64_t)(mrow + it * RPI) * p.ldc + n);
-#pragma unroll
-                for (int it = 0; it < NIT; ++it) t[it] += p.beta * cv[it];
             }
 #pragma unroll
             for (int it = 0; it < NIT; ++it) {
                 float v[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = epilogue_op<EPI>(t[it][e] + bv[e]);
+                for (int e = 0; e < 4; ++e) {
+                    v[e] = epilogue_op<EPI>(t[it][e] + bv[e]) * sc[e];
+                    if constexpr (BETA) v[e] += p.beta * cv[it][e];
+                }
                 const int64_t off = (int64_t)(mrow + it * RPI) * p.ldy + n;
                 if constexpr (OUT == OUT_F32) {
                     *reinterpret_cast<f32x4_t *>((float *)p.Y + off) = f32x4_t{v[0], v[1], v[2], v[3]};
@@ -742,14 +748,14 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
             for (int it = 0; it < NIT; ++it) {
                 const int m = mrow + it * RPI;
                 if (m >= p.M) continue;
-                float v[4] = {t[it][0], t[it][1], t[it][2], t[it][3]};
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = epilogue_op<EPI>(t[it][e] + bv[e]) * sc[e];
                 if constexpr (BETA) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         if (n + e < p.N) v[e] += p.beta * p.Cin[(int64_t)m * p.ldc + n + e];
                 }
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = epilogue_op<EPI>(v[e] + bv[e]);
                 if constexpr (OUT == OUT_F32) {
                     float *y = (float *)p.Y + (int64_t)m * p.ldy + n;
 #pragma unroll
@@ -778,12 +784,15 @@ __device__ __forceinline__ void store_tile_direct(const GemmParams &p, const f32
 #pragma unroll
     for (int i = 0; i < C::FN; ++i) {
         const int nb = n0 + wn * C::WTN + i * 32 + 4 * fh;
-        float bv[4][4];
+        float bv[4][4], sc[4][4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int n = nb + 8 * g;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) bv[g][e] = 0.f;
+            for (int e = 0; e < 4; ++e) {
+                bv[g][e] = 0.f;
+                sc[g][e] = p.colscale ? ((n + e < p.N) ? p.colscale[n + e] : 0.f) : 1.f;
+            }
             if (p.has_bias) {
                 if (n + 3 < p.N) {
                     f32x4_t t = *(const f32x4_t *)(p.bias + n);  // bias is 16-byte aligned, n % 4 == 0
@@ -804,14 +813,12 @@ __device__ __forceinline__ void store_tile_direct(const GemmParams &p, const f32
                 const int n = nb + 8 * g;
                 float v[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = p.alpha * acc[i][j][4 * g + e];
+                for (int e = 0; e < 4; ++e) v[e] = epilogue_op<EPI>(p.alpha * acc[i][j][4 * g + e] + bv[g][e]) * sc[g][e];
                 if constexpr (BETA) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         if (n + e < p.N) v[e] += p.beta * p.Cin[(int64_t)m * p.ldc + n + e];
                 }
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = epilogue_op<EPI>(v[e] + bv[g][e]);
                 if constexpr (OUT == OUT_F32) {
                     float *y = (float *)p.Y + (int64_t)m * p.ldy + n;
                     if (p.vec_store && n + 3 < p.N) {

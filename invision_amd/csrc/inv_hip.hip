@@ -78,7 +78,7 @@ struct State {
     void *pin[2] = {nullptr, nullptr};
     int cu_count = 0, clock_khz = 0;
     char name[256] = {0};
-    Buf xin, x16, w16, win, yout, cin, bias;
+    Buf xin, x16, w16, win, yout, cin, bias, gate;
     // Split/stream-K partial sums and arrival counters: uncached device memory
     // (coherent across XCDs without L2 maintenance).  Such memory is never
     // freed once a kernel has read it: outgrown buffers are retired, not freed.
@@ -331,7 +331,8 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
 // W [N x ldw], X [M x ldx] bf16 device; K a multiple of 8 (zero padded).
 int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, void *Y, int64_t ldy, int out,
              const float *bias, const float *Cin, int64_t ldc, float alpha, float beta, int64_t M, int64_t N,
-             int64_t K, int epi, int64_t w_seg_k = 0, int64_t Kw = -1, int64_t nout = -1) {
+             int64_t K, int epi, int64_t w_seg_k = 0, int64_t Kw = -1, int64_t nout = -1,
+             const float *colscale = nullptr) {
     if (M == 0 || N == 0) return INV_OK;
     if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return fail(INV_ERR_ARG, "dimension too large");
     if (K % 8 || ldw % 8 || ldx % 8 || !aligned(W, 16) || !aligned(X, 16))
@@ -368,6 +369,7 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
     p.alpha = alpha;
     p.beta = beta;
     p.has_bias = bias != nullptr;
+    p.colscale = colscale;
     const size_t esz = (out == inv::OUT_F32) ? 4 : 2;
     p.vec_store = (ldy % 4 == 0) && aligned(Y, 4 * esz) && (bias == nullptr || aligned(bias, 16));
     if (bias && !aligned(bias, 16)) return fail(INV_ERR_ARG, "internal: bias not 16-byte aligned");
@@ -663,6 +665,103 @@ int gemm_slot(int order, int transA, int transB, int64_t M, int64_t N, int64_t K
     return INV_OK;
 }
 
+// Y = epilogue(X . W^T + bias), or with accumulate Y += gate[n] * (X . W^T + bias)
+// (gate null: a plain residual add).  Y stays fp32 when accumulating.
+int linear_impl(const char *who, const void *X, int x_dtype, inv_weight_t W, const float *bias, void *Y, int y_dtype,
+                int64_t M, int64_t K, int64_t N, int epilogue, int flags, bool accumulate, const float *gate) {
+    TRY(check_init());
+    if (!valid_weight(W)) return fail(INV_ERR_ARG, "%s: unknown weight handle", who);
+    if (x_dtype != INV_DT_F32 && x_dtype != INV_DT_BF16) return fail(INV_ERR_ARG, "%s: bad x_dtype %d", who, x_dtype);
+    if (y_dtype != INV_DT_F32 && y_dtype != INV_DT_BF16) return fail(INV_ERR_ARG, "%s: bad y_dtype %d", who, y_dtype);
+    if (!epi_ok(epilogue)) return fail(INV_ERR_ARG, "%s: bad epilogue %d", who, epilogue);
+    if (flags & ~(INV_FLAG_DEVICE_PTRS | INV_FLAG_ASYNC | INV_FLAG_PRECISE))
+        return fail(INV_ERR_ARG, "%s: unknown flags 0x%x", who, flags);
+    if ((flags & INV_FLAG_ASYNC) && !(flags & INV_FLAG_DEVICE_PTRS))
+        return fail(INV_ERR_ARG, "%s: ASYNC requires DEVICE_PTRS", who);
+    if (M < 0) return fail(INV_ERR_ARG, "%s: negative M", who);
+    if (K != W->K || N != W->N)
+        return fail(INV_ERR_ARG, "%s: shape mismatch: call K=%lld N=%lld, weight K=%lld N=%lld", who, (long long)K,
+                    (long long)N, (long long)W->K, (long long)W->N);
+    if (accumulate && W->gated) return fail(INV_ERR_ARG, "%s: a gate/up weight has no gated-add form", who);
+    if ((epilogue == INV_EPI_SWIGLU) != (W->gated != 0))
+        return fail(INV_ERR_ARG, W->gated ? "linear: a gate/up weight needs INV_EPI_SWIGLU"
+                                          : "linear: INV_EPI_SWIGLU needs a gate/up weight (inv_hip_weight_upload_gate_up)");
+    if (W->gated && bias) return fail(INV_ERR_ARG, "%s: a gate/up weight takes its biases at upload", who);
+    if (M == 0) return INV_OK;
+    if (!X || !Y) return fail(INV_ERR_ARG, "%s: X or Y is null", who);
+    if (M > INT32_MAX / 2) return fail(INV_ERR_ARG, "%s: M too large", who);
+    const bool dev = (flags & INV_FLAG_DEVICE_PTRS) != 0;
+    const int out = (y_dtype == INV_DT_F32) ? inv::OUT_F32 : inv::OUT_BF16;
+    const size_t ysz = (y_dtype == INV_DT_F32) ? 4 : 2;
+
+    // Activations -> bf16 [M x ldw] (ldw = K rounded up to 8, zero padded), or
+    // with INV_FLAG_PRECISE and fp32 X: [Xh | Xl], each half K rounded up to 64,
+    // multiplied against the resident W read twice (the W k-tiles wrap).
+    const bool precise = (flags & INV_FLAG_PRECISE) && x_dtype == INV_DT_F32;
+    const uint16_t *Xd = nullptr;
+    int64_t ldx = 0;
+    const int64_t kseg = precise ? round_up(K, 64) : W->ldw;
+    TRY(stage_operand(X, x_dtype, dev, false, M, K, K, precise ? 2 : 1, precise ? 0x2 : 0, precise ? 64 : 8, g.x16,
+                      g.xin, &Xd, &ldx));
+
+    // Bias: explicit argument first, else the handle's.
+    const float *bd = W->bias;
+    if (bias) {
+        if (dev && aligned(bias, 16)) {
+            bd = bias;
+        } else {
+            TRY(ensure(g.bias, (size_t)N * 4));
+            if (dev)
+                HIPCHK(hipMemcpyAsync(g.bias.p, bias, (size_t)N * 4, hipMemcpyDeviceToDevice, g.stream));
+            else
+                TRY(h2d_rows(g.bias.p, bias, 1, (size_t)N * 4, (size_t)N * 4));
+            bd = (const float *)g.bias.p;
+        }
+    }
+
+    // Gate: per-column scale of the projection (device pointers are used as
+    // they are; a host gate is copied next to the bias).
+    const float *gd = nullptr;
+    if (accumulate && gate) {
+        if (dev && aligned(gate, 4)) {
+            gd = gate;
+        } else {
+            TRY(ensure(g.gate, (size_t)N * 4));
+            if (dev)
+                HIPCHK(hipMemcpyAsync(g.gate.p, gate, (size_t)N * 4, hipMemcpyDeviceToDevice, g.stream));
+            else
+                TRY(h2d_rows(g.gate.p, gate, 1, (size_t)N * 4, (size_t)N * 4));
+            gd = (const float *)g.gate.p;
+        }
+    }
+
+    void *Yd = Y;
+    if (!dev) {
+        TRY(ensure(g.yout, (size_t)(M * N) * ysz));
+        Yd = g.yout.p;
+        if (accumulate) TRY(h2d_rows(Yd, Y, M, (size_t)N * ysz, (size_t)N * ysz));
+    }
+    // Accumulating reads Y as C (beta = 1) in place: every element is read and
+    // then written by the one thread that finishes its tile.
+    const float *cin = accumulate ? (const float *)Yd : nullptr;
+    const float beta = accumulate ? 1.0f : 0.0f;
+    // The GEMM runs over the handle's device rows (2 x 128-padded N for a
+    // gate/up pair); Y has N columns either way.
+    if (precise)
+        TRY(run_gemm(W->w, W->ldw, Xd, ldx, Yd, N, out, bd, cin, N, 1.0f, beta, M, W->rows, 2 * kseg, epilogue,
+                     kseg, W->ldw, N, gd));
+    else
+        TRY(run_gemm(W->w, W->ldw, Xd, ldx, Yd, N, out, bd, cin, N, 1.0f, beta, M, W->rows, W->ldw, epilogue,
+                     0, -1, N, gd));
+    g.calls++;
+    if (!dev) {
+        TRY(d2h_rows(Y, Yd, M, (size_t)N * ysz, (size_t)N * ysz));
+    } else if (!(flags & INV_FLAG_ASYNC)) {
+        HIPCHK(hipStreamSynchronize(g.stream));
+    }
+    return INV_OK;
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -720,7 +819,7 @@ int inv_hip_shutdown(void) {
     (void)hipStreamSynchronize(g.stream);
     for (auto *w : g.weights) free_weight(w);
     g.weights.clear();
-    for (Buf *b : {&g.xin, &g.x16, &g.w16, &g.win, &g.yout, &g.cin, &g.bias}) release(*b);
+    for (Buf *b : {&g.xin, &g.x16, &g.w16, &g.win, &g.yout, &g.cin, &g.bias, &g.gate}) release(*b);
     // g.partial / g.counters (uncached) stay allocated until the process ends.
     for (int k = 0; k < 2; ++k) {
         if (g.pin[k]) (void)hipHostFree(g.pin[k]);
@@ -845,75 +944,14 @@ int inv_hip_weight_shape(inv_weight_t w, int64_t *N, int64_t *K) {
 int inv_hip_linear(const void *X, int x_dtype, inv_weight_t W, const float *bias, void *Y, int y_dtype, int64_t M,
                    int64_t K, int64_t N, int epilogue, int flags) {
     std::lock_guard<std::mutex> lk(g_mu);
-    TRY(check_init());
-    if (!valid_weight(W)) return fail(INV_ERR_ARG, "linear: unknown weight handle");
-    if (x_dtype != INV_DT_F32 && x_dtype != INV_DT_BF16) return fail(INV_ERR_ARG, "linear: bad x_dtype %d", x_dtype);
-    if (y_dtype != INV_DT_F32 && y_dtype != INV_DT_BF16) return fail(INV_ERR_ARG, "linear: bad y_dtype %d", y_dtype);
-    if (!epi_ok(epilogue)) return fail(INV_ERR_ARG, "linear: bad epilogue %d", epilogue);
-    if (flags & ~(INV_FLAG_DEVICE_PTRS | INV_FLAG_ASYNC | INV_FLAG_PRECISE))
-        return fail(INV_ERR_ARG, "linear: unknown flags 0x%x", flags);
-    if ((flags & INV_FLAG_ASYNC) && !(flags & INV_FLAG_DEVICE_PTRS))
-        return fail(INV_ERR_ARG, "linear: ASYNC requires DEVICE_PTRS");
-    if (M < 0) return fail(INV_ERR_ARG, "linear: negative M");
-    if (K != W->K || N != W->N)
-        return fail(INV_ERR_ARG, "linear: shape mismatch: call K=%lld N=%lld, weight K=%lld N=%lld", (long long)K,
-                    (long long)N, (long long)W->K, (long long)W->N);
-    if ((epilogue == INV_EPI_SWIGLU) != (W->gated != 0))
-        return fail(INV_ERR_ARG, W->gated ? "linear: a gate/up weight needs INV_EPI_SWIGLU"
-                                          : "linear: INV_EPI_SWIGLU needs a gate/up weight (inv_hip_weight_upload_gate_up)");
-    if (W->gated && bias) return fail(INV_ERR_ARG, "linear: a gate/up weight takes its biases at upload");
-    if (M == 0) return INV_OK;
-    if (!X || !Y) return fail(INV_ERR_ARG, "linear: X or Y is null");
-    if (M > INT32_MAX / 2) return fail(INV_ERR_ARG, "linear: M too large");
-    const bool dev = (flags & INV_FLAG_DEVICE_PTRS) != 0;
-    const int out = (y_dtype == INV_DT_F32) ? inv::OUT_F32 : inv::OUT_BF16;
-    const size_t ysz = (y_dtype == INV_DT_F32) ? 4 : 2;
+    return linear_impl("linear", X, x_dtype, W, bias, Y, y_dtype, M, K, N, epilogue, flags, false, nullptr);
+}
 
-    // Activations -> bf16 [M x ldw] (ldw = K rounded up to 8, zero padded), or
-    // with INV_FLAG_PRECISE and fp32 X: [Xh | Xl], each half K rounded up to 64,
-    // multiplied against the resident W read twice (the W k-tiles wrap).
-    const bool precise = (flags & INV_FLAG_PRECISE) && x_dtype == INV_DT_F32;
-    const uint16_t *Xd = nullptr;
-    int64_t ldx = 0;
-    const int64_t kseg = precise ? round_up(K, 64) : W->ldw;
-    TRY(stage_operand(X, x_dtype, dev, false, M, K, K, precise ? 2 : 1, precise ? 0x2 : 0, precise ? 64 : 8, g.x16,
-                      g.xin, &Xd, &ldx));
-
-    // Bias: explicit argument first, else the handle's.
-    const float *bd = W->bias;
-    if (bias) {
-        if (dev && aligned(bias, 16)) {
-            bd = bias;
-        } else {
-            TRY(ensure(g.bias, (size_t)N * 4));
-            if (dev)
-                HIPCHK(hipMemcpyAsync(g.bias.p, bias, (size_t)N * 4, hipMemcpyDeviceToDevice, g.stream));
-            else
-                TRY(h2d_rows(g.bias.p, bias, 1, (size_t)N * 4, (size_t)N * 4));
-            bd = (const float *)g.bias.p;
-        }
-    }
-
-    void *Yd = Y;
-    if (!dev) {
-        TRY(ensure(g.yout, (size_t)(M * N) * ysz));
-        Yd = g.yout.p;
-    }
-    // The GEMM runs over the handle's device rows (2 x 128-padded N for a
-    // gate/up pair); Y has N columns either way.
-    if (precise)
-        TRY(run_gemm(W->w, W->ldw, Xd, ldx, Yd, N, out, bd, nullptr, 0, 1.0f, 0.0f, M, W->rows, 2 * kseg, epilogue,
-                     kseg, W->ldw, N));
-    else
-        TRY(run_gemm(W->w, W->ldw, Xd, ldx, Yd, N, out, bd, nullptr, 0, 1.0f, 0.0f, M, W->rows, W->ldw, epilogue,
-                     0, -1, N));
-    g.calls++;
-    if (!dev) {
-        TRY(d2h_rows(Y, Yd, M, (size_t)N * ysz, (size_t)N * ysz));
-    } else if (!(flags & INV_FLAG_ASYNC)) {
-        HIPCHK(hipStreamSynchronize(g.stream));
-    }
-    return INV_OK;
+int inv_hip_linear_gated_add(const void *X, int x_dtype, inv_weight_t W, const float *bias, const float *gate,
+                             float *Y, int64_t M, int64_t K, int64_t N, int flags) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return linear_impl("linear_gated_add", X, x_dtype, W, bias, Y, INV_DT_F32, M, K, N, INV_EPI_NONE, flags, true,
+                       gate);
 }
 
 int inv_hip_set_sgemm_precision(int mode) {

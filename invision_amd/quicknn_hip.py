@@ -236,6 +236,40 @@ def linear(x: np.ndarray, W: Weight, bias: Optional[np.ndarray] = None, epilogue
     return y
 
 
+def linear_gated_add_device(x: DeviceArray, W: Weight, y: DeviceArray, M: int, gate: Optional[DeviceArray] = None,
+                            bias: Optional[DeviceArray] = None, asynchronous: bool = False,
+                            precise: bool = False) -> None:
+    """inv_hip_linear_gated_add on resident buffers: y += gate * (x . W^T + bias), y fp32 [M x N]."""
+    if y.inv_dtype != hip.INV_DT_F32:
+        raise TypeError("the residual stream y must be f32")
+    flags = hip.INV_FLAG_DEVICE_PTRS | (hip.INV_FLAG_ASYNC if asynchronous else 0)
+    flags |= hip.INV_FLAG_PRECISE if precise else 0
+    hip.call("inv_hip_linear_gated_add", x.ptr, x.inv_dtype, W.handle, bias.ptr if bias is not None else None,
+             gate.ptr if gate is not None else None, y.ptr, M, W.K, W.N, flags)
+
+
+def linear_gated_add(y: np.ndarray, x: np.ndarray, W: Weight, gate: Optional[np.ndarray],
+                     bias: Optional[np.ndarray] = None, precise: bool = False) -> np.ndarray:
+    """Host arrays, y updated in place: y[M x N] += gate[N] * (x[M x K] . W^T + bias)."""
+    if x.dtype not in (np.float32, np.uint16):
+        raise TypeError("x must be float32 or bf16 bits (uint16)")
+    _check_host(y, np.float32, "y")
+    x = np.ascontiguousarray(x)
+    M = x.shape[0]
+    if x.ndim != 2 or x.shape[1] != W.K:
+        raise ValueError(f"x must be [M x {W.K}]")
+    if y.shape != (M, W.N):
+        raise ValueError(f"y must be [{M} x {W.N}]")
+    xdt = hip.INV_DT_F32 if x.dtype == np.float32 else hip.INV_DT_BF16
+    g = np.ascontiguousarray(gate, dtype=np.float32) if gate is not None else None
+    if g is not None and g.size != W.N:
+        raise ValueError(f"gate must have {W.N} values")
+    b = np.ascontiguousarray(bias, dtype=np.float32) if bias is not None else None
+    hip.call("inv_hip_linear_gated_add", _ptr(x), xdt, W.handle, _ptr(b) if b is not None else None,
+             _ptr(g) if g is not None else None, _ptr(y), M, W.K, W.N, hip.INV_FLAG_PRECISE if precise else 0)
+    return y
+
+
 def set_sgemm_precision(mode: int) -> None:
     """INV_PREC_BF16 / INV_PREC_SPLIT_A / INV_PREC_SPLIT_AB for cblas_gemm."""
     init()
@@ -356,6 +390,35 @@ def QNNLINEAR_BF16_OR_F32(dst: np.ndarray, src: np.ndarray, weight, weight_bf16,
         QNNLinearNoBias_BF16(dst, src, weight_bf16, seq, srcDim, dstDim)
     else:
         QNNLinearNoBias(dst, src, weight, seq, srcDim, dstDim)
+
+
+def QNNLinearGatedAdd(dst: np.ndarray, src: np.ndarray, weight, weight_bf16, gate: np.ndarray, seq: int,
+                      srcDim: int, dstDim: int) -> None:
+    """QNNLINEAR_BF16_OR_F32 into a scratch projection followed by QNNGatedAdd
+    (src/quicknn_transformers.pas:1432-1438), as one GEMM: dst += gate * src . W^T."""
+    _bound(weight is not None or weight_bf16 is not None,
+           "ERROR QNNLINEAR_BF16_OR_F32 : no weight or weight_16 assigned!")
+    _check_host(dst, np.float32, "dst")
+    _check_host(src, np.float32, "src")
+    _bound(src.size >= seq * srcDim, "ERROR : QNNLinear out of bound [x]")
+    _bound(dst.size >= seq * dstDim, "ERROR : QNNLinear out of bound [dst]")
+    W = weight_bf16 if weight_bf16 is not None else weight
+    if not isinstance(W, Weight) and weight_bf16 is not None:
+        _check_host(W, np.uint16, "W")
+    w = _linear_weight(W)
+    try:
+        _bound(w.N == dstDim and w.K == srcDim, "ERROR : QNNLinear weight shape mismatch")
+        _bound(not w.has_bias, "ERROR : QNNLINEAR_BF16_OR_F32 takes no bias")
+        g = None
+        if gate is not None:
+            _check_host(gate, np.float32, "gate")
+            _bound(gate.size >= dstDim, "ERROR : QNNGatedAdd out of bound [gate]")
+            g = gate
+        hip.call("inv_hip_linear_gated_add", _ptr(src), hip.INV_DT_F32, w.handle, None,
+                 _ptr(g) if g is not None else None, _ptr(dst), seq, srcDim, dstDim, 0)
+    finally:
+        if w is not W:
+            w.free()
 
 
 def _weight_has_bias(W: Weight) -> bool:

@@ -19,6 +19,8 @@ How each oracle function is pinned:
     closed forms (math.exp / math.erf), the polynomial's value at fixed points,
     and the documented error bound of the reference approximation.
   * linear (quicknncpu.pas:1807-1847): closed form with bias.
+  * gated add (quicknncpu.pas:853-859): numpy's fp32 elementwise product and
+    sum (bit-exact), gate = 0 leaves dst unchanged, gate = 1 is dst + proj.
 """
 from __future__ import annotations
 
@@ -78,6 +80,7 @@ def lib() -> ctypes.CDLL:
         L.orc_fast_exp.argtypes = [c_float]
         L.orc_silu_qnn.argtypes = [c_int64, c_void_p, c_void_p, c_void_p, c_void_p]
         L.orc_apply_epilogue.argtypes = [c_void_p, c_int64, c_int]
+        L.orc_gated_add.argtypes = [c_void_p, c_void_p, c_void_p, c_int64, c_int64]
         L.orc_add_bias_rows.argtypes = [c_void_p, c_void_p, c_int64, c_int64]
         L.orc_has_avx2.restype = c_int
         L.orc_max_threads.restype = c_int
@@ -209,6 +212,18 @@ def apply_epilogue(Y: np.ndarray, epilogue: int) -> np.ndarray:
     Y = np.ascontiguousarray(Y, dtype=np.float32).copy()
     lib().orc_apply_epilogue(_p(Y), Y.size, epilogue)
     return Y
+
+
+def gated_add(dst: np.ndarray, gate: np.ndarray, proj: np.ndarray) -> np.ndarray:
+    """QNNGatedAdd (quicknncpu.pas:853-859) on a copy of dst: dst + gate[j] * proj."""
+    d = np.ascontiguousarray(dst, dtype=np.float32).copy()
+    g = np.ascontiguousarray(gate, dtype=np.float32)
+    pr = np.ascontiguousarray(proj, dtype=np.float32)
+    seq, hidden = d.shape
+    if pr.shape != d.shape or g.size != hidden:
+        raise ValueError("gated_add: shapes")
+    lib().orc_gated_add(_p(d), _p(g), _p(pr), seq, hidden)
+    return d
 
 
 def silu_qnn(x: np.ndarray, up=None):

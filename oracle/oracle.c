@@ -452,6 +452,16 @@ void orc_apply_epilogue(float *Y, int64_t n, int epilogue) {
     }
 }
 
+/* QNNGatedAdd: quicknncpu.pas:853-859, one QNNAccMul (:1752-1758) per row:
+ * dst[i][j] = dst[i][j] + gate[j] * proj[i][j], product rounded to fp32 first. */
+void orc_gated_add(float *dst, const float *gate, const float *proj, int64_t seq, int64_t hidden) {
+    for (int64_t i = 0; i < seq; ++i)
+        for (int64_t j = 0; j < hidden; ++j) {
+            const float t = gate[j] * proj[i * hidden + j];
+            dst[i * hidden + j] = dst[i * hidden + j] + t;
+        }
+}
+
 /* QNNLinear / QNNLinearNoBias_BF16 / QNNLINEAR_BF16_OR_F32:
  * quicknncpu.pas:1807-1847, 3062-3071.  The bf16 weight is widened into a
  * workspace (:1842-1844), then cblas_gemm(RowMajor, NoTrans, Trans, M, N, K,

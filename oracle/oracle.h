@@ -71,6 +71,8 @@ float orc_fast_exp(float x);
 /* ---- CBLAS-shaped epilogue helpers used by the tests ---------------------- */
 void orc_add_bias_rows(float *Y, const float *bias, int64_t M, int64_t N); /* QNNAddInplace per row */
 void orc_apply_epilogue(float *Y, int64_t n, int epilogue);
+/* QNNGatedAdd (quicknncpu.pas:853-859): dst[i][j] += gate[j] * proj[i][j]. */
+void orc_gated_add(float *dst, const float *gate, const float *proj, int64_t seq, int64_t hidden);
 
 int orc_has_avx2(void);
 int orc_max_threads(void);

@@ -265,6 +265,19 @@ def test_linear_bias_is_added_per_row():
     np.testing.assert_allclose(y1 - y0, np.broadcast_to(b, (3, 5)), rtol=0, atol=1e-5)
 
 
+def test_gated_add_against_numpy_and_special_gates():
+    d, pr = _rand((7, 33), 40), _rand((7, 33), 41)
+    g = _rand((33,), 42)
+    got = oracle.gated_add(d, g, pr)
+    # numpy's fp32 ops round the product, then the sum: the loop's own order
+    np.testing.assert_array_equal(got, d + (g[None, :] * pr))
+    np.testing.assert_array_equal(oracle.gated_add(d, np.zeros(33, np.float32), pr), d)
+    np.testing.assert_array_equal(oracle.gated_add(d, np.ones(33, np.float32), pr), d + pr)
+    # the gate indexes columns, not rows: a row-indexed gate differs
+    g_rows = np.resize(g, 7)
+    assert not np.array_equal(got, d + g_rows[:, None] * pr)
+
+
 # ------------------------------------------------------- planted mistakes --
 
 def test_checks_catch_planted_mistakes():
