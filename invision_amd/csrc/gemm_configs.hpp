@@ -26,9 +26,11 @@
 #define INV_CFG_8 inv::RsCfg<256, 256, 2, 2, 2> /* 4 waves of 128x128, two register stages */
 #define INV_CFG_9 inv::RsCfg<256, 256, 2, 2, 1> /* same, one register stage */
 #define INV_CFG_10 inv::RsCfg<256, 256, 2, 2, 1, 2> /* one register stage, fragments two substeps ahead */
+#define INV_CFG_11 inv::RsCfg<256, 224, 4, 1, 2> /* 4 waves of 64x224 (W rows x X rows) */
+#define INV_CFG_12 inv::RsCfg<224, 256, 1, 4, 2> /* 4 waves of 224x64 */
 
-#define INV_GEMM_CONFIG_IDS(X) X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10)
-#define INV_GEMM_NUM_CONFIGS 11
+#define INV_GEMM_CONFIG_IDS(X) X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10) X(11) X(12)
+#define INV_GEMM_NUM_CONFIGS 13
 
 namespace inv {
 struct GemmParams;

@@ -159,7 +159,9 @@ struct TileCfg {
     static_assert((NTHREADS / SLOTS) % 16 == 0, "copy rows must advance in multiples of 16");
     static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
     static_assert(KSUB % 2 == 0, "register double-buffering alternates over an even substep count");
-    static constexpr bool STAGED_EPI = NWAVES * 32 * (WTN + 4) * 4 <= LDS_BYTES;
+    // The staged epilogue reads rows of WTN floats with WTN/4 lanes each, so a
+    // whole number of rows must fill a wave.
+    static constexpr bool STAGED_EPI = NWAVES * 32 * (WTN + 4) * 4 <= LDS_BYTES && 64 % (WTN / 4) == 0;
     static constexpr bool SWIGLU_OK = STAGED_EPI && TN == 256 && WN == 2;  // wave columns = gate | up
 };
 
@@ -194,7 +196,9 @@ struct RsCfg {
     static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
     static_assert(NREG == 1 || NREG == 2, "one or two register stages");
     static_assert(PF == 1 || PF == 2, "fragment prefetch distance 1 or 2 substeps");
-    static constexpr bool STAGED_EPI = NWAVES * 32 * (WTN + 4) * 4 <= LDS_BYTES;
+    // The staged epilogue reads rows of WTN floats with WTN/4 lanes each, so a
+    // whole number of rows must fill a wave.
+    static constexpr bool STAGED_EPI = NWAVES * 32 * (WTN + 4) * 4 <= LDS_BYTES && 64 % (WTN / 4) == 0;
     static constexpr bool SWIGLU_OK = STAGED_EPI && TN == 256 && WN == 2;  // wave columns = gate | up
     static_assert(NREG * LOADS - 1 < 64, "vmcnt holds at most 63 outstanding loads");
 };
@@ -544,7 +548,7 @@ __device__ __forceinline__ void mainloop_rs(const GemmParams &p, lds_char_t *lds
         return __builtin_amdgcn_raw_buffer_load_b128(rsx, b_base + (cidx - AL) * b_step + kb, 0, 0);
     };
     auto lds_chunk = [&](lds_char_t *buf, int cidx) -> u32x4_t * {
-        return (u32x4_t *)(buf + (cidx < AL ? 0 : C::A_BYTES) + wr_off + (cidx % AL) * RPL * ROWB);
+        return (u32x4_t *)(buf + (cidx < AL ? 0 : C::A_BYTES) + wr_off + (cidx < AL ? cidx : cidx - AL) * RPL * ROWB);
     };
 
     u32x4_t R0[L], R1[C::NREG == 2 ? L : 1];
@@ -672,6 +676,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
     constexpr int SROW = C::WTN + 4;       // staged row pitch in floats
     constexpr int LPR = C::WTN / 4;        // lanes per row on the read side
     constexpr int RPI = 64 / LPR;          // rows per read instruction
+    static_assert(LPR * RPI == 64 && 32 % RPI == 0, "whole rows per wave-wide read");
     const int frow = lane & 31;
     const int fh = lane >> 5;
     lds_float_t *st = (lds_float_t *)lds + wave * 32 * SROW;
