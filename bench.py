@@ -199,6 +199,32 @@ def run_workload(name, steps, warmup, check=True, host_path=False, warmup_second
     return res
 
 
+def mfma_ceiling(gemm_tflops):
+    """The register-only MFMA loop of libinv_probe.so on this GPU, now: the rate a
+    GEMM on the same operand distributions could reach with zero memory traffic
+    under the board's power limit, and the same with constant operands."""
+    import ctypes
+    from invision_amd import build as B
+    if not os.path.exists(B.PROBE_PATH):
+        log("[bench] libinv_probe.so not built: no MFMA ceiling")
+        return None
+    lib = ctypes.CDLL(B.PROBE_PATH)
+    lib.inv_probe_mfma_ceiling.restype = ctypes.c_int
+    lib.inv_probe_mfma_ceiling.argtypes = [ctypes.c_double, ctypes.c_double, ctypes.POINTER(ctypes.c_double),
+                                           ctypes.POINTER(ctypes.c_double)]
+    r, c = ctypes.c_double(), ctypes.c_double()
+    rc = lib.inv_probe_mfma_ceiling(1.0, 1.0, ctypes.byref(r), ctypes.byref(c))
+    if rc != 0:
+        log(f"[bench] MFMA ceiling probe failed ({rc})")
+        return None
+    out = {"random_operands_tflops": round(r.value, 1), "constant_operands_tflops": round(c.value, 1),
+           "gemm_frac_of_random_ceiling": round(gemm_tflops / r.value, 4),
+           "what": "v_mfma_f32_32x32x16_bf16 over a 128x128 wave tile from registers only, 1 wave/SIMD, all CUs, "
+                   "sustained 1 s; W ~ N(0,0.02) and X ~ N(0,1) in bf16, or constant operands"}
+    log(f"[bench] MFMA ceiling: {json.dumps(out)}")
+    return out
+
+
 def cpu_baseline(name):
     """The reference's CPU GEMM on this host's cores (bounded: the c2 GEMM itself)."""
     import oracle
@@ -374,6 +400,8 @@ def main():
     ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
     ap.add_argument("--all", action="store_true", help="also time every workload shape (stderr)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-mfma-ceiling", action="store_true",
+                    help="skip the register-only MFMA ceiling measured on the same GPU (~5 s)")
     ap.add_argument("--profile-run", action="store_true",
                     help="for rocprofv3 passes: a 512 MiB copy-kernel calibration (5 launches), then --steps "
                          "launches of the workload; no CPU baseline")
@@ -400,6 +428,7 @@ def main():
                 r = run_workload(name, max(5, args.steps // 2), 3, warmup_seconds=min(args.warmup_seconds, 0.5))
                 log(f"[bench] {json.dumps(r)}")
 
+    ceiling = None if args.no_mfma_ceiling else mfma_ceiling(res["tflops_kernel"])
     desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[args.workload]
     achieved = res["tflops_kernel"]
     traffic = None
@@ -432,6 +461,7 @@ def main():
         "launch_ms_p10_p50_p90": res["launch_ms_p10_p50_p90"],
         "host_fp32_io_tflops": round(res["host_fp32_io_tflops"], 2) if "host_fp32_io_tflops" in res else None,
         "device": info["name"],
+        "mfma_ceiling": ceiling,
     }
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")

@@ -18,6 +18,8 @@ ROOT = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libinvision_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+PROBE_NAME = "libinv_probe.so"  # the MFMA-ceiling measurement aid (not the linear-layer ABI)
+PROBE_PATH = os.path.join(PKG_DIR, PROBE_NAME)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -52,6 +54,12 @@ def compile_jobs() -> list[tuple[list[str], str]]:
     return jobs
 
 
+def probe_job() -> tuple[list[str], str]:
+    """hipcc command building libinv_probe.so straight from its one source."""
+    return ([HIPCC] + COMMON_FLAGS + ["-shared", os.path.join(CSRC, "mfma_ceiling.hip"), "-o", PROBE_PATH + ".tmp"],
+            PROBE_PATH)
+
+
 def _run(cmd: list[str]) -> tuple[int, str, list[str]]:
     res = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the packed-fp32 feature; that warning is harmless.
@@ -69,7 +77,11 @@ def build_lib(verbose: bool = True, jobs: int = 0) -> str:
     todo = compile_jobs()
     workers = jobs or min(len(todo), max(1, min(16, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=workers) as ex:
-        results = list(ex.map(lambda j: _run(j[0]), todo))
+        results = list(ex.map(lambda j: _run(j[0]), todo + [probe_job()]))
+    results, probe_res = results[:-1], results[-1]
+    if probe_res[0] != 0:
+        raise RuntimeError(f"hipcc failed ({probe_res[0]}):\n{' '.join(probe_res[2])}\n{probe_res[1]}")
+    os.replace(PROBE_PATH + ".tmp", PROBE_PATH)
     for rc, err, cmd in results:
         if rc != 0:
             raise RuntimeError(f"hipcc failed ({rc}):\n{' '.join(cmd)}\n{err}")

@@ -91,12 +91,35 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
 }
 
+// The epilogue's transcendental functions on the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32, about 1 ulp each) instead of the correctly rounded
+// library expf / division / erff, whose range reduction and Newton steps cost
+// several times more VALU work than the whole rest of the epilogue.
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+__device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// x * sigmoid(x): a few ulp from the exact value; 0 for x -> -inf, x for x -> +inf.
+__device__ __forceinline__ float silu(float x) { return x * rcp_fast(1.0f + exp_fast(-x)); }
+
+// 0.5 x (1 + erf(x / sqrt 2)) with erfc from Abramowitz & Stegun 7.1.26
+// (Handbook of Mathematical Functions, |error of erf| <= 1.5e-7):
+// erfc(z) ~ t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2), t = 1 / (1 + p z), z >= 0.
+// For x < 0 the factor 1 + erf is erfc(|z|) itself, so no cancellation.
+__device__ __forceinline__ float gelu_erf(float x) {
+    const float z = fabsf(x) * 0.70710678118654752f;
+    const float t = rcp_fast(fmaf(0.3275911f, z, 1.0f));
+    const float poly =
+        t * fmaf(t, fmaf(t, fmaf(t, fmaf(t, 1.061405429f, -1.453152027f), 1.421413741f), -0.284496736f), 0.254829592f);
+    const float q = poly * exp_fast(-z * z);  // erfc(z)
+    return 0.5f * x * (x >= 0.0f ? 2.0f - q : q);
+}
+
 template <int EPI>
 __device__ __forceinline__ float epilogue_op(float v) {
     if constexpr (EPI == EPI_SILU) {
-        return v / (1.0f + expf(-v));
+        return silu(v);
     } else if constexpr (EPI == EPI_GELU) {
-        return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+        return gelu_erf(v);
     } else {
         return v;
     }
@@ -914,7 +937,7 @@ __device__ __forceinline__ void store_tile_swiglu(const GemmParams &p, lds_char_
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float gt = gv[it][e] + bg[e];
-                v[e] = gt / (1.0f + expf(-gt)) * (uv[it][e] + bu[e]);
+                v[e] = silu(gt) * (uv[it][e] + bu[e]);
             }
             if (m >= p.M) continue;
             const int64_t off = (int64_t)m * p.ldy + f;

@@ -68,3 +68,11 @@ def test_missing_library_raises_instead_of_falling_back(monkeypatch, tmp_path):
     monkeypatch.setattr(h, "_lib", None)
     with pytest.raises(h.HipLibraryError):
         h.load()
+
+
+def test_mfma_ceiling_probe_library_loads():
+    """The bench's measurement aid is a separate library, outside the linear-layer ABI."""
+    from invision_amd import build as B
+    lib = ctypes.CDLL(B.PROBE_PATH)
+    assert hasattr(lib, "inv_probe_mfma_ceiling")
+    assert not hasattr(hip.load(), "inv_probe_mfma_ceiling")
