@@ -19,7 +19,15 @@
  *  - the bf16 weight source  TSafeTensorFile.getTensorDataMemBlockBF16
  *    (src/safetensor.pas:650-683), whose mmap pointer feeds
  *    inv_hip_weight_upload once, instead of the per-call widening at
- *    src/quicknncpu.pas:1842-1844.
+ *    src/quicknncpu.pas:1842-1844; the safetensors reader itself
+ *    (src/safetensor.pas:466-513, 584-683) by inv_hip_weight_load_safetensors;
+ *  - ffnSwigluForward's gate/up projections + QNNSiluMul
+ *    (src/quicknn_transformers.pas:1331-1334) by INV_EPI_SWIGLU, and the
+ *    projection + QNNGatedAdd (src/quicknncpu.pas:853-859) by
+ *    inv_hip_linear_gated_add;
+ *  - QNNFlashAttention and the per-head attention loops
+ *    (src/quicknncpu.pas:2763; src/quicknn_transformers.pas:1150-1311) by
+ *    inv_hip_attention.
  */
 #ifndef INV_HIP_H
 #define INV_HIP_H
@@ -56,10 +64,10 @@ extern "C" {
 
 /* ---- epilogues fused into the GEMM's store ------------------------------- */
 #define INV_EPI_NONE      0 /* Y = acc (+bias)                                            */
-#define INV_EPI_SILU      1 /* Y = silu(acc + bias), exact: v / (1 + exp(-v))              */
+#define INV_EPI_SILU      1 /* Y = silu(acc + bias) = v * rcp(1 + exp2(-v log2 e)), hw ops */
 #define INV_EPI_GELU_ERF  2 /* Y = 0.5 v (1 + erf(v / sqrt 2)); the reference has no GELU */
 #define INV_EPI_SWIGLU    3 /* gate/up weight only (inv_hip_weight_upload_gate_up):
-                               Y = silu(X.Wg^T + bg) * (X.Wu^T + bu), exact SiLU -- the two
+                               Y = silu(X.Wg^T + bg) * (X.Wu^T + bu), SiLU as above -- the two
                                projections and QNNSiluMul of ffnSwigluForward
                                (src/quicknn_transformers.pas:1331-1334, src/quicknncpu.pas:
                                2404-2418) in one GEMM; Y has F columns */
@@ -167,6 +175,30 @@ int inv_hip_linear(const void *X, int x_dtype, inv_weight_t W, const float *bias
  * rejected.  With host pointers Y is copied in, updated and copied back. */
 int inv_hip_linear_gated_add(const void *X, int x_dtype, inv_weight_t W, const float *bias,
                              const float *gate, float *Y, int64_t M, int64_t K, int64_t N, int flags);
+
+/* ---- attention ------------------------------------------------------------ */
+#define INV_ATTN_CAUSAL 0x100 /* key j is visible to query i iff j <= i + (seq_k - seq_q) */
+/* O = softmax(scale * Q . K^T) . V for every head, in the reference's
+ * [tokens x heads*head_dim] layout: Q [seq_q x heads*head_dim], K and V
+ * [seq_k x kv_heads*head_dim], O [seq_q x heads*head_dim], all row-major; head h
+ * uses kv head h / (heads / kv_heads).
+ * Replaces TQNNSingleOPS.QNNFlashAttention(dst, Q, K, V, heads, seq_q, seq_k,
+ * head_dim, scale) (src/quicknncpu.pas:2763, reached via src/quicknn_kernels.pas:
+ * 1655-1663; its callers pass heads first, src/quicknn_transformers.pas:1203,
+ * 1275-1276) and the per-head cblas_gemm + QNNSoftmaxRows + cblas_gemm loops of
+ * multiHeadForward / jointAttentionForward (src/quicknn_transformers.pas:
+ * 1150-1311), Z-Image's attentionForward (:2228-2271) and, with kv_heads < heads
+ * and INV_ATTN_CAUSAL, Qwen3's grouped causal attention (src/quicknn_qwen3.pas:
+ * 727-769).  The [seq_q x seq_k] score matrix is never stored.
+ *  in_dtype: INV_DT_F32 (rounded to bf16, nearest-even, on the device) or
+ *  INV_DT_BF16, for Q, K and V alike; out_dtype INV_DT_F32 or INV_DT_BF16.
+ *  head_dim 64 or 128 (else INV_ERR_UNSUPPORTED); heads a multiple of kv_heads;
+ *  scale > 0.  Scores accumulate in fp32; the softmax weights are rounded to
+ *  bf16 for the P.V product, which accumulates in fp32.
+ *  flags: INV_FLAG_DEVICE_PTRS, INV_FLAG_ASYNC, INV_ATTN_CAUSAL. */
+int inv_hip_attention(const void *Q, const void *K, const void *V, void *O, int in_dtype,
+                      int out_dtype, int64_t heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k,
+                      int64_t head_dim, float scale, int flags);
 
 /* ---- the CBLAS slots ------------------------------------------------------ */
 /* Exactly the signature of TQNNSingleOPS.cblas_sgemm (src/quicknncpu.pas:

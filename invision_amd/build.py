@@ -44,6 +44,8 @@ def compile_jobs() -> list[tuple[list[str], str]]:
     jobs = []
     obj = os.path.join(BUILD_DIR, "inv_hip.o")
     jobs.append(([HIPCC] + COMMON_FLAGS + inc + ["-c", os.path.join(CSRC, "inv_hip.hip"), "-o", obj], obj))
+    obj = os.path.join(BUILD_DIR, "attention.o")
+    jobs.append(([HIPCC] + COMMON_FLAGS + inc + ["-c", os.path.join(CSRC, "attention.hip"), "-o", obj], obj))
     obj = os.path.join(BUILD_DIR, "safetensors.o")  # host code only
     jobs.append(([HIPCC, "-O2", "-std=c++17", "-fPIC", "-Wall"] + inc + ["-c", os.path.join(CSRC, "safetensors.cpp"),
                                                                          "-o", obj], obj))

@@ -1,0 +1,302 @@
+// attention.hip -- attention forward on MI355X (gfx950):
+//   O[q, h] = sum_j softmax_j(scale * Q[q, h] . K[j, g]) V[j, g],  g = h / (heads / kv_heads)
+// for the reference's [tokens x heads*head_dim] layout, one pass over K and V
+// with the running max / running sum of the online softmax (the algorithm of
+// TQNNSingleOPS.QNNFlashAttentionHeadTiled, src/quicknncpu.pas:2662-2761, on
+// MFMA tiles instead of per-row axpy).
+//
+// Workgroup: 4 waves, 128 queries of one head (32 per wave); key tiles of 64
+// staged in LDS (double-buffered, filled from registers loaded one tile
+// ahead) and shared by the 4 waves; two workgroups per CU, so one's softmax
+// VALU work overlaps the other's MFMAs.
+//
+// Per wave and key tile, with v_mfma_f32_32x32x16_bf16 (D[n][m] = sum_k A[n][k] B[m][k],
+// lane l holding A[l%32][8*(l/32) .. +7] and B[l%32][8*(l/32) .. +7], and output
+// register r of lane l at n = 8*(r/4) + 4*(l/32) + r%4, m = l%32):
+//  S^T = K Q^T:  A = K-tile rows (keys), B = the wave's Q rows (held in registers
+//                for the whole kernel), k = head_dim.  Each lane then holds the
+//                scores of ONE query (m = l%32) for 16 keys per 32-key block, so
+//                the row max and row sum are lane-local plus one exchange with
+//                lane l^32.
+//  O^T += V^T P^T: A = V^T tile rows (head_dim), B = P (bf16) straight from the
+//                score registers, k = keys.  For that, the B fragment's 8 k-slots
+//                of lane l must be the keys the lane holds; the K tile is stored
+//                with rows 4-7 and 8-11 of every 16-row group swapped (`quadswap`),
+//                which makes a lane's 8 consecutive score registers exactly keys
+//                16c + 8*(l/32) + 0..7 -- the contiguous 16 bytes its V^T fragment
+//                reads.  No cross-lane shuffle of P is needed.
+// Softmax runs in the exp2 domain: exp(scale*s - m) = exp2(s*scale*log2e - m'),
+// on the hardware exp2; P is rounded to bf16 (nearest-even) for the second MFMA.
+#include "attention.hpp"
+
+namespace inv {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) char lds_t;
+
+#if defined(__HIP_DEVICE_COMPILE__)
+
+// Slot key of a 128-byte LDS row (8 slots of 16 bytes): 16 consecutive rows read
+// at one logical slot land on 16 different 16-byte bank groups.
+__device__ __forceinline__ int key8(int r) { return (r + ((r >> 3) & 1)) & 7; }
+
+// Physical 16-byte slot of chunk c in row r of a K tile (D/8 chunks per row).
+template <int D>
+__device__ __forceinline__ int k_slot(int r, int c) {
+    if constexpr (D == 128)
+        return c ^ (r & 15);  // 256-byte rows: one bank window each
+    else
+        return c ^ key8(r);
+}
+
+// K-tile row r holds key quadswap(r) of the tile: rows 4-7 and 8-11 of every
+// 16-row group trade places (an involution).
+__device__ __forceinline__ int quadswap(int r) { return (((r >> 2) ^ (r >> 3)) & 1) ? (r ^ 12) : r; }
+
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+#endif  // __HIP_DEVICE_COMPILE__
+
+// The body exists only in the device pass; the host pass needs the launch stub
+// (buffer-resource types do not exist for the host target).
+template <int D, bool CAUSAL, int OUT>
+__global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    constexpr int BQ = kAttnBlockQ, BK = kAttnBlockK;
+    static_assert(BQ == 128 && BK == 64, "4 waves of 32 queries, 64-key tiles");
+    static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+    constexpr int KROW = D * 2;            // bytes per K-tile row
+    constexpr int K_BYTES = BK * KROW;     // K tile
+    constexpr int V_BYTES = D * BK * 2;    // V^T tile: D rows of 128 bytes
+    constexpr int STAGE = K_BYTES + V_BYTES;
+    constexpr int KCH = D / 8;             // 16-byte chunks per K row
+    constexpr int KIT = BK * KCH / 256;    // K copies per thread per tile
+    constexpr int VIT = D * 8 / 256;       // V^T copies per thread per tile
+    constexpr int NC = D / 16;             // 16-wide head_dim steps of S
+    constexpr int ND = D / 32;             // 32-row head_dim blocks of O
+    __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+    lds_t *lds = (lds_t *)smem;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int lq = lane & 31, lh = lane >> 5;
+    const int head = blockIdx.y;
+    const int kvh = head / (p.heads / p.kv_heads);
+    const int q0 = blockIdx.x * BQ;
+    const int my_q = q0 + wave * 32 + lq;
+
+    // This wave's Q rows as the B operand of S^T = K Q^T (zero past seq_q).
+    bf16x8_t qf[NC];
+    {
+        const bool ok = my_q < p.seq_q;
+        const uint16_t *qrow = p.Q + (int64_t)(ok ? my_q : 0) * p.ldq + head * D + 8 * lh;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const u32x4_t v = ok ? *(const u32x4_t *)(qrow + 16 * c) : u32x4_t{0u, 0u, 0u, 0u};
+            qf[c] = __builtin_bit_cast(bf16x8_t, v);
+        }
+    }
+
+    // K rows of kv head kvh: the buffer range ends with key seq_k - 1, so the
+    // rows of a partial last tile read as zeros.  V^T rows are padded to ldv.
+    const __amdgpu_buffer_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.K + kvh * D), 0, (int)(((int64_t)(p.seq_k - 1) * p.ldk + D) * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.Vt + (int64_t)kvh * D * p.ldv), 0, (int)((int64_t)D * p.ldv * 2), 0x00020000);
+
+    // Copy assignment: K chunk kc of key rows kr + i*(256/KCH); V^T chunk vc of rows vr + 32*i.
+    const int kc = tid % KCH, kr = tid / KCH;
+    const int vc = tid % 8, vr = tid / 8;
+    int k_lds[KIT], v_lds[VIT];
+#pragma unroll
+    for (int i = 0; i < KIT; ++i) {
+        const int n = quadswap(kr + i * (256 / KCH));
+        k_lds[i] = n * KROW + k_slot<D>(n, kc) * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < VIT; ++i) {
+        const int d = vr + 32 * i;
+        v_lds[i] = K_BYTES + d * 128 + ((vc ^ key8(d)) * 16);
+    }
+    u32x4_t kreg[KIT], vreg[VIT];
+    auto load_tile = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < KIT; ++i)
+            kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                rsk, (uint32_t)((int64_t)(kt * BK + kr + i * (256 / KCH)) * p.ldk * 2) + kc * 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < VIT; ++i)
+            vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                rsv, (uint32_t)((int64_t)(vr + 32 * i) * p.ldv * 2) + kt * BK * 2 + vc * 16, 0, 0);
+    };
+    auto store_tile = [&](lds_t *st) {
+#pragma unroll
+        for (int i = 0; i < KIT; ++i) *(__attribute__((address_space(3))) u32x4_t *)(st + k_lds[i]) = kreg[i];
+#pragma unroll
+        for (int i = 0; i < VIT; ++i) *(__attribute__((address_space(3))) u32x4_t *)(st + v_lds[i]) = vreg[i];
+    };
+
+    // Key tiles this block needs: all of them, or (causal) up to the last key
+    // visible to its last query.
+    int nkt = (p.seq_k + BK - 1) / BK;
+    if constexpr (CAUSAL) {
+        const int last = min(p.seq_k - 1, q0 + BQ - 1 + p.causal_offset);
+        nkt = last < 0 ? 0 : last / BK + 1;
+    }
+
+    f32x16_t o[ND];
+#pragma unroll
+    for (int i = 0; i < ND; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
+    float m_run = -__builtin_inff(), l_run = 0.f;
+    const float sl2 = p.scale_log2;
+
+    // Fragment addresses within a stage.
+    int k_frag[2][NC];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int n = 32 * b + lq;
+            k_frag[b][c] = n * KROW + k_slot<D>(n, 2 * c + lh) * 16;
+        }
+    int v_frag[ND][4];
+#pragma unroll
+    for (int i = 0; i < ND; ++i)
+#pragma unroll
+        for (int kc4 = 0; kc4 < 4; ++kc4) {  // 16-key chunk kc4 = 2*b + c'
+            const int d = 32 * i + lq;
+            v_frag[i][kc4] = K_BYTES + d * 128 + (((2 * kc4 + lh) ^ key8(d)) * 16);
+        }
+
+    if (nkt > 0) {
+        load_tile(0);
+        store_tile(lds);
+    }
+    __syncthreads();
+
+    for (int kt = 0; kt < nkt; ++kt) {
+        const lds_t *cur = lds + (kt & 1) * STAGE;
+        if (kt + 1 < nkt) load_tile(kt + 1);
+
+        // S^T for 64 keys: two 32-key blocks.
+        f32x16_t s[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[b][r] = 0.f;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const bf16x8_t kf = *(const __attribute__((address_space(3))) bf16x8_t *)(cur + k_frag[b][c]);
+                s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[c], s[b], 0, 0, 0);
+            }
+        }
+
+        // Keys past seq_k, and (causal) after the query's diagonal, do not exist.
+        const bool edge = (kt + 1) * BK > p.seq_k || (CAUSAL && (kt + 1) * BK - 1 > q0 + p.causal_offset);
+        if (edge) {
+            const int vis = CAUSAL ? min(p.seq_k - 1, my_q + p.causal_offset) : p.seq_k - 1;
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kt * BK + quadswap(32 * b + 8 * (r >> 2) + 4 * lh + (r & 3));
+                    if (key > vis) s[b][r] = -__builtin_inff();
+                }
+        }
+
+        // Online softmax for this lane's query (the other half of its keys is in lane ^ 32).
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx * sl2);
+        const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;  // no key seen yet
+        const float alpha = exp2_hw(m_run - m_use);
+        float ls = 0.f;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float e = exp2_hw(fmaf(s[b][r], sl2, -m_use));
+                s[b][r] = e;
+                ls += e;
+            }
+        l_run = fmaf(l_run, alpha, ls);
+        m_run = m_new;
+#pragma unroll
+        for (int i = 0; i < ND; ++i) o[i] *= alpha;
+
+        // O^T += V^T P^T over the 4 chunks of 16 keys.
+#pragma unroll
+        for (int kc4 = 0; kc4 < 4; ++kc4) {
+            const int b = kc4 >> 1, c2 = kc4 & 1;
+            const f32x8_t pv = {s[b][8 * c2 + 0], s[b][8 * c2 + 1], s[b][8 * c2 + 2], s[b][8 * c2 + 3],
+                                s[b][8 * c2 + 4], s[b][8 * c2 + 5], s[b][8 * c2 + 6], s[b][8 * c2 + 7]};
+            const bf16x8_t pf = __builtin_convertvector(pv, bf16x8_t);
+#pragma unroll
+            for (int i = 0; i < ND; ++i) {
+                const bf16x8_t vf = *(const __attribute__((address_space(3))) bf16x8_t *)(cur + v_frag[i][kc4]);
+                o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[i], 0, 0, 0);
+            }
+        }
+
+        if (kt + 1 < nkt) store_tile(lds + ((kt + 1) & 1) * STAGE);
+        __syncthreads();
+    }
+
+    // Normalise and store this lane's query row: 4 consecutive head_dim values per register group.
+    const float lt = l_run + __shfl_xor(l_run, 32);
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    if (my_q < p.seq_q) {
+#pragma unroll
+        for (int i = 0; i < ND; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = 32 * i + 8 * j + 4 * lh;
+                const f32x4_t v = {o[i][4 * j] * inv, o[i][4 * j + 1] * inv, o[i][4 * j + 2] * inv,
+                                   o[i][4 * j + 3] * inv};
+                const int64_t off = (int64_t)my_q * p.ldo + head * D + d;
+                if constexpr (OUT == 0) {
+                    *(f32x4_t *)((float *)p.O + off) = v;
+                } else {
+                    typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+                    *(u32x2_t *)((uint16_t *)p.O + off) =
+                        __builtin_bit_cast(u32x2_t, __builtin_convertvector(v, bf16x4_t));
+                }
+            }
+    }
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+template <int D, bool CAUSAL, int OUT>
+hipError_t launch3(const AttnParams &p, hipStream_t s) {
+    const dim3 grid((unsigned)((p.seq_q + kAttnBlockQ - 1) / kAttnBlockQ), (unsigned)p.heads);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL, OUT>), grid, dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch2(const AttnParams &p, bool causal, int out, hipStream_t s) {
+    if (causal) return out ? launch3<D, true, 1>(p, s) : launch3<D, true, 0>(p, s);
+    return out ? launch3<D, false, 1>(p, s) : launch3<D, false, 0>(p, s);
+}
+
+}  // namespace
+
+hipError_t attention_launch(const AttnParams &p, int D, bool causal, int out, hipStream_t stream) {
+    if (D == 128) return launch2<128>(p, causal, out, stream);
+    if (D == 64) return launch2<64>(p, causal, out, stream);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace inv

@@ -40,6 +40,7 @@ INV_EPI_SWIGLU = 3
 INV_FLAG_DEVICE_PTRS = 0x1
 INV_FLAG_ASYNC = 0x2
 INV_FLAG_PRECISE = 0x4
+INV_ATTN_CAUSAL = 0x100
 
 INV_ST_MAX_DIMS = 8
 INV_ST_TRUNCATE = 0x1
@@ -69,6 +70,8 @@ _PROTOS = {
                                c_int, c_int]),
     "inv_hip_linear_gated_add": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
                                          c_int64, c_int]),
+    "inv_hip_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int64, c_int64, c_int64,
+                                  c_int64, c_int64, c_float, c_int]),
     "inv_hip_sgemm": (c_int, [c_int, c_int, c_int, c_int64, c_int64, c_int64, c_float, c_void_p, c_int64, c_void_p,
                               c_int64, c_float, c_void_p, c_int64]),
     "inv_hip_sbgemm": (c_int, [c_int, c_int, c_int, c_int64, c_int64, c_int64, c_float, c_void_p, c_int64, c_void_p,

@@ -270,6 +270,58 @@ def linear_gated_add(y: np.ndarray, x: np.ndarray, W: Weight, gate: Optional[np.
     return y
 
 
+def attention(Q: np.ndarray, K: np.ndarray, V: np.ndarray, heads: int, head_dim: int, kv_heads: Optional[int] = None,
+              scale: Optional[float] = None, causal: bool = False, out_dtype: str = "f32") -> np.ndarray:
+    """Host arrays: O[seq_q x heads*head_dim] = softmax(scale * Q.K^T) V per head.
+
+    Q [seq_q x heads*head_dim], K and V [seq_k x kv_heads*head_dim], float32 or bf16
+    bits (uint16, all three alike); scale defaults to 1/sqrt(head_dim)."""
+    kv_heads = heads if kv_heads is None else kv_heads
+    if Q.dtype not in (np.float32, np.uint16) or K.dtype != Q.dtype or V.dtype != Q.dtype:
+        raise TypeError("Q, K and V must all be float32 or all bf16 bits (uint16)")
+    Q, K, V = (np.ascontiguousarray(a) for a in (Q, K, V))
+    if Q.ndim != 2 or Q.shape[1] != heads * head_dim:
+        raise ValueError(f"Q must be [seq_q x {heads * head_dim}]")
+    if K.ndim != 2 or K.shape[1] != kv_heads * head_dim or V.shape != K.shape:
+        raise ValueError(f"K and V must be [seq_k x {kv_heads * head_dim}]")
+    dt = hip.INV_DT_F32 if Q.dtype == np.float32 else hip.INV_DT_BF16
+    odt, onp = (hip.INV_DT_F32, np.float32) if out_dtype == "f32" else (hip.INV_DT_BF16, np.uint16)
+    O = np.empty((Q.shape[0], heads * head_dim), dtype=onp)
+    sc = 1.0 / float(np.sqrt(head_dim)) if scale is None else float(scale)
+    hip.call("inv_hip_attention", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), dt, odt, heads, kv_heads, Q.shape[0], K.shape[0],
+             head_dim, sc, hip.INV_ATTN_CAUSAL if causal else 0)
+    return O
+
+
+def attention_device(Q: DeviceArray, K: DeviceArray, V: DeviceArray, O: DeviceArray, heads: int, head_dim: int,
+                     kv_heads: Optional[int] = None, scale: Optional[float] = None, causal: bool = False,
+                     asynchronous: bool = False) -> None:
+    """inv_hip_attention on resident buffers (the shapes as for attention())."""
+    kv_heads = heads if kv_heads is None else kv_heads
+    if not (Q.dtype == K.dtype == V.dtype):
+        raise TypeError("Q, K and V must share a dtype")
+    sc = 1.0 / float(np.sqrt(head_dim)) if scale is None else float(scale)
+    flags = hip.INV_FLAG_DEVICE_PTRS | (hip.INV_FLAG_ASYNC if asynchronous else 0)
+    flags |= hip.INV_ATTN_CAUSAL if causal else 0
+    hip.call("inv_hip_attention", Q.ptr, K.ptr, V.ptr, O.ptr, Q.inv_dtype, O.inv_dtype, heads, kv_heads, Q.shape[0],
+             K.shape[0], head_dim, sc, flags)
+
+
+def QNNFlashAttention(dst: np.ndarray, Q: np.ndarray, K: np.ndarray, V: np.ndarray, heads: int, seq_q: int,
+                      seq_k: int, head_dim: int, scale: float) -> None:
+    """TQNNSingleOPS.QNNFlashAttention (src/quicknncpu.pas:2763) on fp32 host arrays:
+    dst[seq_q x heads*head_dim] = softmax(scale * Q.K^T) V for every head.  The
+    argument order is the one its callers use (src/quicknn_transformers.pas:1203,
+    1275-1276)."""
+    for a, nm in ((dst, "dst"), (Q, "Q"), (K, "K"), (V, "V")):
+        _check_host(a, np.float32, nm)
+    hidden = heads * head_dim
+    _bound(Q.size >= seq_q * hidden and dst.size >= seq_q * hidden, "ERROR : QNNFlashAttention out of bound [Q/dst]")
+    _bound(K.size >= seq_k * hidden and V.size >= seq_k * hidden, "ERROR : QNNFlashAttention out of bound [K/V]")
+    hip.call("inv_hip_attention", _ptr(Q), _ptr(K), _ptr(V), _ptr(dst), hip.INV_DT_F32, hip.INV_DT_F32, heads, heads,
+             seq_q, seq_k, head_dim, float(scale), 0)
+
+
 def set_sgemm_precision(mode: int) -> None:
     """INV_PREC_BF16 / INV_PREC_SPLIT_A / INV_PREC_SPLIT_AB for cblas_gemm."""
     init()

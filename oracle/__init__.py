@@ -21,6 +21,10 @@ How each oracle function is pinned:
   * linear (quicknncpu.pas:1807-1847): closed form with bias.
   * gated add (quicknncpu.pas:853-859): numpy's fp32 elementwise product and
     sum (bit-exact), gate = 0 leaves dst unchanged, gate = 1 is dst + proj.
+  * attention (quicknn_transformers.pas:1150-1311; quicknn_qwen3.pas:727-769):
+    numpy float64 softmax(QK^T)V per head; invariants (constant V, one key,
+    equal keys, a vector added to every key, the causal prefix); the restated
+    AVX2 softmax against the exact softmax within its polynomial's error.
 """
 from __future__ import annotations
 
@@ -81,6 +85,13 @@ def lib() -> ctypes.CDLL:
         L.orc_silu_qnn.argtypes = [c_int64, c_void_p, c_void_p, c_void_p, c_void_p]
         L.orc_apply_epilogue.argtypes = [c_void_p, c_int64, c_int]
         L.orc_gated_add.argtypes = [c_void_p, c_void_p, c_void_p, c_int64, c_int64]
+        for f in (L.orc_attention_f64, L.orc_attention_qnn):
+            f.restype = c_int
+        L.orc_attention_f64.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                                        c_int64, ctypes.c_double, c_int, c_int]
+        L.orc_attention_qnn.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                                        c_int64, c_float, c_int, c_int]
+        L.orc_softmax_qnn.argtypes = [c_void_p, c_int64]
         L.orc_add_bias_rows.argtypes = [c_void_p, c_void_p, c_int64, c_int64]
         L.orc_has_avx2.restype = c_int
         L.orc_max_threads.restype = c_int
@@ -224,6 +235,48 @@ def gated_add(dst: np.ndarray, gate: np.ndarray, proj: np.ndarray) -> np.ndarray
         raise ValueError("gated_add: shapes")
     lib().orc_gated_add(_p(d), _p(g), _p(pr), seq, hidden)
     return d
+
+
+def _attn_args(Q, K, V, heads, kv_heads, d):
+    Q = np.ascontiguousarray(Q, dtype=np.float32)
+    K = np.ascontiguousarray(K, dtype=np.float32)
+    V = np.ascontiguousarray(V, dtype=np.float32)
+    seq_q, seq_k = Q.shape[0], K.shape[0]
+    if Q.shape[1] != heads * d or K.shape[1] != kv_heads * d or V.shape != K.shape:
+        raise ValueError("attention: shapes")
+    return Q, K, V, seq_q, seq_k
+
+
+def attention_f64(Q, K, V, heads: int, kv_heads: int, d: int, scale: float, causal: bool = False,
+                  nthreads: int = 0) -> np.ndarray:
+    """softmax(scale * Q_h K_g^T) V_g per head in fp64 (the reference's attention
+    loops, quicknn_transformers.pas:1150-1311; quicknn_qwen3.pas:727-769)."""
+    Q, K, V, seq_q, seq_k = _attn_args(Q, K, V, heads, kv_heads, d)
+    O = np.empty((seq_q, heads * d), dtype=np.float64)
+    rc = lib().orc_attention_f64(_p(Q), _p(K), _p(V), _p(O), heads, kv_heads, seq_q, seq_k, d, float(scale),
+                                 int(causal), nthreads)
+    if rc:
+        raise ValueError(f"oracle attention failed ({rc})")
+    return O
+
+
+def attention_qnn(Q, K, V, heads: int, kv_heads: int, d: int, scale: float, causal: bool = False,
+                  nthreads: int = 0) -> np.ndarray:
+    """The reference's fp32 BLAS path with its AVX2 softmax (orc_attention_qnn)."""
+    Q, K, V, seq_q, seq_k = _attn_args(Q, K, V, heads, kv_heads, d)
+    O = np.empty((seq_q, heads * d), dtype=np.float32)
+    rc = lib().orc_attention_qnn(_p(Q), _p(K), _p(V), _p(O), heads, kv_heads, seq_q, seq_k, d, float(scale),
+                                 int(causal), nthreads)
+    if rc:
+        raise ValueError(f"oracle attention failed ({rc})")
+    return O
+
+
+def softmax_qnn(x: np.ndarray) -> np.ndarray:
+    """sSoftmax_avx2 restated (exact 1/sum) on a copy of a 1-D fp32 array."""
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    lib().orc_softmax_qnn(_p(y), y.size)
+    return y
 
 
 def silu_qnn(x: np.ndarray, up=None):

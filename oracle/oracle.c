@@ -480,3 +480,138 @@ int orc_linear_bf16w(const float *X, const uint16_t *W, const float *bias, float
     orc_apply_epilogue(Y, M * N, epilogue);
     return 0;
 }
+
+/* ---- attention ---------------------------------------------------------------
+ * The reference's transformer layout: Q [seq_q x heads*d], K and V
+ * [seq_k x kv_heads*d], O [seq_q x heads*d], row-major; head h reads kv head
+ * h / (heads / kv_heads) (quicknn_qwen3.pas:735-762).  With causal set, key j is
+ * visible to query i iff j <= i + (seq_k - seq_q) (QNNMatTriangularFill before
+ * the softmax, quicknn_qwen3.pas:752-754, for seq_q = seq_k). */
+
+/* Closed form in fp64: O = softmax(scale * Q.K^T) . V per head and query -- the
+ * mathematics of the per-head cblas_gemm / QNNSoftmaxRows / cblas_gemm loops
+ * (quicknn_transformers.pas:1150-1311, 2228-2271; quicknn_qwen3.pas:727-769) and
+ * of QNNFlashAttention (quicknncpu.pas:2763). */
+int orc_attention_f64(const float *Q, const float *K, const float *V, double *O, int64_t heads, int64_t kv_heads,
+                      int64_t seq_q, int64_t seq_k, int64_t d, double scale, int causal, int nthreads) {
+    if (heads <= 0 || kv_heads <= 0 || heads % kv_heads) return -1;
+    const int64_t hq = heads * d, hk = kv_heads * d, grp = heads / kv_heads, off = seq_k - seq_q;
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+    int bad = 0;
+#pragma omp parallel
+    {
+        double *w = (double *)malloc((size_t)(seq_k > 0 ? seq_k : 1) * sizeof(double));
+        if (!w) {
+#pragma omp atomic write
+            bad = 1;
+        }
+#pragma omp for collapse(2) schedule(static)
+        for (int64_t h = 0; h < heads; ++h)
+            for (int64_t i = 0; i < seq_q; ++i) {
+                if (!w) continue;
+                const float *q = Q + i * hq + h * d;
+                const int64_t g = h / grp;
+                const int64_t last = causal ? (i + off < seq_k - 1 ? i + off : seq_k - 1) : seq_k - 1;
+                double mx = -INFINITY;
+                for (int64_t j = 0; j <= last; ++j) {
+                    const float *k = K + j * hk + g * d;
+                    double dot = 0.0;
+                    for (int64_t e = 0; e < d; ++e) dot += (double)q[e] * (double)k[e];
+                    w[j] = dot * scale;
+                    if (w[j] > mx) mx = w[j];
+                }
+                double sum = 0.0;
+                for (int64_t j = 0; j <= last; ++j) {
+                    w[j] = exp(w[j] - mx);
+                    sum += w[j];
+                }
+                double *o = O + i * hq + h * d;
+                for (int64_t e = 0; e < d; ++e) o[e] = 0.0;
+                for (int64_t j = 0; j <= last; ++j) {
+                    const float *v = V + j * hk + g * d;
+                    const double pj = w[j] / sum;
+                    for (int64_t e = 0; e < d; ++e) o[e] += pj * (double)v[e];
+                }
+            }
+        free(w);
+    }
+    return bad ? -2 : 0;
+}
+
+/* sSoftmax_avx2 (ops_avx2.inc:552-760) restated: t = x - max clamped to
+ * [MIN_EXP, MAX_EXP] = [-87.3, 88.7] (:33-34, 600-603); n = floor(t log2 e + 0.5);
+ * r = fma(n, -ln 2, t); p = Horner of 1 + r(1 + r(0.5 + r(0.16666667 +
+ * r(0.04166667 + r 0.00833333)))) with fused multiply-adds; 2^n added to the
+ * exponent bits; eight running lane sums, then the horizontal sum; every value
+ * times 1/sum.  The reference takes 1/sum with rcpss (an approximation whose
+ * bits are implementation-defined); this restatement divides exactly. */
+void orc_softmax_qnn(float *x, int64_t n) {
+    if (n <= 0) return;
+    float mx = x[0];
+    for (int64_t i = 1; i < n; ++i)
+        if (x[i] > mx) mx = x[i];
+    float lane[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int64_t i = 0; i < n; ++i) {
+        float t = x[i] - mx;
+        if (t >= 88.7f) t = 88.7f;
+        if (t <= -87.3f) t = -87.3f;
+        const float nn = floorf(t * 1.4426950408889634f + 0.5f);
+        const float r = fmaf(nn, -0.6931471805599453f, t);
+        float p = fmaf(r, 0.00833333f, 0.04166667f);
+        p = fmaf(p, r, 0.16666667f);
+        p = fmaf(p, r, 0.5f);
+        p = fmaf(p, r, 1.0f);
+        p = fmaf(p, r, 1.0f);
+        int32_t bits;
+        memcpy(&bits, &p, 4);
+        bits += (int32_t)nn << 23;
+        memcpy(&p, &bits, 4);
+        x[i] = p;
+        lane[i & 7] += p;
+    }
+    const float sum = ((lane[0] + lane[1]) + (lane[2] + lane[3])) + ((lane[4] + lane[5]) + (lane[6] + lane[7]));
+    const float inv = 1.0f / sum;
+    for (int64_t i = 0; i < n; ++i) x[i] *= inv;
+}
+
+/* The reference's BLAS-bound attention as it runs (quicknn_transformers.pas:
+ * 1163-1189; quicknn_qwen3.pas:741-768): scores = scale * Q_h . K_g^T summed in
+ * fp32 (cblas_gemm with alpha = scale), -inf where causal masks, QNNSoftmaxRows
+ * (orc_softmax_qnn), O_h = P . V_g summed in fp32. */
+int orc_attention_qnn(const float *Q, const float *K, const float *V, float *O, int64_t heads, int64_t kv_heads,
+                      int64_t seq_q, int64_t seq_k, int64_t d, float scale, int causal, int nthreads) {
+    if (heads <= 0 || kv_heads <= 0 || heads % kv_heads) return -1;
+    const int64_t hq = heads * d, hk = kv_heads * d, grp = heads / kv_heads, off = seq_k - seq_q;
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+    int bad = 0;
+#pragma omp parallel
+    {
+        float *w = (float *)malloc((size_t)(seq_k > 0 ? seq_k : 1) * sizeof(float));
+        if (!w) {
+#pragma omp atomic write
+            bad = 1;
+        }
+#pragma omp for collapse(2) schedule(static)
+        for (int64_t h = 0; h < heads; ++h)
+            for (int64_t i = 0; i < seq_q; ++i) {
+                if (!w) continue;
+                const float *q = Q + i * hq + h * d;
+                const int64_t g = h / grp;
+                for (int64_t j = 0; j < seq_k; ++j) {
+                    const float *k = K + j * hk + g * d;
+                    float dot = 0.0f;
+                    for (int64_t e = 0; e < d; ++e) dot += q[e] * k[e];
+                    w[j] = (causal && j > i + off) ? -INFINITY : scale * dot;
+                }
+                orc_softmax_qnn(w, seq_k);
+                float *o = O + i * hq + h * d;
+                for (int64_t e = 0; e < d; ++e) o[e] = 0.0f;
+                for (int64_t j = 0; j < seq_k; ++j) {
+                    const float *v = V + j * hk + g * d;
+                    for (int64_t e = 0; e < d; ++e) o[e] += w[j] * v[e];
+                }
+            }
+        free(w);
+    }
+    return bad ? -2 : 0;
+}

@@ -74,6 +74,20 @@ void orc_apply_epilogue(float *Y, int64_t n, int epilogue);
 /* QNNGatedAdd (quicknncpu.pas:853-859): dst[i][j] += gate[j] * proj[i][j]. */
 void orc_gated_add(float *dst, const float *gate, const float *proj, int64_t seq, int64_t hidden);
 
+/* ---- attention: src/quicknn_transformers.pas:1150-1311, 2228-2271;
+ *      src/quicknn_qwen3.pas:727-769; src/quicknncpu.pas:2421-2500, 2763 ------
+ * Q [seq_q x heads*d], K/V [seq_k x kv_heads*d], O [seq_q x heads*d]; head h uses
+ * kv head h / (heads / kv_heads); causal: key j visible to query i iff
+ * j <= i + seq_k - seq_q. */
+int orc_attention_f64(const float *Q, const float *K, const float *V, double *O, int64_t heads,
+                      int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t d, double scale, int causal,
+                      int nthreads);
+int orc_attention_qnn(const float *Q, const float *K, const float *V, float *O, int64_t heads,
+                      int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t d, float scale, int causal,
+                      int nthreads);
+/* sSoftmax_avx2 (ops_avx2.inc:552-760) with an exact 1/sum in place of rcpss. */
+void orc_softmax_qnn(float *x, int64_t n);
+
 int orc_has_avx2(void);
 int orc_max_threads(void);
 

@@ -1,0 +1,167 @@
+"""Attention forward: inv_hip_attention against the oracle.
+
+The reference computes O = softmax(scale * Q.K^T) V per head in fp32
+(src/quicknn_transformers.pas:1150-1311, 2228-2271; src/quicknn_qwen3.pas:
+727-769; QNNFlashAttention src/quicknncpu.pas:2763).  The GPU path rounds Q, K
+and V to bf16 (nearest-even), accumulates scores in fp32 and rounds the softmax
+weights to bf16 for the P.V product (fp32 accumulate).  Tolerances, normwise
+(max|err| / max|ref|):
+  - 4e-3 against the fp64 oracle on the same bf16-rounded Q, K, V (the bf16
+    weights alone measure ~1-1.7e-3 in a CPU emulation of the kernel's rounding);
+  - 1.5e-2 against the reference's fp32 path on the unrounded inputs (adds the
+    bf16 rounding of Q, K and V: ~4-8e-3 measured the same way);
+  - bf16 outputs add their own rounding, 2^-8 relative.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from invision_amd import hip
+from invision_amd import quicknn_hip as q
+from invision_amd.bf16 import as_bf16_bits, bf16_bits_to_f32, round_bf16
+
+TOL_BF16_IN = 4e-3
+TOL_REF = 1.5e-2
+TOL_BF16_OUT = 2.0 ** -8
+
+
+def gen(seed, sq, sk, heads, kv_heads, d):
+    oracle.rng_seed(seed)
+    Q = oracle.randn_scaled((sq, heads * d), 1.0, False)
+    K = oracle.randn_scaled((sk, kv_heads * d), 1.0, False)
+    V = oracle.randn_scaled((sk, kv_heads * d), 1.0, False)
+    return Q, K, V
+
+
+def check(O, Q, K, V, heads, kv_heads, d, scale, causal, out="f32", rows=None, ref_path=True):
+    Of = bf16_bits_to_f32(O) if out == "bf16" else O
+    if rows is not None:
+        Of, Q = Of[rows], Q[rows]
+        assert not causal
+    Qr, Kr, Vr = round_bf16(Q), round_bf16(K), round_bf16(V)
+    r64 = oracle.attention_f64(Qr, Kr, Vr, heads, kv_heads, d, scale, causal)
+    e = oracle.normwise_err(Of, r64)
+    extra = TOL_BF16_OUT if out == "bf16" else 0.0
+    msg = f"  normwise err: vs oracle on bf16 inputs {e:.3e}"
+    if ref_path:
+        rq = oracle.attention_qnn(Q, K, V, heads, kv_heads, d, scale, causal)
+        e_ref = oracle.normwise_err(Of, rq)
+        msg += f", vs the reference's fp32 path {e_ref:.3e}"
+    print(msg, flush=True)
+    assert np.all(np.isfinite(Of))
+    assert e <= TOL_BF16_IN + extra
+    if ref_path:
+        assert e_ref <= TOL_REF + extra
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads,kv_heads,sq,sk,d,causal", [
+    (2, 2, 128, 128, 128, False),
+    (3, 3, 200, 333, 128, False),   # ragged query block and key tile
+    (2, 2, 384, 512, 128, False),   # joint attention: image queries over text + image keys
+    (4, 2, 130, 130, 64, True),     # grouped kv heads, causal
+    (8, 2, 257, 257, 128, True),
+    (2, 1, 77, 300, 64, False),
+    (1, 1, 1, 1, 128, False),
+    (2, 2, 5, 70, 64, True),        # causal with more keys than queries (offset 65)
+])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_attention_matches_oracle(hiplib, heads, kv_heads, sq, sk, d, causal, dtype):
+    Q, K, V = gen(61, sq, sk, heads, kv_heads, d)
+    scale = 1.0 / math.sqrt(d)
+    ins = (Q, K, V) if dtype == "f32" else tuple(as_bf16_bits(a) for a in (Q, K, V))
+    O = q.attention(*ins, heads=heads, head_dim=d, kv_heads=kv_heads, scale=scale, causal=causal)
+    check(O, Q, K, V, heads, kv_heads, d, scale, causal)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d", [64, 128])
+def test_attention_bf16_output_and_sharp_softmax(hiplib, d):
+    """A larger scale concentrates the weights on few keys (the max-subtraction path)."""
+    heads, sq, sk = 2, 160, 200
+    Q, K, V = gen(62, sq, sk, heads, heads, d)
+    scale = 4.0 / math.sqrt(d)
+    O = q.attention(Q, K, V, heads=heads, head_dim=d, scale=scale, out_dtype="bf16")
+    check(O, Q, K, V, heads, heads, d, scale, False, out="bf16")
+
+
+@pytest.mark.gpu
+def test_gqa_equals_repeated_kv_heads(hiplib):
+    """Grouped kv heads read exactly what repeating each kv head per query head gives."""
+    heads, kvh, d, sq, sk = 8, 2, 128, 150, 190
+    Q, K, V = gen(63, sq, sk, heads, kvh, d)
+    rep = lambda A: np.ascontiguousarray(np.concatenate([A[:, (h // 4) * d:(h // 4 + 1) * d] for h in range(heads)], 1))
+    O1 = q.attention(Q, K, V, heads=heads, head_dim=d, kv_heads=kvh, causal=True)
+    O2 = q.attention(Q, rep(K), rep(V), heads=heads, head_dim=d, kv_heads=heads, causal=True)
+    np.testing.assert_array_equal(O1, O2)
+
+
+@pytest.mark.gpu
+def test_causal_rows_equal_their_prefix(hiplib):
+    """Query i of a causal call equals a non-causal call over keys 0 .. i + offset."""
+    heads, d, sq, sk = 2, 64, 100, 140
+    Q, K, V = gen(64, sq, sk, heads, heads, d)
+    O = q.attention(Q, K, V, heads=heads, head_dim=d, causal=True)
+    for i in (0, 1, 63, 64, 65, 99):
+        n = i + sk - sq + 1
+        Oi = q.attention(np.ascontiguousarray(Q[i:i + 1]), np.ascontiguousarray(K[:n]), np.ascontiguousarray(V[:n]),
+                         heads=heads, head_dim=d)
+        assert oracle.normwise_err(O[i:i + 1], Oi) < 1e-6, i
+
+
+@pytest.mark.gpu
+def test_device_pointers_match_host_path(hiplib):
+    heads, d, sq, sk = 3, 128, 140, 260
+    Q, K, V = gen(65, sq, sk, heads, heads, d)
+    ref = q.attention(Q, K, V, heads=heads, head_dim=d)
+    qd, kd, vd = (q.DeviceArray.from_host(as_bf16_bits(a), "bf16") for a in (Q, K, V))
+    od = q.DeviceArray((sq, heads * d), "f32")
+    q.attention_device(qd, kd, vd, od, heads=heads, head_dim=d, asynchronous=True)
+    hip.call("inv_hip_synchronize")
+    np.testing.assert_array_equal(od.to_host(), ref)
+    for a in (qd, kd, vd, od):
+        a.free()
+
+
+@pytest.mark.gpu
+def test_qnn_flash_attention_mirror(hiplib):
+    heads, d, sq, sk = 2, 128, 96, 96
+    Q, K, V = gen(66, sq, sk, heads, heads, d)
+    dst = np.zeros((sq, heads * d), np.float32)
+    q.QNNFlashAttention(dst, Q, K, V, heads, sq, sk, d, 1.0 / math.sqrt(d))
+    check(dst, Q, K, V, heads, heads, d, 1.0 / math.sqrt(d), False)
+    with pytest.raises(AssertionError, match="out of bound"):
+        q.QNNFlashAttention(dst, Q, K, V, heads, sq, sk + 1, d, 0.1)
+
+
+@pytest.mark.gpu
+def test_flux2_joint_attention_shape_sampled_rows(hiplib):
+    """FLUX2-Klein-4B at 1024x1024: 24 heads of 128, 4096 image + 512 text tokens."""
+    heads, d, sq, sk = 24, 128, 4608, 4608
+    Q, K, V = gen(67, sq, sk, heads, heads, d)
+    Qb, Kb, Vb = (as_bf16_bits(a) for a in (Q, K, V))
+    O = q.attention(Qb, Kb, Vb, heads=heads, head_dim=d)
+    rows = np.unique(np.linspace(0, sq - 1, 12).astype(int))
+    check(O, Q, K, V, heads, heads, d, 1.0 / math.sqrt(d), False, rows=rows, ref_path=False)
+
+
+@pytest.mark.gpu
+def test_attention_argument_errors(hiplib):
+    Q, K, V = gen(68, 8, 8, 2, 2, 64)
+    lib = hip.load()
+    O = np.zeros_like(Q)
+    args = lambda **kw: dict(dict(heads=2, kv=2, sq=8, sk=8, d=64, scale=0.125, flags=0), **kw)
+
+    def call(a):
+        return lib.inv_hip_attention(Q.ctypes.data, K.ctypes.data, V.ctypes.data, O.ctypes.data, hip.INV_DT_F32,
+                                     hip.INV_DT_F32, a["heads"], a["kv"], a["sq"], a["sk"], a["d"], a["scale"],
+                                     a["flags"])
+    assert call(args(d=96)) == hip.INV_ERR_UNSUPPORTED and "head_dim" in hip.last_error()
+    assert call(args(heads=3, kv=2)) == hip.INV_ERR_ARG and "multiple of kv_heads" in hip.last_error()
+    assert call(args(sk=0)) == hip.INV_ERR_ARG and "seq_k is 0" in hip.last_error()
+    assert call(args(scale=0.0)) == hip.INV_ERR_ARG and "scale" in hip.last_error()
+    assert call(args(flags=0x8)) == hip.INV_ERR_ARG and "unknown flags" in hip.last_error()
+    assert call(args(sq=0)) == hip.INV_OK
+    assert not np.any(O)  # nothing written on error or for zero queries

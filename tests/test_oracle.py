@@ -278,6 +278,95 @@ def test_gated_add_against_numpy_and_special_gates():
     assert not np.array_equal(got, d + g_rows[:, None] * pr)
 
 
+# ------------------------------------------------------------ attention ----
+
+def _np_attention(Q, K, V, heads, kv_heads, d, scale, causal=False):
+    """numpy float64 softmax(QK^T)V per head: an independent statement."""
+    sq, sk = Q.shape[0], K.shape[0]
+    O = np.zeros((sq, heads * d))
+    for h in range(heads):
+        g = h // (heads // kv_heads)
+        S = Q[:, h * d:(h + 1) * d].astype(np.float64) @ K[:, g * d:(g + 1) * d].astype(np.float64).T * scale
+        if causal:
+            S[np.arange(sk)[None, :] > np.arange(sq)[:, None] + (sk - sq)] = -np.inf
+        P = np.exp(S - S.max(axis=1, keepdims=True))
+        O[:, h * d:(h + 1) * d] = (P / P.sum(axis=1, keepdims=True)) @ V[:, g * d:(g + 1) * d].astype(np.float64)
+    return O
+
+
+def _qkv(seed, sq, sk, heads, kv_heads, d):
+    return (_rand((sq, heads * d), seed), _rand((sk, kv_heads * d), seed + 1), _rand((sk, kv_heads * d), seed + 2))
+
+
+@pytest.mark.parametrize("heads,kv_heads,sq,sk,d,causal", [(2, 2, 5, 9, 16, False), (4, 2, 9, 9, 8, True),
+                                                          (3, 1, 7, 12, 8, True), (1, 1, 1, 1, 4, False)])
+def test_attention_f64_vs_numpy(heads, kv_heads, sq, sk, d, causal):
+    Q, K, V = _qkv(50, sq, sk, heads, kv_heads, d)
+    got = oracle.attention_f64(Q, K, V, heads, kv_heads, d, 0.3, causal)
+    np.testing.assert_allclose(got, _np_attention(Q, K, V, heads, kv_heads, d, 0.3, causal), rtol=0, atol=1e-12)
+
+
+def test_attention_invariants():
+    h, d, sq, sk = 2, 8, 6, 10
+    Q, K, V = _qkv(51, sq, sk, h, h, d)
+    base = oracle.attention_f64(Q, K, V, h, h, d, 0.5)
+    # every key holding the same value row: the output is that row
+    Vc = np.tile(V[3:4], (sk, 1))
+    np.testing.assert_allclose(oracle.attention_f64(Q, K, Vc, h, h, d, 0.5), np.tile(V[3:4], (sq, 1)), atol=1e-6)
+    # one key: its value
+    np.testing.assert_allclose(oracle.attention_f64(Q, K[:1], V[:1], h, h, d, 0.5), np.tile(V[:1], (sq, 1)), atol=1e-7)
+    # all keys equal: uniform weights, the mean of V
+    Ke = np.tile(K[:1], (sk, 1))
+    np.testing.assert_allclose(oracle.attention_f64(Q, Ke, V, h, h, d, 0.5),
+                               np.tile(V.astype(np.float64).mean(0, keepdims=True), (sq, 1)), atol=1e-6)
+    # one vector added to every key shifts each query's scores by a constant
+    u = _rand((1, h * d), 52)
+    np.testing.assert_allclose(oracle.attention_f64(Q, (K + u).astype(np.float32), V, h, h, d, 0.5), base, atol=1e-5)
+    # causal: query i sees exactly the keys up to i + (sk - sq)
+    c = oracle.attention_f64(Q, K, V, h, h, d, 0.5, causal=True)
+    for i in range(sq):
+        n = i + sk - sq + 1
+        np.testing.assert_allclose(c[i:i + 1], oracle.attention_f64(Q[i:i + 1], K[:n], V[:n], h, h, d, 0.5), atol=1e-12)
+    # grouped kv heads equal the same kv heads repeated per query head
+    Qg, Kg, Vg = _qkv(53, 5, 7, 4, 2, 8)
+    rep = lambda A: np.concatenate([A[:, (j // 2) * 8:(j // 2 + 1) * 8] for j in range(4)], axis=1)
+    np.testing.assert_allclose(oracle.attention_f64(Qg, Kg, Vg, 4, 2, 8, 0.4),
+                               oracle.attention_f64(Qg, rep(Kg), rep(Vg), 4, 4, 8, 0.4), atol=1e-12)
+
+
+def test_softmax_qnn_is_the_softmax_within_its_polynomial():
+    x = np.concatenate([np.linspace(-30, 5, 999), [-200.0, 3.0]]).astype(np.float32)
+    got = oracle.softmax_qnn(x)
+    e = np.exp(x.astype(np.float64) - x.max())
+    ref = e / e.sum()
+    assert abs(float(got.sum()) - 1.0) < 1e-5
+    assert np.max(np.abs(got - ref) / np.maximum(ref, 1e-30)[None]) < 1e-5 or np.max(np.abs(got - ref)) < 1e-9
+    # the clamp at -87.3: far-below-max inputs get ~exp(-87.3), not 0
+    assert 0.0 < got[-2] < 1e-37
+    # the restated reference path equals the closed form to fp32 rounding
+    Q, K, V = _qkv(54, 6, 11, 2, 2, 16)
+    assert oracle.normwise_err(oracle.attention_qnn(Q, K, V, 2, 2, 16, 0.25),
+                               oracle.attention_f64(Q, K, V, 2, 2, 16, 0.25)) < 1e-5
+
+
+def test_attention_checks_catch_planted_mistakes():
+    """A wrong scale, a value row shifted by one key, a causal diagonal off by one
+    and a wrong kv-head grouping each fail the attention parity bound (4e-3)."""
+    h, d, sq, sk = 4, 16, 12, 12
+    Q, K, V = _qkv(55, sq, sk, h, 2, d)
+    good = oracle.attention_f64(Q, K, V, h, 2, d, 0.5, causal=True)
+    assert oracle.normwise_err(oracle.attention_f64(Q, K, V, h, 2, d, 0.55, causal=True), good) > 4e-3
+    Vr = np.ascontiguousarray(np.roll(V, 1, axis=0))
+    assert oracle.normwise_err(oracle.attention_f64(Q, K, Vr, h, 2, d, 0.5, causal=True), good) > 4e-3
+    # diagonal one key later: as if seq_k were one longer
+    K1 = np.concatenate([K, K[-1:]]); V1 = np.concatenate([V, V[-1:]])
+    assert oracle.normwise_err(oracle.attention_f64(Q, K1, V1, h, 2, d, 0.5, causal=True), good) > 4e-3
+    # kv head g = h % kv_heads instead of h // (heads / kv_heads): query heads 1 and 2 trade kv heads
+    perm = np.r_[0:d, 2 * d:3 * d, d:2 * d, 3 * d:4 * d]
+    wrong = oracle.attention_f64(np.ascontiguousarray(Q[:, perm]), K, V, h, 2, d, 0.5, causal=True)[:, perm]
+    assert oracle.normwise_err(wrong, good) > 4e-3
+
+
 # ------------------------------------------------------- planted mistakes --
 
 def test_checks_catch_planted_mistakes():
