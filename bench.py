@@ -60,6 +60,15 @@ WORKLOADS = {
 }
 
 
+# Attention shapes: (description, heads, kv_heads, seq_q, seq_k, head_dim, causal).
+ATTN_WORKLOADS = {
+    "flux2_attention": ("FLUX2-Klein-4B joint attention at 1024x1024 (4096 image + 512 text tokens)", 24, 24, 4608,
+                        4608, 128, False),
+    "zimage_attention": ("Z-Image block attention, 4096 tokens", 30, 30, 4096, 4096, 128, False),
+    "qwen3_prefill_attention": ("Qwen3-4B causal grouped-query attention, 512 tokens", 32, 8, 512, 512, 128, True),
+}
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -223,6 +232,62 @@ def mfma_ceiling(gemm_tflops):
                    "sustained 1 s; W ~ N(0,0.02) and X ~ N(0,1) in bf16, or constant operands"}
     log(f"[bench] MFMA ceiling: {json.dumps(out)}")
     return out
+
+
+def run_attention(name, steps, warmup_seconds=0.5, check=True):
+    """inv_hip_attention on resident bf16 Q, K, V; FLOP = 4 * seq_q * seq_k * head_dim * heads
+    (halved for causal: the keys after the diagonal are skipped)."""
+    import ctypes
+    from invision_amd import hip
+    from invision_amd import quicknn_hip as q
+    from invision_amd.bf16 import as_bf16_bits, bf16_bits_to_f32
+    desc, heads, kvh, sq, sk, d, causal = ATTN_WORKLOADS[name]
+    log(f"[bench] {name}: {desc} heads={heads} kv_heads={kvh} seq_q={sq} seq_k={sk} head_dim={d} causal={causal}")
+    rng = np.random.default_rng(2)
+    Q, K, V = (as_bf16_bits(rng.standard_normal(sh, dtype=np.float32))
+               for sh in ((sq, heads * d), (sk, kvh * d), (sk, kvh * d)))
+    qd, kd, vd = (q.DeviceArray.from_host(a, "bf16") for a in (Q, K, V))
+    od = q.DeviceArray((sq, heads * d), "bf16")
+
+    def launch():
+        q.attention_device(qd, kd, vd, od, heads=heads, head_dim=d, kv_heads=kvh, causal=causal, asynchronous=True)
+
+    warm, tw = 0, time.perf_counter()
+    while warm < 3 or time.perf_counter() - tw < warmup_seconds:
+        for _ in range(10):
+            launch()
+        warm += 10
+        hip.call("inv_hip_synchronize")
+    ms = ctypes.c_float()
+    t0 = time.perf_counter()
+    hip.call("inv_hip_timer_start")
+    for _ in range(steps):
+        launch()
+    hip.call("inv_hip_timer_stop", ctypes.byref(ms))
+    hip.call("inv_hip_synchronize")
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    gpu_ms = ms.value / steps
+    flops = 4.0 * sq * sk * d * heads * (0.5 if causal else 1.0)
+    res = {"name": name, "heads": heads, "kv_heads": kvh, "seq_q": sq, "seq_k": sk, "head_dim": d, "causal": causal,
+           "warmup_steps": warm, "wall_ms": wall_ms, "kernel_ms": gpu_ms, "tflops_kernel": flops / (gpu_ms * 1e-3) / 1e12,
+           "tflops_wall": flops / (wall_ms * 1e-3) / 1e12}
+    if check:
+        import math
+        # fp64 spot check of a few query rows of head 0 (numpy, independent of the oracle)
+        O = bf16_bits_to_f32(od.to_host())
+        rows = np.unique(np.linspace(0, sq - 1, num=min(sq, 4)).astype(int))
+        qh = bf16_bits_to_f32(Q)[rows, :d].astype(np.float64)
+        kh = bf16_bits_to_f32(K)[:, :d].astype(np.float64)
+        vh = bf16_bits_to_f32(V)[:, :d].astype(np.float64)
+        S = qh @ kh.T / math.sqrt(d)
+        if causal:
+            S[np.arange(sk)[None, :] > rows[:, None] + (sk - sq)] = -np.inf
+        P = np.exp(S - S.max(1, keepdims=True))
+        ref = (P / P.sum(1, keepdims=True)) @ vh
+        res["parity_normwise_sampled_rows"] = float(np.max(np.abs(O[rows, :d] - ref)) / np.max(np.abs(ref)))
+    for a in (qd, kd, vd, od):
+        a.free()
+    return res
 
 
 def cpu_baseline(name):
@@ -427,6 +492,9 @@ def main():
             if name != args.workload:
                 r = run_workload(name, max(5, args.steps // 2), 3, warmup_seconds=min(args.warmup_seconds, 0.5))
                 log(f"[bench] {json.dumps(r)}")
+        for name in ATTN_WORKLOADS:
+            r = run_attention(name, max(5, args.steps // 4), warmup_seconds=min(args.warmup_seconds, 0.5))
+            log(f"[bench] {json.dumps(r)}")
 
     ceiling = None if args.no_mfma_ceiling else mfma_ceiling(res["tflops_kernel"])
     desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[args.workload]

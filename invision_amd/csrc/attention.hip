@@ -6,9 +6,9 @@
 // MFMA tiles instead of per-row axpy).
 //
 // Workgroup: 4 waves, 128 queries of one head (32 per wave); key tiles of 64
-// staged in LDS (double-buffered, filled from registers loaded one tile
-// ahead) and shared by the 4 waves; two workgroups per CU, so one's softmax
-// VALU work overlaps the other's MFMAs.
+// staged in LDS (double-buffered, filled one tile ahead by direct
+// buffer_load ... lds copies) and shared by the 4 waves; two workgroups per CU,
+// so one's softmax VALU work overlaps the other's MFMAs.
 //
 // Per wave and key tile, with v_mfma_f32_32x32x16_bf16 (D[n][m] = sum_k A[n][k] B[m][k],
 // lane l holding A[l%32][8*(l/32) .. +7] and B[l%32][8*(l/32) .. +7], and output
@@ -110,36 +110,33 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
     const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(p.Vt + (int64_t)kvh * D * p.ldv), 0, (int)((int64_t)D * p.ldv * 2), 0x00020000);
 
-    // Copy assignment: K chunk kc of key rows kr + i*(256/KCH); V^T chunk vc of rows vr + 32*i.
-    const int kc = tid % KCH, kr = tid / KCH;
-    const int vc = tid % 8, vr = tid / 8;
-    int k_lds[KIT], v_lds[VIT];
+    // Global -> LDS copies (buffer_load ... lds): copy i of thread tid fills the
+    // 16-byte LDS slot i*256 + tid of its tile, so each thread fetches the chunk
+    // that belongs there -- the swizzle and the K row order live in these
+    // global offsets.  K slot s: row n = s / KCH holds key quadswap(n), physical
+    // chunk s % KCH holds logical chunk (s % KCH) ^ swizzle(n).  V^T slot s: row
+    // d = s / 8, logical chunk (s % 8) ^ key8(d).
+    uint32_t k_goff[KIT], v_goff[VIT];
 #pragma unroll
     for (int i = 0; i < KIT; ++i) {
-        const int n = quadswap(kr + i * (256 / KCH));
-        k_lds[i] = n * KROW + k_slot<D>(n, kc) * 16;
+        const int sl = i * 256 + tid, n = sl / KCH;
+        k_goff[i] = (uint32_t)(quadswap(n) * p.ldk * 2 + k_slot<D>(n, sl % KCH) * 16);
     }
 #pragma unroll
     for (int i = 0; i < VIT; ++i) {
-        const int d = vr + 32 * i;
-        v_lds[i] = K_BYTES + d * 128 + ((vc ^ key8(d)) * 16);
+        const int sl = i * 256 + tid, d = sl / 8;
+        v_goff[i] = (uint32_t)(d * p.ldv * 2 + ((sl % 8) ^ key8(d)) * 16);
     }
-    u32x4_t kreg[KIT], vreg[VIT];
-    auto load_tile = [&](int kt) {
+    const uint32_t k_tile_step = (uint32_t)(BK * p.ldk * 2), v_tile_step = BK * 2;
+    auto load_tile = [&](int kt, lds_t *st) {
+        lds_t *wk = st + wave * 64 * 16;
 #pragma unroll
         for (int i = 0; i < KIT; ++i)
-            kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                rsk, (uint32_t)((int64_t)(kt * BK + kr + i * (256 / KCH)) * p.ldk * 2) + kc * 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsk, wk + i * 256 * 16, 16, k_goff[i] + kt * k_tile_step, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < VIT; ++i)
-            vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                rsv, (uint32_t)((int64_t)(vr + 32 * i) * p.ldv * 2) + kt * BK * 2 + vc * 16, 0, 0);
-    };
-    auto store_tile = [&](lds_t *st) {
-#pragma unroll
-        for (int i = 0; i < KIT; ++i) *(__attribute__((address_space(3))) u32x4_t *)(st + k_lds[i]) = kreg[i];
-#pragma unroll
-        for (int i = 0; i < VIT; ++i) *(__attribute__((address_space(3))) u32x4_t *)(st + v_lds[i]) = vreg[i];
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsv, wk + K_BYTES + i * 256 * 16, 16, v_goff[i] + kt * v_tile_step,
+                                                     0, 0, 0);
     };
 
     // Key tiles this block needs: all of them, or (causal) up to the last key
@@ -155,8 +152,12 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
     for (int i = 0; i < ND; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
+    // Running max (log2 domain) and this lane's partial running sum.  The max is
+    // only moved when a score exceeds it by more than 2^8 (or on the first
+    // tile): exp2 values then stay below 256, and O is rescaled on few tiles.
     float m_run = -__builtin_inff(), l_run = 0.f;
     const float sl2 = p.scale_log2;
+    constexpr float kSlack = 8.0f;
 
     // Fragment addresses within a stage.
     int k_frag[2][NC];
@@ -176,28 +177,42 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
             v_frag[i][kc4] = K_BYTES + d * 128 + (((2 * kc4 + lh) ^ key8(d)) * 16);
         }
 
-    if (nkt > 0) {
-        load_tile(0);
-        store_tile(lds);
-    }
+    if (nkt > 0) load_tile(0, lds);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): tile 0 is in LDS
     __syncthreads();
 
     for (int kt = 0; kt < nkt; ++kt) {
         const lds_t *cur = lds + (kt & 1) * STAGE;
-        if (kt + 1 < nkt) load_tile(kt + 1);
+        if (kt + 1 < nkt) load_tile(kt + 1, lds + ((kt + 1) & 1) * STAGE);
 
-        // S^T for 64 keys: two 32-key blocks.
+        // S^T for 64 keys: two 32-key blocks whose MFMAs alternate (no back-to-back
+        // accumulator chain); K fragments are read two head_dim steps ahead.
+        auto read_k = [&](int c, bf16x8_t (&f)[2]) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) f[b] = *(const __attribute__((address_space(3))) bf16x8_t *)(cur + k_frag[b][c]);
+        };
         f32x16_t s[2];
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
+        for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int r = 0; r < 16; ++r) s[b][r] = 0.f;
+        bf16x8_t kf[3][2];
+        read_k(0, kf[0]);
+        read_k(1, kf[1]);
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const bf16x8_t kf = *(const __attribute__((address_space(3))) bf16x8_t *)(cur + k_frag[b][c]);
-                s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[c], s[b], 0, 0, 0);
-            }
+        for (int c = 0; c < NC; ++c) {
+            if (c + 2 < NC) read_k(c + 2, kf[(c + 2) % 3]);
+#pragma unroll
+            for (int b = 0; b < 2; ++b) s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[c % 3][b], qf[c], s[b], 0, 0, 0);
         }
+
+        // The first V^T fragments: their LDS latency hides under the softmax.
+        auto read_v = [&](int kc4, bf16x8_t (&f)[ND]) {
+#pragma unroll
+            for (int i = 0; i < ND; ++i) f[i] = *(const __attribute__((address_space(3))) bf16x8_t *)(cur + v_frag[i][kc4]);
+        };
+        bf16x8_t vf[2][ND];
+        read_v(0, vf[0]);
 
         // Keys past seq_k, and (causal) after the query's diagonal, do not exist.
         const bool edge = (kt + 1) * BK > p.seq_k || (CAUSAL && (kt + 1) * BK - 1 > q0 + p.causal_offset);
@@ -218,10 +233,17 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
         for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[b][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx * sl2);
-        const float m_use = (m_new == -__builtin_inff()) ? 0.f : m_new;  // no key seen yet
-        const float alpha = exp2_hw(m_run - m_use);
+        mx = fmaxf(mx, __shfl_xor(mx, 32)) * sl2;
+        const bool grow = mx > m_run + kSlack;
+        if (__builtin_amdgcn_ballot_w64(grow)) {  // some query's max moved: rescale (alpha = 1 elsewhere)
+            const float m_new = grow ? mx : m_run;
+            const float alpha = exp2_hw(m_run - m_new);  // 0 on the first tile, 1 where the max stays
+            l_run *= alpha;
+#pragma unroll
+            for (int i = 0; i < ND; ++i) o[i] *= alpha;
+            m_run = m_new;
+        }
+        const float m_use = (m_run == -__builtin_inff()) ? 0.f : m_run;  // no key seen yet
         float ls = 0.f;
 #pragma unroll
         for (int b = 0; b < 2; ++b)
@@ -231,26 +253,23 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
                 s[b][r] = e;
                 ls += e;
             }
-        l_run = fmaf(l_run, alpha, ls);
-        m_run = m_new;
-#pragma unroll
-        for (int i = 0; i < ND; ++i) o[i] *= alpha;
+        l_run += ls;
 
-        // O^T += V^T P^T over the 4 chunks of 16 keys.
+        // O^T += V^T P^T over the 4 chunks of 16 keys, V^T fragments one chunk ahead.
 #pragma unroll
         for (int kc4 = 0; kc4 < 4; ++kc4) {
+            if (kc4 + 1 < 4) read_v(kc4 + 1, vf[(kc4 + 1) & 1]);
             const int b = kc4 >> 1, c2 = kc4 & 1;
             const f32x8_t pv = {s[b][8 * c2 + 0], s[b][8 * c2 + 1], s[b][8 * c2 + 2], s[b][8 * c2 + 3],
                                 s[b][8 * c2 + 4], s[b][8 * c2 + 5], s[b][8 * c2 + 6], s[b][8 * c2 + 7]};
             const bf16x8_t pf = __builtin_convertvector(pv, bf16x8_t);
 #pragma unroll
-            for (int i = 0; i < ND; ++i) {
-                const bf16x8_t vf = *(const __attribute__((address_space(3))) bf16x8_t *)(cur + v_frag[i][kc4]);
-                o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[i], 0, 0, 0);
-            }
+            for (int i = 0; i < ND; ++i) o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[kc4 & 1][i], pf, o[i], 0, 0, 0);
         }
 
-        if (kt + 1 < nkt) store_tile(lds + ((kt + 1) & 1) * STAGE);
+        // The next tile has landed in the other buffer, and every wave is done
+        // reading this one, before it is refilled.
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
     }
 
