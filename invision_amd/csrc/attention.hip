@@ -26,7 +26,8 @@
 //                16c + 8*(l/32) + 0..7 -- the contiguous 16 bytes its V^T fragment
 //                reads.  No cross-lane shuffle of P is needed.
 // Softmax runs in the exp2 domain: exp(scale*s - m) = exp2(s*scale*log2e - m'),
-// on the hardware exp2; P is rounded to bf16 (nearest-even) for the second MFMA.
+// on the hardware exp2; P is rounded to bf16 (nearest-even) for the second MFMA,
+// and the row sum is taken over those same bf16 weights (v_dot2_f32_bf16).
 #include "attention.hpp"
 
 namespace inv {
@@ -61,6 +62,15 @@ __device__ __forceinline__ int quadswap(int r) { return (((r >> 2) ^ (r >> 3)) &
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Hardware dispatches workgroup b to XCD b % 8: the logical index whose
+// consecutive values share an XCD, so the query blocks of one head meet its K
+// and V in one L2.
+__device__ __forceinline__ int xcd_order(int bid, int count) {
+    const int per = count >> 3, rem = count & 7;
+    const int xcd = bid & 7, local = bid >> 3;
+    return (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+}
+
 #endif  // __HIP_DEVICE_COMPILE__
 
 // The body exists only in the device pass; the host pass needs the launch stub
@@ -86,9 +96,13 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int lq = lane & 31, lh = lane >> 5;
-    const int head = blockIdx.y;
+    // 1-D grid of heads x query blocks; causal blocks run longest first.
+    const int nqb = (p.seq_q + BQ - 1) / BQ;
+    const int L = xcd_order(blockIdx.x, nqb * p.heads);
+    const int head = L / nqb;
+    const int qb = CAUSAL ? nqb - 1 - L % nqb : L % nqb;
     const int kvh = head / (p.heads / p.kv_heads);
-    const int q0 = blockIdx.x * BQ;
+    const int q0 = qb * BQ;
     const int my_q = q0 + wave * 32 + lq;
 
     // This wave's Q rows as the B operand of S^T = K Q^T (zero past seq_q).
@@ -244,16 +258,10 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
             m_run = m_new;
         }
         const float m_use = (m_run == -__builtin_inff()) ? 0.f : m_run;  // no key seen yet
-        float ls = 0.f;
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float e = exp2_hw(fmaf(s[b][r], sl2, -m_use));
-                s[b][r] = e;
-                ls += e;
-            }
-        l_run += ls;
+            for (int r = 0; r < 16; ++r) s[b][r] = exp2_hw(fmaf(s[b][r], sl2, -m_use));
 
         // O^T += V^T P^T over the 4 chunks of 16 keys, V^T fragments one chunk ahead.
 #pragma unroll
@@ -265,6 +273,13 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
             const bf16x8_t pf = __builtin_convertvector(pv, bf16x8_t);
 #pragma unroll
             for (int i = 0; i < ND; ++i) o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[kc4 & 1][i], pf, o[i], 0, 0, 0);
+            // the row sum of the same bf16 weights the MFMA multiplies, two per dot2
+            typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+            const bf16x2_t one2 = {(__bf16)1.0f, (__bf16)1.0f};
+            l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 0, 1), one2, l_run, false);
+            l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 2, 3), one2, l_run, false);
+            l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 4, 5), one2, l_run, false);
+            l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 6, 7), one2, l_run, false);
         }
 
         // The next tile has landed in the other buffer, and every wave is done
@@ -299,7 +314,7 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
 
 template <int D, bool CAUSAL, int OUT>
 hipError_t launch3(const AttnParams &p, hipStream_t s) {
-    const dim3 grid((unsigned)((p.seq_q + kAttnBlockQ - 1) / kAttnBlockQ), (unsigned)p.heads);
+    const dim3 grid((unsigned)(((p.seq_q + kAttnBlockQ - 1) / kAttnBlockQ) * p.heads));
     hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL, OUT>), grid, dim3(256), 0, s, p);
     return hipGetLastError();
 }

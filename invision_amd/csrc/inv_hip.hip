@@ -979,7 +979,8 @@ int inv_hip_attention(const void *Q, const void *K, const void *V, void *O, int 
     if (seq_q == 0) return INV_OK;
     if (seq_k == 0) return fail(INV_ERR_ARG, "attention: seq_k is 0 (a softmax over no keys)");
     if (!Q || !K || !V || !O) return fail(INV_ERR_ARG, "attention: Q, K, V or O is null");
-    if (heads > 65535 || seq_q > INT32_MAX / 2 || seq_k > INT32_MAX / 2)
+    if (seq_q > INT32_MAX / 2 || seq_k > INT32_MAX / 2 ||
+        ((seq_q + inv::kAttnBlockQ - 1) / inv::kAttnBlockQ) * heads > INT32_MAX)
         return fail(INV_ERR_UNSUPPORTED, "attention: too many heads or tokens");
     const int64_t hq = heads * head_dim, hk = kv_heads * head_dim;
     const int64_t ldv = round_up(seq_k, inv::kAttnBlockK);
