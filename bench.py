@@ -57,6 +57,8 @@ WORKLOADS = {
                      "bf16"),
     "flux2_gated_out": ("FLUX2 attention out-projection into the gated fp32 residual", 4608, 3072, 3072, False,
                         "gated_add", "bf16", "f32"),
+    "flux2_adaln_qkv": ("FLUX2 AdaLN of the fp32 residual stream fused into the QKV projection", 4608, 3072, 9216,
+                        False, "adaln", "f32", "f32"),
 }
 
 
@@ -115,6 +117,11 @@ def run_workload(name, steps, warmup, check=True, host_path=False, warmup_second
     xd = q.DeviceArray.from_host(Xin, xdt)
     yd = q.DeviceArray((M, N), ydt)
     gd = None
+    if epi == "adaln":
+        rng = np.random.default_rng(3)
+        shift = (rng.standard_normal(K, dtype=np.float32) * np.float32(0.3)).astype(np.float32)
+        scale = (rng.standard_normal(K, dtype=np.float32) * np.float32(0.3)).astype(np.float32)
+        sd, hd = q.DeviceArray.from_host(scale, "f32"), q.DeviceArray.from_host(shift, "f32")
     if epi == "gated_add":
         rng = np.random.default_rng(1)
         Y0 = rng.standard_normal((M, N), dtype=np.float32)
@@ -123,7 +130,10 @@ def run_workload(name, steps, warmup, check=True, host_path=False, warmup_second
         gd = q.DeviceArray.from_host(gate, "f32")
 
     def launch():
-        if epi == "gated_add":
+        if epi == "adaln":
+            hip.call("inv_hip_linear_norm", xd.ptr, hip.INV_NORM_ADALN, sd.ptr, hd.ptr, q.EPSILON, w.handle, None,
+                     yd.ptr, yd.inv_dtype, M, K, N, hip.INV_EPI_NONE, hip.INV_FLAG_DEVICE_PTRS | hip.INV_FLAG_ASYNC)
+        elif epi == "gated_add":
             q.linear_gated_add_device(xd, w, yd, M, gate=gd, asynchronous=True)
         else:
             q.linear_device(xd, w, yd, M, epilogue=epi, asynchronous=True)
@@ -185,7 +195,12 @@ def run_workload(name, steps, warmup, check=True, host_path=False, warmup_second
         Y = Y1 if epi == "gated_add" else yd.to_host()
         Yf = bf16_bits_to_f32(Y) if ydt == "bf16" else Y.astype(np.float64)
         rows = np.unique(np.linspace(0, M - 1, num=min(M, 6)).astype(int))
-        Xr = bf16_bits_to_f32(as_bf16_bits(X[rows])).astype(np.float64)
+        Xs = X[rows]
+        if epi == "adaln":
+            Xs = Xs.astype(np.float64)
+            mu = Xs.mean(1, keepdims=True)
+            Xs = (1 + scale) * ((Xs - mu) / np.sqrt(((Xs - mu) ** 2).mean(1, keepdims=True) + 1e-6)) + shift
+        Xr = bf16_bits_to_f32(as_bf16_bits(np.asarray(Xs, np.float32))).astype(np.float64)
         ref = Xr @ bf16_bits_to_f32(W).astype(np.float64).T
         if has_bias:
             ref += b.astype(np.float64)
@@ -205,6 +220,9 @@ def run_workload(name, steps, warmup, check=True, host_path=False, warmup_second
     w.free()
     if gd is not None:
         gd.free()
+    if epi == "adaln":
+        sd.free()
+        hd.free()
     return res
 
 
@@ -357,7 +375,10 @@ def profile_run(args):
     a.free()
     b.free()
     log(f"[profile] copy calibration: 5 x copy_words16 of {n} bytes")
-    res = run_workload(args.workload, args.steps, args.warmup, check=False, warmup_seconds=args.warmup_seconds)
+    if args.workload in ATTN_WORKLOADS:
+        res = run_attention(args.workload, args.steps, warmup_seconds=args.warmup_seconds, check=False)
+    else:
+        res = run_workload(args.workload, args.steps, args.warmup, check=False, warmup_seconds=args.warmup_seconds)
     log(f"[profile] {json.dumps(res)}")
     print(json.dumps({"profile_run": args.workload, "copy_bytes": n, **res}), flush=True)
     q.shutdown()
@@ -462,7 +483,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10, help="minimum warm-up steps")
     ap.add_argument("--warmup-seconds", type=float, default=1.5,
                     help="minimum seconds of back-to-back warm-up steps before timing")
-    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS),
+                    help="GEMM shape for the bench line; attention shapes only with --profile-run")
     ap.add_argument("--all", action="store_true", help="also time every workload shape (stderr)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-mfma-ceiling", action="store_true",
@@ -484,6 +506,9 @@ def main():
     log(f"[bench] device: {info}")
     if args.profile_run:
         return profile_run(args)
+    if args.workload in ATTN_WORKLOADS:
+        print("the bench line is a GEMM shape; attention shapes run with --all or --profile-run", file=sys.stderr)
+        return 2
 
     res = run_workload(args.workload, args.steps, args.warmup, host_path=True, warmup_seconds=args.warmup_seconds)
     log(f"[bench] {json.dumps(res)}")

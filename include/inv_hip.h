@@ -176,6 +176,25 @@ int inv_hip_linear(const void *X, int x_dtype, inv_weight_t W, const float *bias
 int inv_hip_linear_gated_add(const void *X, int x_dtype, inv_weight_t W, const float *bias,
                              const float *gate, float *Y, int64_t M, int64_t K, int64_t N, int flags);
 
+/* ---- normalised projections ------------------------------------------------ */
+#define INV_NORM_ADALN 1 /* (1 + scale[k]) * (x - mean) / sqrt(var + eps) + shift[k], population
+                            variance over the row: QNNAdaLN (src/quicknncpu.pas:3042-3060)    */
+#define INV_NORM_RMS   2 /* x * weight[k] / sqrt(mean(x^2) + eps); weight may be NULL:
+                            QNNRMSNorm (src/quicknncpu.pas:2159-2185)                          */
+/* Y = epilogue(norm(X) . W^T + bias) for the fp32 residual stream X [M x K]:
+ * replaces QNNAdaLN (or QNNRMSNorm) into a scratch activation followed by the
+ * projection (e.g. src/quicknn_transformers.pas:1400-1404, 1440-1441).  The
+ * normalisation runs while X is rounded into the GEMM's bf16 operand, so it
+ * costs the same one pass over X as the plain fp32 path, and the normalised
+ * activation is never stored.  norm_scale / norm_shift are [K] fp32 (AdaLN:
+ * both required; RMS: weight or NULL, shift NULL).  The reference uses
+ * EPSILON = 1e-6 (src/quicknn_common.pas:51) whatever eps its callers pass;
+ * give 1e-6 to match.  flags: INV_FLAG_DEVICE_PTRS (X, Y, bias and the norm
+ * vectors on the device), INV_FLAG_ASYNC. */
+int inv_hip_linear_norm(const float *X, int norm, const float *norm_scale, const float *norm_shift,
+                        float eps, inv_weight_t W, const float *bias, void *Y, int y_dtype, int64_t M,
+                        int64_t K, int64_t N, int epilogue, int flags);
+
 /* ---- attention ------------------------------------------------------------ */
 #define INV_ATTN_CAUSAL 0x100 /* key j is visible to query i iff j <= i + (seq_k - seq_q) */
 /* O = softmax(scale * Q . K^T) . V for every head, in the reference's

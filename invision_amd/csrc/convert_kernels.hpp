@@ -76,6 +76,148 @@ __global__ void __launch_bounds__(256) cvt_rows_f32_bf16(const float *__restrict
     for (int sg = 0; sg < nseg; ++sg) *(uint4 *)(d + sg * cols_pad) = ((lo_mask >> sg) & 1) ? olo : ohi;
 }
 
+// Normalisations that precede the reference's projections, applied while the
+// fp32 activation is rounded into the GEMM's bf16 operand (the same one read of
+// X and one bf16 write the plain conversion costs):
+//  NORM_ADALN: (1 + a[c]) * ((x - mean) * rstd) + b[c], rstd = 1 / sqrt(var + eps),
+//              mean and population variance over the row (QNNAdaLN,
+//              src/quicknncpu.pas:3042-3060; QNNMean :679-685, QNNVariance :687-695);
+//  NORM_RMS:   x * rstd * a[c] (a may be null), rstd = 1 / sqrt(sum(x^2) / cols + eps)
+//              (QNNRMSNorm, src/quicknncpu.pas:2159-2185).
+// One workgroup of 256 threads per row; the row is read from L2 once per pass.
+// Columns cols..cols_pad-1 are zero; cols_pad % 8 == 0, ldd % 8 == 0, dst 16-byte aligned.
+enum { NORM_ADALN = 1, NORM_RMS = 2 };
+
+// Sum over the 256 threads of a workgroup (4 waves of 64); every thread gets it.
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    __syncthreads();  // red is free (a previous call's readers are done)
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+template <int NORM>
+__global__ void __launch_bounds__(256) norm_rows_f32_bf16(const float *__restrict__ src, int64_t lds,
+                                                          const float *__restrict__ a, const float *__restrict__ b,
+                                                          float eps, uint16_t *__restrict__ dst, int64_t ldd,
+                                                          int64_t cols, int64_t cols_pad) {
+    __shared__ float red[4];
+    const int64_t r = blockIdx.x;
+    const float *x = src + r * lds;
+    float mean = 0.0f, rstd;
+    if constexpr (NORM == NORM_ADALN) {
+        float s = 0.0f;
+        for (int64_t c = threadIdx.x; c < cols; c += 256) s += x[c];
+        mean = block_sum256(s, red) / (float)cols;
+        float q = 0.0f;
+        for (int64_t c = threadIdx.x; c < cols; c += 256) {
+            const float d = x[c] - mean;
+            q += d * d;
+        }
+        rstd = 1.0f / sqrtf(block_sum256(q, red) / (float)cols + eps);
+    } else {
+        float q = 0.0f;
+        for (int64_t c = threadIdx.x; c < cols; c += 256) q += x[c] * x[c];
+        rstd = 1.0f / sqrtf(block_sum256(q, red) / (float)cols + eps);
+    }
+    for (int64_t c0 = (int64_t)threadIdx.x * 8; c0 < cols_pad; c0 += 256 * 8) {
+        uint16_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int64_t c = c0 + e;
+            float y = 0.0f;
+            if (c < cols) {
+                if constexpr (NORM == NORM_ADALN)
+                    y = (1.0f + a[c]) * ((x[c] - mean) * rstd) + b[c];
+                else
+                    y = a ? x[c] * rstd * a[c] : x[c] * rstd;
+            }
+            h[e] = bf16_rne(y);
+        }
+        *(uint4 *)(dst + r * ldd + c0) = pack8(h);
+    }
+}
+
+// The same normalisation with the row held in registers (one read of X):
+// thread t owns the 4-column groups t, t + 256, ... (J of them); cols % 4 == 0,
+// cols <= 4 * 256 * J, src rows 16-byte aligned.  J is the smallest of 1, 2, 4,
+// 8, 16 that holds the row, so short rows keep few registers and many rows in flight.
+constexpr int NORM_ROW_GROUPS = 16;  // rows up to 16384 columns
+
+template <int NORM, int J>
+__global__ void __launch_bounds__(256) norm_rows_f32_bf16_reg(const float *__restrict__ src, int64_t lds,
+                                                              const float *__restrict__ a,
+                                                              const float *__restrict__ b, float eps,
+                                                              uint16_t *__restrict__ dst, int64_t ldd, int64_t cols,
+                                                              int64_t cols_pad) {
+    __shared__ float red[4];
+    const int64_t r = blockIdx.x;
+    const float *x = src + r * lds;
+    const int ng = (int)(cols >> 2);
+    // All loads first (a clamped, always valid address; groups past the row are
+    // zeroed after) so they are in flight together.
+    float4 v[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) v[j] = *(const float4 *)(x + 4 * min((int)threadIdx.x + 256 * j, ng - 1));
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+        if ((int)threadIdx.x + 256 * j >= ng) v[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+        s += (NORM == NORM_ADALN) ? (v[j].x + v[j].y) + (v[j].z + v[j].w)
+                                  : (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+    float mean = 0.0f, rstd;
+    if constexpr (NORM == NORM_ADALN) {
+        mean = block_sum256(s, red) / (float)cols;
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            if ((int)threadIdx.x + 256 * j < ng) {
+                const float d0 = v[j].x - mean, d1 = v[j].y - mean, d2 = v[j].z - mean, d3 = v[j].w - mean;
+                q += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+            }
+        }
+        rstd = 1.0f / sqrtf(block_sum256(q, red) / (float)cols + eps);
+    } else {
+        rstd = 1.0f / sqrtf(block_sum256(s, red) / (float)cols + eps);
+    }
+    uint16_t *d = dst + r * ldd;
+    // the per-column vectors, likewise loaded together (clamped columns)
+    float av[J][4], bv[J][4];
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int c = 4 * min((int)threadIdx.x + 256 * j, ng - 1) + e;
+            av[j][e] = a ? a[c] : 1.0f;
+            bv[j][e] = (NORM == NORM_ADALN) ? b[c] : 0.0f;
+        }
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int g = threadIdx.x + 256 * j;
+        if (g < ng) {
+            const float xv[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+            uint16_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float y;
+                if constexpr (NORM == NORM_ADALN)
+                    y = (1.0f + av[j][e]) * ((xv[e] - mean) * rstd) + bv[j][e];
+                else
+                    y = xv[e] * rstd * av[j][e];
+                h[e] = bf16_rne(y);
+            }
+            *(uint2 *)(d + 4 * g) = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16),
+                                               (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+        }
+    }
+    // zero padding up to cols_pad (fewer than 8 columns: at most one group of 4)
+    if (threadIdx.x < (cols_pad >> 2) - ng) *(uint2 *)(d + 4 * (ng + threadIdx.x)) = make_uint2(0u, 0u);
+}
+
 // dst[r, c] = src[r, c] (bf16) for c < cols, 0 up to cols_pad.  One thread per 8 outputs.
 __global__ void __launch_bounds__(256) copy_rows_bf16(const uint16_t *__restrict__ src, int64_t lds,
                                                       uint16_t *__restrict__ dst, int64_t ldd, int64_t rows,

@@ -81,6 +81,7 @@ struct State {
     char name[256] = {0};
     Buf xin, x16, w16, win, yout, cin, bias, gate;
     Buf aq, ak, avt, aqin, akin, avin;  // attention operands (bf16) and their staging
+    Buf nvec;                           // normalisation scale/shift vectors from host
     // Split/stream-K partial sums and arrival counters: uncached device memory
     // (coherent across XCDs without L2 maintenance).  Such memory is never
     // freed once a kernel has read it: outgrown buffers are retired, not freed.
@@ -669,8 +670,64 @@ int gemm_slot(int order, int transA, int transB, int64_t M, int64_t N, int64_t K
 
 // Y = epilogue(X . W^T + bias), or with accumulate Y += gate[n] * (X . W^T + bias)
 // (gate null: a plain residual add).  Y stays fp32 when accumulating.
+// A row normalisation applied while the fp32 X is rounded into the bf16 operand.
+struct NormArgs {
+    int kind;            // INV_NORM_ADALN or INV_NORM_RMS
+    const float *scale;  // AdaLN scale (the 1 + scale factor) or RMS weight, [K]
+    const float *shift;  // AdaLN shift [K]; null for RMS
+    float eps;
+};
+
+// Stage X = norm(X_f32) as bf16 [M x round_up(K, 8)] in g.x16 (X, scale and
+// shift host or device per `dev`).
+int stage_normalized(const char *who, const float *X, const NormArgs &nm, bool dev, int64_t M, int64_t K,
+                     const uint16_t **out, int64_t *out_ld) {
+    const int64_t ldw = round_up(K, 8);
+    const float *xd = X, *ad = nm.scale, *bd = nm.shift;
+    if (!dev) {
+        TRY(ensure(g.xin, (size_t)(M * K) * 4));
+        TRY(h2d_rows(g.xin.p, X, M, (size_t)K * 4, (size_t)K * 4));
+        xd = (const float *)g.xin.p;
+        const size_t vb = (size_t)K * 4;
+        TRY(ensure(g.nvec, 2 * vb));
+        if (nm.scale) TRY(h2d_rows(g.nvec.p, nm.scale, 1, vb, vb));
+        if (nm.shift) TRY(h2d_rows((char *)g.nvec.p + vb, nm.shift, 1, vb, vb));
+        ad = nm.scale ? (const float *)g.nvec.p : nullptr;
+        bd = nm.shift ? (const float *)((char *)g.nvec.p + vb) : nullptr;
+    } else if (!aligned(X, 4)) {
+        return fail(INV_ERR_ARG, "%s: X not 4-byte aligned", who);
+    }
+    TRY(ensure(g.x16, (size_t)(M * ldw) * 2));
+    uint16_t *d = (uint16_t *)g.x16.p;
+    const bool in_regs = K % 4 == 0 && K <= 4 * 256 * inv::NORM_ROW_GROUPS && aligned(xd, 16);
+    if (in_regs) {
+        const int64_t groups = (K / 4 + 255) / 256;  // register groups of 4 columns per thread
+        auto launch = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3((unsigned)M), dim3(256), 0, g.stream, xd, K, ad, bd, nm.eps, d, ldw, K,
+                               ldw);
+        };
+        const bool ada = nm.kind == INV_NORM_ADALN;
+        using namespace inv;
+        if (groups <= 1) ada ? launch(norm_rows_f32_bf16_reg<NORM_ADALN, 1>) : launch(norm_rows_f32_bf16_reg<NORM_RMS, 1>);
+        else if (groups <= 2) ada ? launch(norm_rows_f32_bf16_reg<NORM_ADALN, 2>) : launch(norm_rows_f32_bf16_reg<NORM_RMS, 2>);
+        else if (groups <= 4) ada ? launch(norm_rows_f32_bf16_reg<NORM_ADALN, 4>) : launch(norm_rows_f32_bf16_reg<NORM_RMS, 4>);
+        else if (groups <= 8) ada ? launch(norm_rows_f32_bf16_reg<NORM_ADALN, 8>) : launch(norm_rows_f32_bf16_reg<NORM_RMS, 8>);
+        else ada ? launch(norm_rows_f32_bf16_reg<NORM_ADALN, 16>) : launch(norm_rows_f32_bf16_reg<NORM_RMS, 16>);
+    } else if (nm.kind == INV_NORM_ADALN)
+        hipLaunchKernelGGL(inv::norm_rows_f32_bf16<inv::NORM_ADALN>, dim3((unsigned)M), dim3(256), 0, g.stream, xd, K,
+                           ad, bd, nm.eps, d, ldw, K, ldw);
+    else
+        hipLaunchKernelGGL(inv::norm_rows_f32_bf16<inv::NORM_RMS>, dim3((unsigned)M), dim3(256), 0, g.stream, xd, K,
+                           ad, bd, nm.eps, d, ldw, K, ldw);
+    HIPCHK(hipGetLastError());
+    *out = d;
+    *out_ld = ldw;
+    return INV_OK;
+}
+
 int linear_impl(const char *who, const void *X, int x_dtype, inv_weight_t W, const float *bias, void *Y, int y_dtype,
-                int64_t M, int64_t K, int64_t N, int epilogue, int flags, bool accumulate, const float *gate) {
+                int64_t M, int64_t K, int64_t N, int epilogue, int flags, bool accumulate, const float *gate,
+                const NormArgs *nm = nullptr) {
     TRY(check_init());
     if (!valid_weight(W)) return fail(INV_ERR_ARG, "%s: unknown weight handle", who);
     if (x_dtype != INV_DT_F32 && x_dtype != INV_DT_BF16) return fail(INV_ERR_ARG, "%s: bad x_dtype %d", who, x_dtype);
@@ -703,8 +760,13 @@ int linear_impl(const char *who, const void *X, int x_dtype, inv_weight_t W, con
     const uint16_t *Xd = nullptr;
     int64_t ldx = 0;
     const int64_t kseg = precise ? round_up(K, 64) : W->ldw;
-    TRY(stage_operand(X, x_dtype, dev, false, M, K, K, precise ? 2 : 1, precise ? 0x2 : 0, precise ? 64 : 8, g.x16,
-                      g.xin, &Xd, &ldx));
+    if (nm) {
+        if (precise) return fail(INV_ERR_UNSUPPORTED, "%s: INV_FLAG_PRECISE with a normalisation", who);
+        TRY(stage_normalized(who, (const float *)X, *nm, dev, M, K, &Xd, &ldx));
+    } else {
+        TRY(stage_operand(X, x_dtype, dev, false, M, K, K, precise ? 2 : 1, precise ? 0x2 : 0, precise ? 64 : 8,
+                          g.x16, g.xin, &Xd, &ldx));
+    }
 
     // Bias: explicit argument first, else the handle's.
     const float *bd = W->bias;
@@ -822,7 +884,7 @@ int inv_hip_shutdown(void) {
     for (auto *w : g.weights) free_weight(w);
     g.weights.clear();
     for (Buf *b : {&g.xin, &g.x16, &g.w16, &g.win, &g.yout, &g.cin, &g.bias, &g.gate, &g.aq, &g.ak, &g.avt, &g.aqin,
-                   &g.akin, &g.avin}) release(*b);
+                   &g.akin, &g.avin, &g.nvec}) release(*b);
     // g.partial / g.counters (uncached) stay allocated until the process ends.
     for (int k = 0; k < 2; ++k) {
         if (g.pin[k]) (void)hipHostFree(g.pin[k]);
@@ -955,6 +1017,19 @@ int inv_hip_linear_gated_add(const void *X, int x_dtype, inv_weight_t W, const f
     std::lock_guard<std::mutex> lk(g_mu);
     return linear_impl("linear_gated_add", X, x_dtype, W, bias, Y, INV_DT_F32, M, K, N, INV_EPI_NONE, flags, true,
                        gate);
+}
+
+int inv_hip_linear_norm(const float *X, int norm, const float *norm_scale, const float *norm_shift, float eps,
+                        inv_weight_t W, const float *bias, void *Y, int y_dtype, int64_t M, int64_t K, int64_t N,
+                        int epilogue, int flags) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (norm != INV_NORM_ADALN && norm != INV_NORM_RMS) return fail(INV_ERR_ARG, "linear_norm: bad norm %d", norm);
+    if (norm == INV_NORM_ADALN && (!norm_scale || !norm_shift))
+        return fail(INV_ERR_ARG, "linear_norm: AdaLN needs scale and shift");
+    if (norm == INV_NORM_RMS && norm_shift) return fail(INV_ERR_ARG, "linear_norm: RMSNorm takes no shift");
+    if (!(eps >= 0.0f) || eps > 3.0e38f) return fail(INV_ERR_ARG, "linear_norm: eps must be finite and >= 0");
+    const NormArgs nm{norm, norm_scale, norm_shift, eps};
+    return linear_impl("linear_norm", X, INV_DT_F32, W, bias, Y, y_dtype, M, K, N, epilogue, flags, false, nullptr, &nm);
 }
 
 int inv_hip_attention(const void *Q, const void *K, const void *V, void *O, int in_dtype, int out_dtype,

@@ -41,6 +41,8 @@ INV_FLAG_DEVICE_PTRS = 0x1
 INV_FLAG_ASYNC = 0x2
 INV_FLAG_PRECISE = 0x4
 INV_ATTN_CAUSAL = 0x100
+INV_NORM_ADALN = 1
+INV_NORM_RMS = 2
 
 INV_ST_MAX_DIMS = 8
 INV_ST_TRUNCATE = 0x1
@@ -70,6 +72,8 @@ _PROTOS = {
                                c_int, c_int]),
     "inv_hip_linear_gated_add": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
                                          c_int64, c_int]),
+    "inv_hip_linear_norm": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_int,
+                                    c_int64, c_int64, c_int64, c_int, c_int]),
     "inv_hip_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int64, c_int64, c_int64,
                                   c_int64, c_int64, c_float, c_int]),
     "inv_hip_sgemm": (c_int, [c_int, c_int, c_int, c_int64, c_int64, c_int64, c_float, c_void_p, c_int64, c_void_p,

@@ -270,6 +270,56 @@ def linear_gated_add(y: np.ndarray, x: np.ndarray, W: Weight, gate: Optional[np.
     return y
 
 
+_NORM = {"adaln": hip.INV_NORM_ADALN, "rms": hip.INV_NORM_RMS}
+EPSILON = 1e-6  # the reference's normalisation epsilon (src/quicknn_common.pas:51)
+
+
+def linear_norm(x: np.ndarray, norm: str, W: Weight, scale: Optional[np.ndarray], shift: Optional[np.ndarray] = None,
+                bias: Optional[np.ndarray] = None, epilogue: str = "none", out_dtype: str = "f32",
+                eps: float = EPSILON) -> np.ndarray:
+    """Host arrays: Y = epi(norm(x) . W^T + bias), norm "adaln" ((1 + scale) * layernorm(x) + shift,
+    QNNAdaLN) or "rms" (x * scale / rms(x), QNNRMSNorm), x fp32 [M x K]."""
+    _check_host(x, np.float32, "x")
+    if x.ndim != 2 or x.shape[1] != W.K:
+        raise ValueError(f"x must be [M x {W.K}]")
+    vecs = []
+    for v, nm in ((scale, "scale"), (shift, "shift"), (bias, "bias")):
+        if v is not None:
+            v = np.ascontiguousarray(v, dtype=np.float32)
+            if v.size != (W.N if nm == "bias" else W.K):
+                raise ValueError(f"{nm} has {v.size} values")
+        vecs.append(v)
+    sc, sh, b = vecs
+    ydt, ynp = (hip.INV_DT_F32, np.float32) if out_dtype == "f32" else (hip.INV_DT_BF16, np.uint16)
+    y = np.empty((x.shape[0], W.N), dtype=ynp)
+    hip.call("inv_hip_linear_norm", _ptr(x), _NORM[norm], _ptr(sc) if sc is not None else None,
+             _ptr(sh) if sh is not None else None, float(eps), W.handle, _ptr(b) if b is not None else None, _ptr(y),
+             ydt, x.shape[0], W.K, W.N, _EPI[epilogue], 0)
+    return y
+
+
+def QNNAdaLNLinear(dst: np.ndarray, x: np.ndarray, shift: np.ndarray, scale: np.ndarray, weight, weight_bf16,
+                   seq: int, hidden: int, dstDim: int) -> None:
+    """QNNAdaLN(norm, x, shift, scale, seq, hidden) then QNNLINEAR_BF16_OR_F32(dst, norm, ...)
+    (src/quicknn_transformers.pas:1400-1404), as one normalising projection."""
+    _bound(weight is not None or weight_bf16 is not None,
+           "ERROR QNNLINEAR_BF16_OR_F32 : no weight or weight_16 assigned!")
+    for a, nm in ((dst, "dst"), (x, "x"), (shift, "shift"), (scale, "scale")):
+        _check_host(a, np.float32, nm)
+    _bound(x.size >= seq * hidden and dst.size >= seq * dstDim, "ERROR : QNNAdaLN out of bound")
+    _bound(shift.size >= hidden and scale.size >= hidden, "ERROR : QNNAdaLN out of bound [shift/scale]")
+    W = weight_bf16 if weight_bf16 is not None else weight
+    w = _linear_weight(W)
+    try:
+        _bound(w.N == dstDim and w.K == hidden, "ERROR : QNNLinear weight shape mismatch")
+        _bound(not w.has_bias, "ERROR : QNNLINEAR_BF16_OR_F32 takes no bias")
+        hip.call("inv_hip_linear_norm", _ptr(x), hip.INV_NORM_ADALN, _ptr(scale), _ptr(shift), EPSILON, w.handle, None,
+                 _ptr(dst), hip.INV_DT_F32, seq, hidden, dstDim, hip.INV_EPI_NONE, 0)
+    finally:
+        if w is not W:
+            w.free()
+
+
 def attention(Q: np.ndarray, K: np.ndarray, V: np.ndarray, heads: int, head_dim: int, kv_heads: Optional[int] = None,
               scale: Optional[float] = None, causal: bool = False, out_dtype: str = "f32") -> np.ndarray:
     """Host arrays: O[seq_q x heads*head_dim] = softmax(scale * Q.K^T) V per head.

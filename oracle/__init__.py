@@ -21,6 +21,9 @@ How each oracle function is pinned:
   * linear (quicknncpu.pas:1807-1847): closed form with bias.
   * gated add (quicknncpu.pas:853-859): numpy's fp32 elementwise product and
     sum (bit-exact), gate = 0 leaves dst unchanged, gate = 1 is dst + proj.
+  * AdaLN / RMSNorm (quicknncpu.pas:3042-3060, 2159-2198): numpy float64
+    layer and RMS norms; zero shift/scale rows have mean 0 and variance 1;
+    invariance to a per-row offset (AdaLN) and to a per-row scale (both).
   * attention (quicknn_transformers.pas:1150-1311; quicknn_qwen3.pas:727-769):
     numpy float64 softmax(QK^T)V per head; invariants (constant V, one key,
     equal keys, a vector added to every key, the causal prefix); the restated
@@ -92,6 +95,8 @@ def lib() -> ctypes.CDLL:
         L.orc_attention_qnn.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                         c_int64, c_float, c_int, c_int]
         L.orc_softmax_qnn.argtypes = [c_void_p, c_int64]
+        L.orc_adaln.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64]
+        L.orc_rmsnorm_rows.argtypes = [c_void_p, c_void_p, c_void_p, c_int64, c_int64]
         L.orc_add_bias_rows.argtypes = [c_void_p, c_void_p, c_int64, c_int64]
         L.orc_has_avx2.restype = c_int
         L.orc_max_threads.restype = c_int
@@ -276,6 +281,25 @@ def softmax_qnn(x: np.ndarray) -> np.ndarray:
     """sSoftmax_avx2 restated (exact 1/sum) on a copy of a 1-D fp32 array."""
     y = np.ascontiguousarray(x, dtype=np.float32).copy()
     lib().orc_softmax_qnn(_p(y), y.size)
+    return y
+
+
+def adaln(x: np.ndarray, shift: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """QNNAdaLN (quicknncpu.pas:3042-3060): (1 + scale) * layernorm(x) + shift per row."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    sh = np.ascontiguousarray(shift, dtype=np.float32)
+    sc = np.ascontiguousarray(scale, dtype=np.float32)
+    lib().orc_adaln(_p(y), _p(x), _p(sh), _p(sc), x.shape[0], x.shape[1])
+    return y
+
+
+def rmsnorm_rows(x: np.ndarray, weight=None) -> np.ndarray:
+    """QNNRMSNormRows (quicknncpu.pas:2159-2198): x * weight / rms(x) per row."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    w = np.ascontiguousarray(weight, dtype=np.float32) if weight is not None else None
+    lib().orc_rmsnorm_rows(_p(y), _p(x), _p(w) if w is not None else None, x.shape[0], x.shape[1])
     return y
 
 

@@ -615,3 +615,42 @@ int orc_attention_qnn(const float *Q, const float *K, const float *V, float *O, 
     }
     return bad ? -2 : 0;
 }
+
+/* ---- normalisations before the projections ---------------------------------
+ * EPSILON = 1e-6 (quicknn_common.pas:51).  QNNAdaLN's eps argument is not used
+ * by its body (quicknncpu.pas:3052): the constant always applies. */
+
+/* QNNAdaLN (quicknncpu.pas:3042-3060): per row, mean = QNNSum / N (:679-685),
+ * population variance = sum((x - mean)^2) / N (:687-695), stdInv = 1/sqrt(var +
+ * EPSILON), out = (1 + scale[j]) * ((x - mean) * stdInv) + shift[j]. */
+void orc_adaln(float *dst, const float *src, const float *shift, const float *scale, int64_t seq, int64_t hidden) {
+    for (int64_t i = 0; i < seq; ++i) {
+        const float *x = src + i * hidden;
+        float *y = dst + i * hidden;
+        float sum = 0.0f;
+        for (int64_t j = 0; j < hidden; ++j) sum += x[j];
+        const float mean = sum / (float)hidden;
+        float sq = 0.0f;
+        for (int64_t j = 0; j < hidden; ++j) sq += (x[j] - mean) * (x[j] - mean);
+        const float var = sq / (float)hidden;
+        const float inv = 1.0f / sqrtf(var + 1e-6f);
+        for (int64_t j = 0; j < hidden; ++j) {
+            const float norm = (x[j] - mean) * inv;
+            y[j] = (1.0f + scale[j]) * norm + shift[j];
+        }
+    }
+}
+
+/* QNNRMSNormRows / QNNRMSNorm (quicknncpu.pas:2159-2198): invRMS = 1/sqrt(
+ * QNNSumSqr / N + EPSILON); dst = src * weights * invRMS (src * invRMS without
+ * weights). */
+void orc_rmsnorm_rows(float *dst, const float *src, const float *weight, int64_t rows, int64_t dim) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *x = src + r * dim;
+        float *y = dst + r * dim;
+        float sq = 0.0f;
+        for (int64_t j = 0; j < dim; ++j) sq += x[j] * x[j];
+        const float inv = 1.0f / sqrtf(sq / (float)dim + 1e-6f);
+        for (int64_t j = 0; j < dim; ++j) y[j] = weight ? x[j] * weight[j] * inv : x[j] * inv;
+    }
+}

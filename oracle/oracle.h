@@ -88,6 +88,10 @@ int orc_attention_qnn(const float *Q, const float *K, const float *V, float *O, 
 /* sSoftmax_avx2 (ops_avx2.inc:552-760) with an exact 1/sum in place of rcpss. */
 void orc_softmax_qnn(float *x, int64_t n);
 
+/* ---- QNNAdaLN (quicknncpu.pas:3042-3060), QNNRMSNormRows (:2159-2198) ---- */
+void orc_adaln(float *dst, const float *src, const float *shift, const float *scale, int64_t seq, int64_t hidden);
+void orc_rmsnorm_rows(float *dst, const float *src, const float *weight, int64_t rows, int64_t dim);
+
 int orc_has_avx2(void);
 int orc_max_threads(void);
 

@@ -278,6 +278,33 @@ def test_gated_add_against_numpy_and_special_gates():
     assert not np.array_equal(got, d + g_rows[:, None] * pr)
 
 
+# ------------------------------------------------------- normalisations ----
+
+def test_adaln_and_rmsnorm_against_numpy_and_invariants():
+    x = _rand((9, 300), 70, 2.0) + np.float32(0.5)
+    sh, sc = _rand((300,), 71, 0.3), _rand((300,), 72, 0.3)
+    x64 = x.astype(np.float64)
+    mu = x64.mean(1, keepdims=True)
+    ln = (x64 - mu) / np.sqrt(((x64 - mu) ** 2).mean(1, keepdims=True) + 1e-6)
+    np.testing.assert_allclose(oracle.adaln(x, sh, sc), (1 + sc) * ln + sh, rtol=0, atol=2e-5)
+    z = np.zeros(300, np.float32)
+    y0 = oracle.adaln(x, z, z).astype(np.float64)
+    np.testing.assert_allclose(y0.mean(1), 0.0, atol=1e-5)
+    np.testing.assert_allclose(y0.var(1), 1.0, atol=1e-4)
+    # a per-row offset and a per-row positive scale leave the layer norm unchanged
+    xs = (x * np.float32(3.0) + np.float32(7.0)).astype(np.float32)
+    np.testing.assert_allclose(oracle.adaln(xs, sh, sc), oracle.adaln(x, sh, sc), rtol=0, atol=1e-4)
+    w = _rand((300,), 73)
+    rms = x64 / np.sqrt((x64 ** 2).mean(1, keepdims=True) + 1e-6)
+    np.testing.assert_allclose(oracle.rmsnorm_rows(x, w), rms * w, rtol=0, atol=2e-5)
+    np.testing.assert_allclose(oracle.rmsnorm_rows(x), rms, rtol=0, atol=2e-5)
+    np.testing.assert_allclose(oracle.rmsnorm_rows(x * np.float32(5.0), w), oracle.rmsnorm_rows(x, w), atol=1e-5)
+    # planted: sample variance (N-1) or a missing (1 + scale) are caught
+    bad = (1 + sc) * ((x64 - mu) / np.sqrt(((x64 - mu) ** 2).sum(1, keepdims=True) / 299 + 1e-6)) + sh
+    assert np.max(np.abs(oracle.adaln(x, sh, sc) - bad)) > 1e-4
+    assert np.max(np.abs(oracle.adaln(x, sh, sc) - (sc * ln + sh))) > 1e-2
+
+
 # ------------------------------------------------------------ attention ----
 
 def _np_attention(Q, K, V, heads, kv_heads, d, scale, causal=False):
