@@ -273,6 +273,51 @@ __global__ void __launch_bounds__(256) transpose_to_bf16(const SrcT *__restrict_
     }
 }
 
+// dst[c, r] = bf16(src[r, c]) for a [rows x cols] source with cols % 64 == 0,
+// 16-byte aligned rows (lds % 8 for bf16, % 4 for fp32), into [cols x rows_pad]
+// with rows_pad % 64 == 0 (zeros past rows): 64x64 tiles, 16-byte loads and
+// stores on both sides, the transpose itself through LDS.
+template <typename SrcT>
+__global__ void __launch_bounds__(256) transpose64_to_bf16(const SrcT *__restrict__ src, int64_t lds,
+                                                           uint16_t *__restrict__ dst, int64_t ldd, int64_t rows,
+                                                           int64_t rows_pad) {
+    constexpr int PITCH = 64 + 8;  // u16 per LDS row
+    __shared__ __attribute__((aligned(16))) uint16_t tile[64 * PITCH];
+    const int64_t r0 = (int64_t)blockIdx.y * 64;
+    const int64_t c0 = (int64_t)blockIdx.x * 64;
+    const int tid = threadIdx.x;
+    if constexpr (sizeof(SrcT) == 2) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int q = tid + 256 * i, row = q >> 3, cc = q & 7;
+            uint4 v = make_uint4(0u, 0u, 0u, 0u);
+            if (r0 + row < rows) v = *(const uint4 *)(src + (r0 + row) * lds + c0 + 8 * cc);
+            *(uint4 *)(tile + row * PITCH + 8 * cc) = v;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = tid + 256 * i, row = q >> 4, cc = q & 15;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (r0 + row < rows) v = *(const float4 *)(src + (r0 + row) * lds + c0 + 4 * cc);
+            uint16_t *t = tile + row * PITCH + 4 * cc;
+            t[0] = bf16_rne(v.x);
+            t[1] = bf16_rne(v.y);
+            t[2] = bf16_rne(v.z);
+            t[3] = bf16_rne(v.w);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int q = tid + 256 * i, oc = q >> 3, rr = q & 7;
+        uint16_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = tile[(8 * rr + e) * PITCH + oc];
+        *(uint4 *)(dst + (c0 + oc) * ldd + r0 + 8 * rr) = pack8(h);
+    }
+}
+
 // dst[i] = src[i] for n16 16-byte words, grid-stride (device-to-device copy of
 // resident buffers; also the reference kernel of known traffic, 2 x bytes).
 __global__ void __launch_bounds__(256) copy_words16(const uint4 *__restrict__ src, uint4 *__restrict__ dst,

@@ -449,8 +449,14 @@ int launch_transpose(const T *src, int64_t lds, uint16_t *dst, int64_t ldd, int6
     if (rows_pad == 0 || cols == 0) return INV_OK;
     dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows_pad + 63) / 64));
     if (grid.y > 65535) return fail(INV_ERR_UNSUPPORTED, "transpose: too many rows");
-    hipLaunchKernelGGL(inv::transpose_to_bf16<T>, grid, dim3(256), 0, g.stream, src, lds, dst, ldd, rows, cols,
-                       rows_pad, nseg, lo_mask);
+    const bool vec = nseg == 1 && cols % 64 == 0 && rows_pad % 64 == 0 && aligned(src, 16) &&
+                     lds % (16 / (int64_t)sizeof(T)) == 0 && aligned(dst, 16) && ldd % 8 == 0;
+    if (vec)
+        hipLaunchKernelGGL(inv::transpose64_to_bf16<T>, grid, dim3(256), 0, g.stream, src, lds, dst, ldd, rows,
+                           rows_pad);
+    else
+        hipLaunchKernelGGL(inv::transpose_to_bf16<T>, grid, dim3(256), 0, g.stream, src, lds, dst, ldd, rows, cols,
+                           rows_pad, nseg, lo_mask);
     HIPCHK(hipGetLastError());
     return INV_OK;
 }
