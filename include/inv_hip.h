@@ -204,7 +204,7 @@ int inv_hip_linear_norm(const float *X, int norm, const float *norm_scale, const
  * Replaces TQNNSingleOPS.QNNFlashAttention(dst, Q, K, V, heads, seq_q, seq_k,
  * head_dim, scale) (src/quicknncpu.pas:2763, reached via src/quicknn_kernels.pas:
  * 1655-1663; its callers pass heads first, src/quicknn_transformers.pas:1203,
- * 1275-1276) and the per-head cblas_gemm + QNNSoftmaxRows + cblas_gemm loops of
+ * 1301-1302) and the per-head cblas_gemm + QNNSoftmaxRows + cblas_gemm loops of
  * multiHeadForward / jointAttentionForward (src/quicknn_transformers.pas:
  * 1150-1311), Z-Image's attentionForward (:2228-2271) and, with kv_heads < heads
  * and INV_ATTN_CAUSAL, Qwen3's grouped causal attention (src/quicknn_qwen3.pas:

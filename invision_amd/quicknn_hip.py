@@ -362,7 +362,7 @@ def QNNFlashAttention(dst: np.ndarray, Q: np.ndarray, K: np.ndarray, V: np.ndarr
     """TQNNSingleOPS.QNNFlashAttention (src/quicknncpu.pas:2763) on fp32 host arrays:
     dst[seq_q x heads*head_dim] = softmax(scale * Q.K^T) V for every head.  The
     argument order is the one its callers use (src/quicknn_transformers.pas:1203,
-    1275-1276)."""
+    1301-1302)."""
     for a, nm in ((dst, "dst"), (Q, "Q"), (K, "K"), (V, "V")):
         _check_host(a, np.float32, nm)
     hidden = heads * head_dim

@@ -618,7 +618,7 @@ int orc_attention_qnn(const float *Q, const float *K, const float *V, float *O, 
 
 /* ---- normalisations before the projections ---------------------------------
  * EPSILON = 1e-6 (quicknn_common.pas:51).  QNNAdaLN's eps argument is not used
- * by its body (quicknncpu.pas:3052): the constant always applies. */
+ * by its body (quicknncpu.pas:3053): the constant always applies. */
 
 /* QNNAdaLN (quicknncpu.pas:3042-3060): per row, mean = QNNSum / N (:679-685),
  * population variance = sum((x - mean)^2) / N (:687-695), stdInv = 1/sqrt(var +
