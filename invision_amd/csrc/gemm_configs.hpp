@@ -28,9 +28,13 @@
 #define INV_CFG_10 inv::RsCfg<256, 256, 2, 2, 1, 2> /* one register stage, fragments two substeps ahead */
 #define INV_CFG_11 inv::RsCfg<256, 224, 4, 1, 2> /* 4 waves of 64x224 (W rows x X rows) */
 #define INV_CFG_12 inv::RsCfg<224, 256, 1, 4, 2> /* 4 waves of 224x64 */
+#define INV_CFG_13 inv::RsCfg<256, 128, 2, 2, 2> /* 4 waves of 128x64: half-height X tile */
+#define INV_CFG_14 inv::RsCfg<128, 256, 2, 2, 2> /* 4 waves of 64x128: half-height W tile */
+#define INV_CFG_15 inv::RsCfg<128, 128, 2, 2, 2> /* 4 waves of 64x64: small problems, two workgroups per CU */
 
-#define INV_GEMM_CONFIG_IDS(X) X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10) X(11) X(12)
-#define INV_GEMM_NUM_CONFIGS 13
+#define INV_GEMM_CONFIG_IDS(X) \
+    X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10) X(11) X(12) X(13) X(14) X(15)
+#define INV_GEMM_NUM_CONFIGS 16
 
 namespace inv {
 struct GemmParams;

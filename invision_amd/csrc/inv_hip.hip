@@ -266,58 +266,43 @@ int env_int(const char *name, int dflt) {
 // Workgroups of configuration m resident per CU (LDS is the binding limit).
 int cfg_occupancy(const CfgMeta &m) { return std::max(1, std::min(2, (160 * 1024) / m.lds)); }
 
-// Pick a tile shape and how the grid covers it.  Large problems take the
-// 256x256 tile; skinny ones stream W with a short X tile.  When the tile count
-// does not fill the chip in whole rounds (or is below one round and K is
-// long), a persistent stream-K grid gives every workgroup the same share of
-// k-iterations instead of leaving CUs idle in the last round.
+// Pick a tile shape and how the grid covers it (rules from measurements on
+// MI355X, 256 CUs):
+//  - at least 3/4 of a round of 256x256 tiles: the 256x256 register-staged tile
+//    (configuration 8), whose energy per FLOP is lowest; a partial last round
+//    costs little because the chip clocks up while CUs idle;
+//  - else half a round of 256x128 tiles (configuration 13: 256 W rows, 128 X
+//    rows), else half a round of 128x128 tiles (configuration 15, two
+//    workgroups per CU);
+//  - else (fewer than 128 tiles even at 128x128) configuration 15 with the K
+//    range split in two when K is deep (>= 32 k-tiles): measured 1.3-1.6x at
+//    512x9728x2560 and 256x3072x3072 (more splits lose to the partial-sum
+//    traffic, stream-K to its bookkeeping);
+//  - M <= 64: the W-streaming ring tiles with a short X tile.
 TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
-    TileChoice c{0, inv::GRID_TILES, 1};
+    TileChoice c{8, inv::GRID_TILES, 1};
     const int cus = g.cu_count > 0 ? g.cu_count : 256;
+    auto tiles_of = [&](int cfg) { return ((M + kCfg[cfg].tm - 1) / kCfg[cfg].tm) * ((N + kCfg[cfg].tn - 1) / kCfg[cfg].tn); };
     if (M <= 32) {
         c.cfg = 5;
     } else if (M <= 64) {
         c.cfg = 4;
+    } else if (tiles_of(8) * 4 >= (int64_t)cus * 3) {
+        c.cfg = 8;
+    } else if (tiles_of(13) * 2 >= cus) {
+        c.cfg = 13;
     } else {
-        // Among the larger tiles, the one with the least MFMA-feeding cost:
-        // the 256x256 register-staged tile loads and reads the fewest bytes
-        // per MFMA; smaller tiles only when the problem cannot fill the chip
-        // with it.
-        const int cand[3] = {8, 2, 3};
-        const double eff[3] = {1.0, 0.8, 0.65};
-        double best = -1.0;
-        for (int q = 0; q < 3; ++q) {
-            const CfgMeta &m = kCfg[cand[q]];
-            const int64_t tiles = ((M + m.tm - 1) / m.tm) * ((N + m.tn - 1) / m.tn);
-            const double slots = (double)cus * cfg_occupancy(m);
-            // stream-K evens out the last round, so only under-filled chips pay
-            const double fill = std::min(1.0, (double)tiles / slots);
-            const double score = fill * eff[q] * ((double)M * N) / ((double)tiles * m.tm * m.tn);
-            if (score > best) {
-                best = score;
-                c.cfg = cand[q];
-            }
+        c.cfg = 15;
+        const int64_t KT = (K + kCfg[15].bk - 1) / kCfg[15].bk;
+        if (tiles_of(15) * 2 < cus && KT >= 32) {
+            c.mode = inv::GRID_SPLITK;
+            c.count = 2;
         }
     }
     int ov = env_int("INV_HIP_TILE_CFG", -1);
     if (ov >= 0 && ov < kNumCfg) c.cfg = ov;
     const CfgMeta &m = kCfg[c.cfg];
-    const int64_t KT = (K + m.bk - 1) / m.bk;
-    const int64_t tiles = ((M + m.tm - 1) / m.tm) * ((N + m.tn - 1) / m.tn);
     const int64_t slots = (int64_t)cus * cfg_occupancy(m);
-    // Share of the slot-rounds left idle by one workgroup per tile.
-    const int64_t rounds = (tiles + slots - 1) / slots;
-    const double idle = 1.0 - (double)tiles / (double)(rounds * slots);
-    if (!m.reg_staged && m.tm >= 128 && ((tiles * 2 <= slots && KT >= 32) || (idle >= 0.25 && KT >= 128))) {
-        // A persistent stream-K grid spreads the k-iterations over all slots
-        // (at least 8 k-tiles per workgroup so the pipeline fill stays cheap).
-        // It pays when the last round would leave many slots idle and K is
-        // deep enough to amortise the partial-sum handoff; measured: better
-        // at 512x2560x9728-down and 9216x3840x15360-down, worse at
-        // 4608x9216x3072 (16% idle) and for the bandwidth-bound small-M tiles.
-        c.mode = inv::GRID_STREAMK;
-        c.count = (int)std::max<int64_t>(1, std::min<int64_t>(slots, tiles * KT / 8));
-    }
     const int mode = env_int("INV_HIP_MODE", -1);
     if (mode == inv::GRID_TILES) {
         c.mode = inv::GRID_TILES;

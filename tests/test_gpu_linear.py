@@ -165,8 +165,8 @@ GRID_MODES = {  # INV_HIP_MODE / INV_HIP_KSPLIT / INV_HIP_SK_GRID
 }
 
 
-ALL_CFGS = list(range(13))  # INV_GEMM_NUM_CONFIGS in invision_amd/csrc/gemm_configs.hpp
-REG_STAGED_CFGS = [8, 9, 10, 11, 12]  # 11 and 12: unequal W and X copy-chunk counts (8 + 7, 7 + 8)
+ALL_CFGS = list(range(16))  # INV_GEMM_NUM_CONFIGS in invision_amd/csrc/gemm_configs.hpp
+REG_STAGED_CFGS = [8, 9, 10, 11, 12, 13, 14, 15]  # 11-14: unequal W and X copy-chunk counts
 
 
 @pytest.mark.parametrize("cfg", ALL_CFGS)
