@@ -30,6 +30,8 @@
 // and the row sum is taken over those same bf16 weights (v_dot2_f32_bf16).
 #include "attention.hpp"
 
+#include <type_traits>
+
 namespace inv {
 namespace {
 
@@ -195,7 +197,10 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): tile 0 is in LDS
     __syncthreads();
 
-    for (int kt = 0; kt < nkt; ++kt) {
+    // One key tile; EDGE tiles (a partial last tile, or keys after some
+    // query's diagonal) mask scores, the others carry no masking code at all.
+    auto step = [&](int kt, auto edge_c) {
+        constexpr bool EDGE = decltype(edge_c)::value;
         const lds_t *cur = lds + (kt & 1) * STAGE;
         if (kt + 1 < nkt) load_tile(kt + 1, lds + ((kt + 1) & 1) * STAGE);
 
@@ -229,8 +234,7 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
         read_v(0, vf[0]);
 
         // Keys past seq_k, and (causal) after the query's diagonal, do not exist.
-        const bool edge = (kt + 1) * BK > p.seq_k || (CAUSAL && (kt + 1) * BK - 1 > q0 + p.causal_offset);
-        if (edge) {
+        if constexpr (EDGE) {
             const int vis = CAUSAL ? min(p.seq_k - 1, my_q + p.causal_offset) : p.seq_k - 1;
 #pragma unroll
             for (int b = 0; b < 2; ++b)
@@ -250,6 +254,9 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
         mx = fmaxf(mx, __shfl_xor(mx, 32)) * sl2;
         const bool grow = mx > m_run + kSlack;
         if (__builtin_amdgcn_ballot_w64(grow)) {  // some query's max moved: rescale (alpha = 1 elsewhere)
+            // (the empty volatile asm pins this block as a branch, skipped on most
+            // tiles, rather than 64 multiplies executed on every one)
+            asm volatile("" ::: "memory");
             const float m_new = grow ? mx : m_run;
             const float alpha = exp2_hw(m_run - m_new);  // 0 on the first tile, 1 where the max stays
             l_run *= alpha;
@@ -286,7 +293,13 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
         // reading this one, before it is refilled.
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
-    }
+    };
+    // Tiles before n_full need no mask for any query of this block.
+    int n_full = p.seq_k / BK;
+    if constexpr (CAUSAL) n_full = min(n_full, max(0, (q0 + p.causal_offset + 1) / BK));
+    n_full = min(n_full, nkt);
+    for (int kt = 0; kt < n_full; ++kt) step(kt, std::false_type{});
+    for (int kt = n_full; kt < nkt; ++kt) step(kt, std::true_type{});
 
     // Normalise and store this lane's query row: 4 consecutive head_dim values per register group.
     const float lt = l_run + __shfl_xor(l_run, 32);
