@@ -142,8 +142,9 @@ __global__ void __launch_bounds__(256) norm_rows_f32_bf16(const float *__restric
 
 // The same normalisation with the row held in registers (one read of X):
 // thread t owns the 4-column groups t, t + 256, ... (J of them); cols % 4 == 0,
-// cols <= 4 * 256 * J, src rows 16-byte aligned.  J is the smallest of 1, 2, 4,
-// 8, 16 that holds the row, so short rows keep few registers and many rows in flight.
+// cols <= 4 * 256 * J, src rows and the per-column vectors 16-byte aligned.  J
+// is the smallest of 1, 2, 3, 4, 6, 8, 12, 16 that holds the row, so short rows
+// keep few registers and many rows in flight.
 constexpr int NORM_ROW_GROUPS = 16;  // rows up to 16384 columns
 
 template <int NORM, int J>
@@ -156,11 +157,17 @@ __global__ void __launch_bounds__(256) norm_rows_f32_bf16_reg(const float *__res
     const int64_t r = blockIdx.x;
     const float *x = src + r * lds;
     const int ng = (int)(cols >> 2);
-    // All loads first (a clamped, always valid address; groups past the row are
-    // zeroed after) so they are in flight together.
-    float4 v[J];
+    // Every load of this thread is issued before the first reduction: its groups
+    // of the row and the same groups of the per-column vectors, at a clamped
+    // (always valid) group; groups past the row are zeroed after.
+    float4 v[J], av[J], bv[J];
 #pragma unroll
-    for (int j = 0; j < J; ++j) v[j] = *(const float4 *)(x + 4 * min((int)threadIdx.x + 256 * j, ng - 1));
+    for (int j = 0; j < J; ++j) {
+        const int gi = min((int)threadIdx.x + 256 * j, ng - 1);
+        v[j] = *(const float4 *)(x + 4 * gi);
+        av[j] = a ? *(const float4 *)(a + 4 * gi) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        if constexpr (NORM == NORM_ADALN) bv[j] = *(const float4 *)(b + 4 * gi);
+    }
 #pragma unroll
     for (int j = 0; j < J; ++j)
         if ((int)threadIdx.x + 256 * j >= ng) v[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -185,29 +192,24 @@ __global__ void __launch_bounds__(256) norm_rows_f32_bf16_reg(const float *__res
         rstd = 1.0f / sqrtf(block_sum256(s, red) / (float)cols + eps);
     }
     uint16_t *d = dst + r * ldd;
-    // the per-column vectors, likewise loaded together (clamped columns)
-    float av[J][4], bv[J][4];
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int c = 4 * min((int)threadIdx.x + 256 * j, ng - 1) + e;
-            av[j][e] = a ? a[c] : 1.0f;
-            bv[j][e] = (NORM == NORM_ADALN) ? b[c] : 0.0f;
-        }
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int g = threadIdx.x + 256 * j;
         if (g < ng) {
             const float xv[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+            const float sv[4] = {av[j].x, av[j].y, av[j].z, av[j].w};
+            float hv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (NORM == NORM_ADALN) {
+                hv[0] = bv[j].x; hv[1] = bv[j].y; hv[2] = bv[j].z; hv[3] = bv[j].w;
+            }
             uint16_t h[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 float y;
                 if constexpr (NORM == NORM_ADALN)
-                    y = (1.0f + av[j][e]) * ((xv[e] - mean) * rstd) + bv[j][e];
+                    y = (1.0f + sv[e]) * ((xv[e] - mean) * rstd) + hv[e];
                 else
-                    y = xv[e] * rstd * av[j][e];
+                    y = xv[e] * rstd * sv[e];
                 h[e] = bf16_rne(y);
             }
             *(uint2 *)(d + 4 * g) = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16),

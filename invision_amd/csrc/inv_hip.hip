@@ -687,6 +687,14 @@ int stage_normalized(const char *who, const float *X, const NormArgs &nm, bool d
         bd = nm.shift ? (const float *)((char *)g.nvec.p + vb) : nullptr;
     } else if (!aligned(X, 4)) {
         return fail(INV_ERR_ARG, "%s: X not 4-byte aligned", who);
+    } else if ((ad && !aligned(ad, 16)) || (bd && !aligned(bd, 16))) {
+        // the register kernel reads the per-column vectors 16 bytes at a time
+        const size_t vb = (size_t)K * 4;
+        TRY(ensure(g.nvec, 2 * vb));
+        if (ad) HIPCHK(hipMemcpyAsync(g.nvec.p, ad, vb, hipMemcpyDeviceToDevice, g.stream));
+        if (bd) HIPCHK(hipMemcpyAsync((char *)g.nvec.p + vb, bd, vb, hipMemcpyDeviceToDevice, g.stream));
+        ad = ad ? (const float *)g.nvec.p : nullptr;
+        bd = bd ? (const float *)((char *)g.nvec.p + vb) : nullptr;
     }
     TRY(ensure(g.x16, (size_t)(M * ldw) * 2));
     uint16_t *d = (uint16_t *)g.x16.p;
@@ -699,11 +707,16 @@ int stage_normalized(const char *who, const float *X, const NormArgs &nm, bool d
         };
         const bool ada = nm.kind == INV_NORM_ADALN;
         using namespace inv;
-        if (groups <= 1) ada ? launch(norm_rows_f32_bf16_reg<NORM_ADALN, 1>) : launch(norm_rows_f32_bf16_reg<NORM_RMS, 1>);
-        else if (groups <= 2) ada ? launch(norm_rows_f32_bf16_reg<NORM_ADALN, 2>) : launch(norm_rows_f32_bf16_reg<NORM_RMS, 2>);
-        else if (groups <= 4) ada ? launch(norm_rows_f32_bf16_reg<NORM_ADALN, 4>) : launch(norm_rows_f32_bf16_reg<NORM_RMS, 4>);
-        else if (groups <= 8) ada ? launch(norm_rows_f32_bf16_reg<NORM_ADALN, 8>) : launch(norm_rows_f32_bf16_reg<NORM_RMS, 8>);
-        else ada ? launch(norm_rows_f32_bf16_reg<NORM_ADALN, 16>) : launch(norm_rows_f32_bf16_reg<NORM_RMS, 16>);
+#define INV_NORM_J(J) (ada ? launch(norm_rows_f32_bf16_reg<NORM_ADALN, J>) : launch(norm_rows_f32_bf16_reg<NORM_RMS, J>))
+        if (groups <= 1) INV_NORM_J(1);
+        else if (groups <= 2) INV_NORM_J(2);
+        else if (groups <= 3) INV_NORM_J(3);
+        else if (groups <= 4) INV_NORM_J(4);
+        else if (groups <= 6) INV_NORM_J(6);
+        else if (groups <= 8) INV_NORM_J(8);
+        else if (groups <= 12) INV_NORM_J(12);
+        else INV_NORM_J(16);
+#undef INV_NORM_J
     } else if (nm.kind == INV_NORM_ADALN)
         hipLaunchKernelGGL(inv::norm_rows_f32_bf16<inv::NORM_ADALN>, dim3((unsigned)M), dim3(256), 0, g.stream, xd, K,
                            ad, bd, nm.eps, d, ldw, K, ldw);

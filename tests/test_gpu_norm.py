@@ -42,7 +42,8 @@ def gen(seed, M, K, N):
 @pytest.mark.parametrize("M,K,N", [(300, 1024, 520), (64, 3072, 256), (1, 1536, 130), (257, 200, 96),
                                    (40, 1036, 96),   # K % 8 == 4: one zero-padded group of 4 columns
                                    (33, 77, 64),     # K % 4 != 0: the multi-pass kernel
-                                   (8, 8192, 64), (4, 12288, 32)])  # 8 and 12 register groups per thread
+                                   (16, 5120, 64), (8, 8192, 64), (4, 12288, 32), (4, 16384, 64)])
+                                   # 6, 8, 12 and 16 register groups per thread
 def test_adaln_linear_matches_oracle(hiplib, M, K, N):
     X, W, b, shift, scale = gen(81, M, K, N)
     with q.Weight(W, b) as w:
@@ -93,7 +94,15 @@ def test_device_pointers_match_host_path(hiplib):
         hip.call("inv_hip_linear_norm", xd.ptr, hip.INV_NORM_ADALN, sd.ptr, hd.ptr, q.EPSILON, w.handle, None, yd.ptr,
                  hip.INV_DT_F32, M, K, N, hip.INV_EPI_NONE, hip.INV_FLAG_DEVICE_PTRS)
         np.testing.assert_array_equal(yd.to_host(), y_host)
-        for a in (xd, sd, hd, yd):
+        # modulation vectors at a 4-byte (not 16-byte) offset into device memory
+        sh = np.concatenate([np.zeros(1, np.float32), scale]), np.concatenate([np.zeros(1, np.float32), shift])
+        sd1, hd1 = (q.DeviceArray.from_host(a, "f32") for a in sh)
+        yd.free()
+        yd = q.DeviceArray((M, N), "f32")
+        hip.call("inv_hip_linear_norm", xd.ptr, hip.INV_NORM_ADALN, sd1.ptr + 4, hd1.ptr + 4, q.EPSILON, w.handle,
+                 None, yd.ptr, hip.INV_DT_F32, M, K, N, hip.INV_EPI_NONE, hip.INV_FLAG_DEVICE_PTRS)
+        np.testing.assert_array_equal(yd.to_host(), y_host)
+        for a in (xd, sd, hd, yd, sd1, hd1):
             a.free()
 
 
