@@ -691,10 +691,23 @@ __device__ __forceinline__ void mainloop_rs(const GemmParams &p, lds_char_t *lds
 // among the stores: loads and stores share vmcnt, and a wait for a load that
 // may have been issued also waits for every store before it.
 // Requires the ring to be idle (a barrier first) and NWAVES*32*(WTN+4)*4 bytes.
-template <class C, int EPI, int OUT, bool BETA>
+//
+// Shared tiles (split-K / stream-K) go through the same row loop:
+//  SK_PUBLISH: the staged rows (alpha * acc) are written to the unit's
+//              workspace slot instead of Y, no epilogue;
+//  SK_FINISH:  the rows are the sum, in unit (K) order, of every unit's slot
+//              (this unit's own included), then the epilogue as usual.
+// A slot holds each wave's 32-row blocks row-major: float index
+// ((wave * FM + j) * 32 + row) * WTN + col, so both sides move whole rows and
+// the accumulators are never touched by VALU adds (which would need them in
+// VGPRs next to the main loop's registers).
+enum { SK_NONE = 0, SK_PUBLISH = 1, SK_FINISH = 2 };
+
+template <class C, int EPI, int OUT, bool BETA, int SKM = SK_NONE, int MODE = 0>
 __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_t *lds,
                                                   const f32x16_t (&acc)[C::FN][C::FM], int m0, int n0, int wn,
-                                                  int wm, int lane, int wave) {
+                                                  int wm, int lane, int wave, const UnitFix *fix = nullptr,
+                                                  float *slot = nullptr) {
     typedef __attribute__((address_space(3))) float lds_float_t;
     constexpr int SROW = C::WTN + 4;       // staged row pitch in floats
     constexpr int LPR = C::WTN / 4;        // lanes per row on the read side
@@ -708,7 +721,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
     const int n = n0 + wn * C::WTN + col;
     const bool nvec = p.vec_store && n + 3 < p.N;
     float bv[4] = {0.f, 0.f, 0.f, 0.f}, sc[4] = {1.f, 1.f, 1.f, 1.f};
-    if (p.has_bias) {
+    if (SKM != SK_PUBLISH && p.has_bias) {
         if (n + 3 < p.N) {
             const f32x4_t t = *(const f32x4_t *)(p.bias + n);  // bias is 16-byte aligned, n % 4 == 0
 #pragma unroll
@@ -718,7 +731,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
             for (int e = 0; e < 4; ++e) bv[e] = (n + e < p.N) ? p.bias[n + e] : 0.f;
         }
     }
-    if (p.colscale) {
+    if (SKM != SK_PUBLISH && p.colscale) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) sc[e] = (n + e < p.N) ? p.colscale[n + e] : 0.f;
     }
@@ -728,22 +741,40 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
     __syncthreads();  // every wave has finished with the ring
 #pragma unroll
     for (int j = 0; j < C::FM; ++j) {
-#pragma unroll
-        for (int i = 0; i < C::FN; ++i)
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-                *(__attribute__((address_space(3))) f32x4_t *)(st + frow * SROW + i * 32 + 8 * g + 4 * fh) =
-                    f32x4_t{p.alpha * acc[i][j][4 * g], p.alpha * acc[i][j][4 * g + 1],
-                            p.alpha * acc[i][j][4 * g + 2], p.alpha * acc[i][j][4 * g + 3]};
-        // LDS operations of one wave execute in order: the reads below see the
-        // writes above, and the next block's writes follow these reads.  All
-        // reads (and C loads) of the block are issued before any store, so the
-        // stores are never behind a wait.
         constexpr int NIT = 32 / RPI;
         f32x4_t t[NIT];
+        const int64_t slot_off = ((int64_t)(wave * C::FM + j) * 32 + rsub) * C::WTN + col;
+        if constexpr (SKM == SK_FINISH) {
+            for (int sp = 0; sp < fix->nseg; ++sp) {
+                const float *src = unit_slot<MODE, C>(p, *fix, sp) + slot_off;
+                f32x4_t u[NIT];
 #pragma unroll
-        for (int it = 0; it < NIT; ++it)
-            t[it] = *(const __attribute__((address_space(3))) f32x4_t *)(st + (it * RPI + rsub) * SROW + col);
+                for (int it = 0; it < NIT; ++it)
+                    u[it] = __builtin_nontemporal_load((const f32x4_t *)(src + it * RPI * C::WTN));
+#pragma unroll
+                for (int it = 0; it < NIT; ++it) t[it] = (sp == 0) ? u[it] : t[it] + u[it];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    *(__attribute__((address_space(3))) f32x4_t *)(st + frow * SROW + i * 32 + 8 * g + 4 * fh) =
+                        f32x4_t{p.alpha * acc[i][j][4 * g], p.alpha * acc[i][j][4 * g + 1],
+                                p.alpha * acc[i][j][4 * g + 2], p.alpha * acc[i][j][4 * g + 3]};
+            // LDS operations of one wave execute in order: the reads below see the
+            // writes above, and the next block's writes follow these reads.  All
+            // reads (and C loads) of the block are issued before any store, so the
+            // stores are never behind a wait.
+#pragma unroll
+            for (int it = 0; it < NIT; ++it)
+                t[it] = *(const __attribute__((address_space(3))) f32x4_t *)(st + (it * RPI + rsub) * SROW + col);
+        }
+        if constexpr (SKM == SK_PUBLISH) {
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) *(f32x4_t *)(slot + slot_off + it * RPI * C::WTN) = t[it];
+            continue;
+        }
         const int mrow = m0 + wm * C::WTM + j * 32 + rsub;  // row of it = 0; it adds RPI rows
         if (nvec && mrow + (NIT - 1) * RPI < p.M) {
             // every row of this lane in range, 16-byte aligned: no branches
@@ -997,7 +1028,36 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
         mainloop_ring<C>(p, lds, rsw, rsx, kt_begin, kt_end, acc);
 
 
-    if constexpr (MODE != GRID_TILES) {
+    if constexpr (MODE != GRID_TILES && C::STAGED_EPI && EPI != EPI_SWIGLU) {
+        if (fix.nseg > 1) {
+            // Park this unit's partial rows; the last arriving unit of the tile
+            // sums every unit's rows in K order and finishes the tile.
+            store_tile_staged<C, EPI, OUT, false, SK_PUBLISH, MODE>(p, lds, acc, m0, n0, wn, wm, lane, wave, &fix,
+                                                                    unit_slot<MODE, C>(p, fix, fix.my_seg));
+            // Uncached workspace and counters: the stores are in memory once
+            // acknowledged, coherent across XCDs without fences.
+            wait_vmcnt<0>();
+            volatile __attribute__((address_space(3))) unsigned *s_last =
+                (volatile __attribute__((address_space(3))) unsigned *)lds;
+            __syncthreads();  // every wave's staging reads and slot stores are done
+            if (tid == 0) {
+                unsigned prev =
+                    __hip_atomic_fetch_add(&p.counters[fix.tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                *s_last = (prev == (unsigned)(fix.nseg - 1)) ? 1u : 0u;
+            }
+            __syncthreads();
+            const bool last = *s_last != 0;
+            __syncthreads();  // everyone has read the flag before the ring is reused
+            if (!last) return;
+            if (p.beta != 0.0f)
+                store_tile_staged<C, EPI, OUT, true, SK_FINISH, MODE>(p, lds, acc, m0, n0, wn, wm, lane, wave, &fix);
+            else
+                store_tile_staged<C, EPI, OUT, false, SK_FINISH, MODE>(p, lds, acc, m0, n0, wn, wm, lane, wave, &fix);
+            if (tid == 0)  // ready for the next call
+                __hip_atomic_store(&p.counters[fix.tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+    } else if constexpr (MODE != GRID_TILES) {
         if (fix.nseg > 1) {
             // Park this unit's partial sums, then let the last arriving unit of
             // the tile finish it.

@@ -246,7 +246,7 @@ struct TileChoice {
 // Instantiated tile configurations (gemm_configs.hpp).
 struct CfgMeta {
     int tn, tm, threads, acc_regs, bk, lds;
-    bool reg_staged;  // RsCfg: no stream-K / split-K (its fixup path spills registers)
+    bool reg_staged;  // RsCfg: register-staged main loop
     bool swiglu_ok;   // 256-row tiles over two wave columns with a staged epilogue
     hipError_t (*launch)(const inv::GemmParams &, int, int, int, hipStream_t);
 };

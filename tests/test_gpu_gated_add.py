@@ -144,3 +144,22 @@ def test_gated_add_argument_errors(hiplib):
                                           64, 127, 0)
         assert rc == hip.INV_ERR_ARG and "shape mismatch" in hip.last_error()
         np.testing.assert_array_equal(Y, Y0)  # untouched on error
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cfg", [8, 13, 15])
+@pytest.mark.parametrize("grid", [{"INV_HIP_MODE": "1", "INV_HIP_KSPLIT": "3"},
+                                  {"INV_HIP_MODE": "2", "INV_HIP_SK_GRID": "37"}], ids=["splitk3", "streamk37"])
+def test_gated_add_with_shared_tiles(hiplib, monkeypatch, cfg, grid):
+    """Tiles whose K range is shared by several workgroups: the last one sums
+    the parked partial rows, then applies bias, gate and the residual add."""
+    monkeypatch.setenv("INV_HIP_TILE_CFG", str(cfg))
+    for k, v in grid.items():
+        monkeypatch.setenv(k, v)
+    M, K, N = 300, 1000, 520
+    X, W, b, g, Y0 = gen(33, M, K, N)
+    with q.Weight(W) as w:
+        Y = q.linear_gated_add(Y0.copy(), as_bf16_bits(X), w, g, b)
+        Y2 = q.linear_gated_add(Y0.copy(), as_bf16_bits(X), w, g, b)
+    assert update_err(Y, Y0, oracle_gated(Y0, round_bf16(X), W, b, g)) <= TOL_TIGHT
+    np.testing.assert_array_equal(Y, Y2)

@@ -184,6 +184,20 @@ def test_every_tile_shape_and_grid_mode(hiplib, monkeypatch, cfg, grid):
     np.testing.assert_array_equal(y, y2)  # deterministic, counters reset
 
 
+@pytest.mark.parametrize("cfg", [8, 13, 15])
+@pytest.mark.parametrize("grid", ["splitk3", "streamk37"])
+def test_shared_tiles_bf16_out_and_gelu(hiplib, monkeypatch, cfg, grid):
+    """Split- and stream-K tiles with the bf16 output and GELU epilogue."""
+    monkeypatch.setenv("INV_HIP_TILE_CFG", str(cfg))
+    for k, v in GRID_MODES[grid].items():
+        monkeypatch.setenv(k, v)
+    M, K, N = 300, 1000, 520
+    X, W, b = gen(17, M, K, N)
+    with q.Weight(W, b) as w:
+        y = q.linear(X, w, epilogue="gelu", out_dtype="bf16")
+    check(bf16_bits_to_f32(y), X, W, b, "gelu", tight=TOL_TIGHT + 2.0 ** -8, ref_tol=TOL_REF + 2.0 ** -8)
+
+
 @pytest.mark.parametrize("cfg", REG_STAGED_CFGS)
 @pytest.mark.parametrize("K", [8, 64, 128, 200, 576, 1000, 3072])
 def test_register_staged_k_tile_counts(hiplib, monkeypatch, cfg, K):
