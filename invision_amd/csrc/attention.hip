@@ -96,7 +96,8 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
     lds_t *lds = (lds_t *)smem;
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS copy bases stay scalar
     const int lq = lane & 31, lh = lane >> 5;
     // 1-D grid of heads x query blocks; causal blocks run longest first.
     const int nqb = (p.seq_q + BQ - 1) / BQ;
@@ -199,10 +200,15 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
 
     // One key tile; EDGE tiles (a partial last tile, or keys after some
     // query's diagonal) mask scores, the others carry no masking code at all.
-    auto step = [&](int kt, auto edge_c) {
+    // PAR is the buffer holding tile kt when it is known at compile time (the
+    // unmasked loop runs two tiles per trip), so LDS addresses are a register
+    // plus an immediate offset; -1: it follows kt at run time (edge tiles).
+    auto step = [&](int kt, auto edge_c, auto par_c) {
         constexpr bool EDGE = decltype(edge_c)::value;
-        const lds_t *cur = lds + (kt & 1) * STAGE;
-        if (kt + 1 < nkt) load_tile(kt + 1, lds + ((kt + 1) & 1) * STAGE);
+        constexpr int PAR = decltype(par_c)::value;
+        const int par = PAR < 0 ? (kt & 1) : PAR;
+        const lds_t *cur = lds + par * STAGE;
+        if (kt + 1 < nkt) load_tile(kt + 1, lds + (1 - par) * STAGE);
 
         // S^T for 64 keys: two 32-key blocks whose MFMAs alternate (no back-to-back
         // accumulator chain); K fragments are read two head_dim steps ahead.
@@ -218,12 +224,17 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
         bf16x8_t kf[3][2];
         read_k(0, kf[0]);
         read_k(1, kf[1]);
+        // Raised issue priority while this wave feeds the matrix core: the
+        // other workgroup's wave on the SIMD then runs its softmax in the gaps
+        // instead of competing with the MFMA issue.
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             if (c + 2 < NC) read_k(c + 2, kf[(c + 2) % 3]);
 #pragma unroll
             for (int b = 0; b < 2; ++b) s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[c % 3][b], qf[c], s[b], 0, 0, 0);
         }
+        __builtin_amdgcn_s_setprio(0);
 
         // The first V^T fragments: their LDS latency hides under the softmax.
         auto read_v = [&](int kc4, bf16x8_t (&f)[ND]) {
@@ -271,6 +282,7 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
             for (int r = 0; r < 16; ++r) s[b][r] = exp2_hw(fmaf(s[b][r], sl2, -m_use));
 
         // O^T += V^T P^T over the 4 chunks of 16 keys, V^T fragments one chunk ahead.
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int kc4 = 0; kc4 < 4; ++kc4) {
             if (kc4 + 1 < 4) read_v(kc4 + 1, vf[(kc4 + 1) & 1]);
@@ -289,6 +301,7 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
             l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 6, 7), one2, l_run, false);
         }
 
+        __builtin_amdgcn_s_setprio(0);
         // The next tile has landed in the other buffer, and every wave is done
         // reading this one, before it is refilled.
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -298,8 +311,15 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
     int n_full = p.seq_k / BK;
     if constexpr (CAUSAL) n_full = min(n_full, max(0, (q0 + p.causal_offset + 1) / BK));
     n_full = min(n_full, nkt);
-    for (int kt = 0; kt < n_full; ++kt) step(kt, std::false_type{});
-    for (int kt = n_full; kt < nkt; ++kt) step(kt, std::true_type{});
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    int kt = 0;
+    for (; kt + 1 < n_full; kt += 2) {
+        step(kt, std::false_type{}, P0{});
+        step(kt + 1, std::false_type{}, P1{});
+    }
+    if (kt < n_full) step(kt++, std::false_type{}, P0{});
+    for (; kt < nkt; ++kt) step(kt, std::true_type{}, std::integral_constant<int, -1>{});
 
     // Normalise and store this lane's query row: 4 consecutive head_dim values per register group.
     const float lt = l_run + __shfl_xor(l_run, 32);
