@@ -274,10 +274,13 @@ int cfg_occupancy(const CfgMeta &m) { return std::max(1, std::min(2, (160 * 1024
 //  - else half a round of 256x128 tiles (configuration 13: 256 W rows, 128 X
 //    rows), else half a round of 128x128 tiles (configuration 15, two
 //    workgroups per CU);
-//  - else (fewer than 128 tiles even at 128x128) configuration 15 with the K
-//    range split in two when K is deep (>= 32 k-tiles): measured 1.3-1.6x at
-//    512x9728x2560 and 256x3072x3072 (more splits lose to the partial-sum
-//    traffic, stream-K to its bookkeeping);
+//  - else (fewer than 128 tiles even at 128x128): 128x128 tiles, or for
+//    M <= 256 the 128x64 ring tile (configuration 4), with the K range split
+//    so that the units fill at most one workgroup per CU (2 to 4 splits of at
+//    least 8 k-tiles, when K has at least 32).  Sustained: 512x9728x2560 three
+//    ways 623 -> 669 TFLOP/s against two; 256x3072x3072 at 128x64 split two
+//    ways 234 against 204 (128x128, two ways) and 220 (four ways).  More
+//    splits lose to the partial-sum traffic, stream-K to its bookkeeping;
 //  - M <= 64: the W-streaming ring tiles with a short X tile.
 TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
     TileChoice c{8, inv::GRID_TILES, 1};
@@ -292,11 +295,12 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
     } else if (tiles_of(13) * 2 >= cus) {
         c.cfg = 13;
     } else {
-        c.cfg = 15;
-        const int64_t KT = (K + kCfg[15].bk - 1) / kCfg[15].bk;
-        if (tiles_of(15) * 2 < cus && KT >= 32) {
+        c.cfg = (M <= 256) ? 4 : 15;
+        const int64_t KT = (K + kCfg[c.cfg].bk - 1) / kCfg[c.cfg].bk;
+        const int64_t ks = std::min<int64_t>({4, cus / tiles_of(c.cfg), KT / 8});
+        if (KT >= 32 && ks >= 2) {
             c.mode = inv::GRID_SPLITK;
-            c.count = 2;
+            c.count = (int)ks;
         }
     }
     int ov = env_int("INV_HIP_TILE_CFG", -1);
@@ -830,6 +834,53 @@ int linear_impl(const char *who, const void *X, int x_dtype, inv_weight_t W, con
     return INV_OK;
 }
 
+// The library stream, its timing events and the two pinned bounce buffers.
+int init_stream_objects() {
+    HIPCHK(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
+    for (hipEvent_t *e : {&g.tim0, &g.tim1, &g.st0, &g.st1}) HIPCHK(hipEventCreate(e));
+    for (int k = 0; k < 2; ++k) {
+        HIPCHK(hipEventCreateWithFlags(&g.pin_ev[k], hipEventDisableTiming));
+        HIPCHK(hipEventRecord(g.pin_ev[k], g.stream));
+        if (hipHostMalloc(&g.pin[k], kPinChunk, hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            g.pin[k] = nullptr;
+            return fail(INV_ERR_OOM, "pinned bounce buffer allocation failed");
+        }
+    }
+    return INV_OK;
+}
+
+void release_stream_objects() {
+    if (g.stream) (void)hipStreamSynchronize(g.stream);
+    for (int k = 0; k < 2; ++k) {
+        if (g.pin[k]) (void)hipHostFree(g.pin[k]);
+        if (g.pin_ev[k]) (void)hipEventDestroy(g.pin_ev[k]);
+        g.pin[k] = nullptr;
+        g.pin_ev[k] = nullptr;
+    }
+    for (hipEvent_t *e : {&g.tim0, &g.tim1, &g.st0, &g.st1}) {
+        if (*e) (void)hipEventDestroy(*e);
+        *e = nullptr;
+    }
+    if (g.stream) (void)hipStreamDestroy(g.stream);
+    g.stream = nullptr;
+}
+
+// Query-key pairs an attention call evaluates: all of them, or (causal) key j
+// <= i + offset for query i, offset = seq_k - seq_q.
+double attention_pairs(int64_t sq, int64_t sk, bool causal) {
+    if (!causal) return (double)sq * (double)sk;
+    double n = 0.0;
+    const int64_t off = sk - sq;
+    // query i sees clamp(i + off + 1, 0, sk) keys: zero below i0, sk from i1 on
+    const int64_t i0 = std::min<int64_t>(sq, std::max<int64_t>(0, -off));
+    const int64_t i1 = std::min<int64_t>(sq, std::max<int64_t>(i0, sk - off - 1));
+    // i in [i0, i1): i + off + 1 keys, an arithmetic series
+    n += (double)(i1 - i0) * (double)(i0 + i1 - 1) / 2.0 + (double)(i1 - i0) * (double)(off + 1);
+    n += (double)(sq - i1) * (double)sk;
+    return n;
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -859,18 +910,10 @@ int inv_hip_init(int device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(INV_ERR_NO_DEVICE, "device %d is %s, this library is built for gfx950", device, prop.gcnArchName);
     HIPCHK(hipSetDevice(device));
-    HIPCHK(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
-    HIPCHK(hipEventCreate(&g.tim0));
-    HIPCHK(hipEventCreate(&g.tim1));
-    HIPCHK(hipEventCreate(&g.st0));
-    HIPCHK(hipEventCreate(&g.st1));
-    for (int k = 0; k < 2; ++k) {
-        HIPCHK(hipEventCreateWithFlags(&g.pin_ev[k], hipEventDisableTiming));
-        HIPCHK(hipEventRecord(g.pin_ev[k], g.stream));
-        if (hipHostMalloc(&g.pin[k], kPinChunk, hipHostMallocDefault) != hipSuccess) {
-            (void)hipGetLastError();
-            return fail(INV_ERR_OOM, "pinned bounce buffer allocation failed");
-        }
+    const int rc = init_stream_objects();
+    if (rc) {
+        release_stream_objects();  // a later call may try again from scratch
+        return rc;
     }
     g.device = device;
     g.cu_count = prop.multiProcessorCount;
@@ -890,18 +933,7 @@ int inv_hip_shutdown(void) {
     for (Buf *b : {&g.xin, &g.x16, &g.w16, &g.win, &g.yout, &g.cin, &g.bias, &g.gate, &g.aq, &g.ak, &g.avt, &g.aqin,
                    &g.akin, &g.avin, &g.nvec}) release(*b);
     // g.partial / g.counters (uncached) stay allocated until the process ends.
-    for (int k = 0; k < 2; ++k) {
-        if (g.pin[k]) (void)hipHostFree(g.pin[k]);
-        if (g.pin_ev[k]) (void)hipEventDestroy(g.pin_ev[k]);
-        g.pin[k] = nullptr;
-        g.pin_ev[k] = nullptr;
-    }
-    for (hipEvent_t *e : {&g.tim0, &g.tim1, &g.st0, &g.st1}) {
-        if (*e) (void)hipEventDestroy(*e);
-        *e = nullptr;
-    }
-    (void)hipStreamDestroy(g.stream);
-    g.stream = nullptr;
+    release_stream_objects();
     g.init = false;
     g.device = -1;
     g.stats = false;
@@ -1105,7 +1137,7 @@ int inv_hip_attention(const void *Q, const void *K, const void *V, void *O, int 
         float ms = 0.f;
         HIPCHK(hipEventElapsedTime(&ms, g.st0, g.st1));
         g.gemm_ms += ms;
-        g.flops += 4.0 * (double)seq_q * (double)seq_k * (double)head_dim * (double)heads;
+        g.flops += 4.0 * attention_pairs(seq_q, seq_k, causal) * (double)head_dim * (double)heads;
     }
     g.calls++;
     if (!dev) {

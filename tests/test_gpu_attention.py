@@ -165,3 +165,20 @@ def test_attention_argument_errors(hiplib):
     assert call(args(flags=0x8)) == hip.INV_ERR_ARG and "unknown flags" in hip.last_error()
     assert call(args(sq=0)) == hip.INV_OK
     assert not np.any(O)  # nothing written on error or for zero queries
+
+
+@pytest.mark.gpu
+def test_stats_count_the_evaluated_pairs(hiplib):
+    """The library's FLOP counter counts 4 * D FLOPs per evaluated query-key pair
+    per head: every pair, or (causal) key j <= i + seq_k - seq_q for query i."""
+    heads, d = 2, 64
+    for sq, sk, causal in ((5, 70, True), (100, 40, True), (33, 77, False)):
+        Q, K, V = gen(69, sq, sk, heads, heads, d)
+        hip.call("inv_hip_stats_reset")
+        hip.call("inv_hip_stats_enable", 1)
+        try:
+            q.attention(Q, K, V, heads=heads, head_dim=d, causal=causal)
+        finally:
+            hip.call("inv_hip_stats_enable", 0)
+        pairs = sum(min(sk, max(0, i + sk - sq + 1)) for i in range(sq)) if causal else sq * sk
+        assert q.stats()["flops"] == 4.0 * pairs * d * heads
