@@ -27,7 +27,8 @@
  *    inv_hip_linear_gated_add;
  *  - QNNFlashAttention and the per-head attention loops
  *    (src/quicknncpu.pas:2763; src/quicknn_transformers.pas:1150-1311) by
- *    inv_hip_attention.
+ *    inv_hip_attention, and Qwen3's masked causal attention
+ *    (src/quicknn_qwen3.pas:727-769) by inv_hip_attention_masked.
  */
 #ifndef INV_HIP_H
 #define INV_HIP_H
@@ -218,6 +219,20 @@ int inv_hip_linear_norm(const float *X, int norm, const float *norm_scale, const
 int inv_hip_attention(const void *Q, const void *K, const void *V, void *O, int in_dtype,
                       int out_dtype, int64_t heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k,
                       int64_t head_dim, float scale, int flags);
+
+/* inv_hip_attention with the key mask of Qwen3's attention: key j is hidden
+ * from every query where key_mask[j] == 0 (seq_k int32 entries, host or device
+ * per INV_FLAG_DEVICE_PTRS; null: no mask).  Replaces the mask argument of
+ * QNNMatTriangularFill(seq_len, scores, -inf, attention_mask) before
+ * QNNSoftmaxRows (src/quicknn_qwen3.pas:753-754; src/quicknncpu.pas:
+ * 3017-3028), which with INV_ATTN_CAUSAL and seq_q == seq_k is the same mask;
+ * the encoder's padding to 512 tokens sets it (src/quicknn_qwen3.pas:
+ * 1136-1140, 293-303).  A query that sees no key gets zeros (the reference's
+ * softmax gives NaN there). */
+int inv_hip_attention_masked(const void *Q, const void *K, const void *V, void *O, int in_dtype,
+                             int out_dtype, int64_t heads, int64_t kv_heads, int64_t seq_q,
+                             int64_t seq_k, int64_t head_dim, float scale, const int32_t *key_mask,
+                             int flags);
 
 /* ---- the CBLAS slots ------------------------------------------------------ */
 /* Exactly the signature of TQNNSingleOPS.cblas_sgemm (src/quicknncpu.pas:

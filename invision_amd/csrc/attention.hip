@@ -245,14 +245,24 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
         read_v(0, vf[0]);
 
         // Keys past seq_k, and (causal) after the query's diagonal, do not exist.
+        // With a key mask every tile is an edge tile: bit k of `keep` says key
+        // kt*BK + k is kept.  Lane half lh holds the tile's keys 16*g + 8*lh +
+        // (0..7) (g = 2b + r/8, the K rows being quadswapped), so after a shift
+        // by 8*lh each score's bit sits at a compile-time position.
         if constexpr (EDGE) {
             const int vis = CAUSAL ? min(p.seq_k - 1, my_q + p.causal_offset) : p.seq_k - 1;
+            uint64_t keep = ~0ull;
+            if (p.key_mask) {
+                const int kk = kt * BK + lane;
+                keep = __builtin_amdgcn_ballot_w64(kk < p.seq_k && p.key_mask[kk] != 0) >> (8 * lh);
+            }
 #pragma unroll
             for (int b = 0; b < 2; ++b)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int key = kt * BK + quadswap(32 * b + 8 * (r >> 2) + 4 * lh + (r & 3));
-                    if (key > vis) s[b][r] = -__builtin_inff();
+                    const bool kept = (keep >> (16 * (2 * b + (r >> 3)) + (r & 7))) & 1u;
+                    if (key > vis || !kept) s[b][r] = -__builtin_inff();
                 }
         }
 
@@ -310,7 +320,7 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
     // Tiles before n_full need no mask for any query of this block.
     int n_full = p.seq_k / BK;
     if constexpr (CAUSAL) n_full = min(n_full, max(0, (q0 + p.causal_offset + 1) / BK));
-    n_full = min(n_full, nkt);
+    n_full = p.key_mask ? 0 : min(n_full, nkt);
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
     int kt = 0;

@@ -21,6 +21,7 @@ struct AttnParams {
     int seq_q, seq_k, heads, kv_heads;
     float scale_log2;    // scale * log2(e): scores enter exp2 directly
     int causal_offset;   // causal: key j is visible to query i iff j <= i + causal_offset
+    const int32_t *key_mask;  // null, or [seq_k]: key j hidden from every query where key_mask[j] == 0
 };
 
 // D: 64 or 128; causal: mask keys after the query's diagonal; out: 0 fp32, 1 bf16.

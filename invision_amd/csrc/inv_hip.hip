@@ -82,6 +82,7 @@ struct State {
     Buf xin, x16, w16, win, yout, cin, bias, gate;
     Buf aq, ak, avt, aqin, akin, avin;  // attention operands (bf16) and their staging
     Buf nvec;                           // normalisation scale/shift vectors from host
+    Buf amask;                          // attention key mask from host
     // Split/stream-K partial sums and arrival counters: uncached device memory
     // (coherent across XCDs without L2 maintenance).  Such memory is never
     // freed once a kernel has read it: outgrown buffers are retired, not freed.
@@ -881,6 +882,92 @@ double attention_pairs(int64_t sq, int64_t sk, bool causal) {
     return n;
 }
 
+int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_dtype, int out_dtype, int64_t heads,
+                   int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t head_dim, float scale,
+                   const int32_t *key_mask, int flags) {
+    TRY(check_init());
+    if (in_dtype != INV_DT_F32 && in_dtype != INV_DT_BF16) return fail(INV_ERR_ARG, "attention: bad in_dtype %d", in_dtype);
+    if (out_dtype != INV_DT_F32 && out_dtype != INV_DT_BF16)
+        return fail(INV_ERR_ARG, "attention: bad out_dtype %d", out_dtype);
+    if (flags & ~(INV_FLAG_DEVICE_PTRS | INV_FLAG_ASYNC | INV_ATTN_CAUSAL))
+        return fail(INV_ERR_ARG, "attention: unknown flags 0x%x", flags);
+    if ((flags & INV_FLAG_ASYNC) && !(flags & INV_FLAG_DEVICE_PTRS))
+        return fail(INV_ERR_ARG, "attention: ASYNC requires DEVICE_PTRS");
+    if (heads <= 0 || kv_heads <= 0 || heads % kv_heads)
+        return fail(INV_ERR_ARG, "attention: heads (%lld) must be a positive multiple of kv_heads (%lld)",
+                    (long long)heads, (long long)kv_heads);
+    if (seq_q < 0 || seq_k < 0) return fail(INV_ERR_ARG, "attention: negative sequence length");
+    if (head_dim != 64 && head_dim != 128)
+        return fail(INV_ERR_UNSUPPORTED, "attention: head_dim %lld (64 and 128 are supported)", (long long)head_dim);
+    if (!(scale > 0.0f) || scale > 3.0e38f) return fail(INV_ERR_ARG, "attention: scale must be positive and finite");
+    if (seq_q == 0) return INV_OK;
+    if (seq_k == 0) return fail(INV_ERR_ARG, "attention: seq_k is 0 (a softmax over no keys)");
+    if (!Q || !K || !V || !O) return fail(INV_ERR_ARG, "attention: Q, K, V or O is null");
+    if (seq_q > INT32_MAX / 2 || seq_k > INT32_MAX / 2 ||
+        ((seq_q + inv::kAttnBlockQ - 1) / inv::kAttnBlockQ) * heads > INT32_MAX)
+        return fail(INV_ERR_UNSUPPORTED, "attention: too many heads or tokens");
+    const int64_t hq = heads * head_dim, hk = kv_heads * head_dim;
+    const int64_t ldv = round_up(seq_k, inv::kAttnBlockK);
+    if (seq_k * hk * 2 >= ((int64_t)1 << 31) || head_dim * ldv * 2 >= ((int64_t)1 << 31))
+        return fail(INV_ERR_UNSUPPORTED, "attention: K or V above 2 GiB (32-bit buffer offsets)");
+    const bool dev = (flags & INV_FLAG_DEVICE_PTRS) != 0;
+    const size_t osz = out_dtype == INV_DT_F32 ? 4 : 2;
+    if (dev && !aligned(O, 16)) return fail(INV_ERR_ARG, "attention: device O must be 16-byte aligned");
+    if (dev && key_mask && !aligned(key_mask, 4)) return fail(INV_ERR_ARG, "attention: device key_mask not 4-byte aligned");
+
+    // bf16 operands: Q and K row-major as given (in place when already bf16 on
+    // the device), V transposed to [kv_heads*head_dim x ldv] with zero keys up to ldv.
+    const uint16_t *Qd = nullptr, *Kd = nullptr, *Vt = nullptr;
+    int64_t ldq = 0, ldk = 0, ldvt = 0;
+    TRY(stage_operand(Q, in_dtype, dev, false, seq_q, hq, hq, 1, 0, 8, g.aq, g.aqin, &Qd, &ldq));
+    TRY(stage_operand(K, in_dtype, dev, false, seq_k, hk, hk, 1, 0, 8, g.ak, g.akin, &Kd, &ldk));
+    TRY(stage_operand(V, in_dtype, dev, true, hk, seq_k, hk, 1, 0, inv::kAttnBlockK, g.avt, g.avin, &Vt, &ldvt));
+    void *Od = O;
+    if (!dev) {
+        TRY(ensure(g.yout, (size_t)(seq_q * hq) * osz));
+        Od = g.yout.p;
+    }
+    inv::AttnParams p{};
+    p.Q = Qd;
+    p.K = Kd;
+    p.Vt = Vt;
+    p.O = Od;
+    p.ldq = ldq;
+    p.ldk = ldk;
+    p.ldv = ldvt;
+    p.ldo = hq;
+    p.seq_q = (int)seq_q;
+    p.seq_k = (int)seq_k;
+    p.heads = (int)heads;
+    p.kv_heads = (int)kv_heads;
+    p.scale_log2 = scale * 1.44269504088896341f;
+    p.causal_offset = (int)(seq_k - seq_q);
+    p.key_mask = key_mask;
+    if (key_mask && !dev) {
+        TRY(ensure(g.amask, (size_t)seq_k * 4));
+        TRY(h2d_rows(g.amask.p, key_mask, 1, (size_t)seq_k * 4, (size_t)seq_k * 4));
+        p.key_mask = (const int32_t *)g.amask.p;
+    }
+    const bool causal = (flags & INV_ATTN_CAUSAL) != 0;
+    if (g.stats) HIPCHK(hipEventRecord(g.st0, g.stream));
+    HIPCHK(inv::attention_launch(p, (int)head_dim, causal, out_dtype == INV_DT_BF16 ? 1 : 0, g.stream));
+    if (g.stats) {
+        HIPCHK(hipEventRecord(g.st1, g.stream));
+        HIPCHK(hipEventSynchronize(g.st1));
+        float ms = 0.f;
+        HIPCHK(hipEventElapsedTime(&ms, g.st0, g.st1));
+        g.gemm_ms += ms;
+        g.flops += 4.0 * attention_pairs(seq_q, seq_k, causal) * (double)head_dim * (double)heads;
+    }
+    g.calls++;
+    if (!dev) {
+        TRY(d2h_rows(O, Od, seq_q, (size_t)hq * osz, (size_t)hq * osz));
+    } else if (!(flags & INV_FLAG_ASYNC)) {
+        HIPCHK(hipStreamSynchronize(g.stream));
+    }
+    return INV_OK;
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -931,7 +1018,7 @@ int inv_hip_shutdown(void) {
     for (auto *w : g.weights) free_weight(w);
     g.weights.clear();
     for (Buf *b : {&g.xin, &g.x16, &g.w16, &g.win, &g.yout, &g.cin, &g.bias, &g.gate, &g.aq, &g.ak, &g.avt, &g.aqin,
-                   &g.akin, &g.avin, &g.nvec}) release(*b);
+                   &g.akin, &g.avin, &g.nvec, &g.amask}) release(*b);
     // g.partial / g.counters (uncached) stay allocated until the process ends.
     release_stream_objects();
     g.init = false;
@@ -1072,80 +1159,16 @@ int inv_hip_attention(const void *Q, const void *K, const void *V, void *O, int 
                       int64_t heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t head_dim, float scale,
                       int flags) {
     std::lock_guard<std::mutex> lk(g_mu);
-    TRY(check_init());
-    if (in_dtype != INV_DT_F32 && in_dtype != INV_DT_BF16) return fail(INV_ERR_ARG, "attention: bad in_dtype %d", in_dtype);
-    if (out_dtype != INV_DT_F32 && out_dtype != INV_DT_BF16)
-        return fail(INV_ERR_ARG, "attention: bad out_dtype %d", out_dtype);
-    if (flags & ~(INV_FLAG_DEVICE_PTRS | INV_FLAG_ASYNC | INV_ATTN_CAUSAL))
-        return fail(INV_ERR_ARG, "attention: unknown flags 0x%x", flags);
-    if ((flags & INV_FLAG_ASYNC) && !(flags & INV_FLAG_DEVICE_PTRS))
-        return fail(INV_ERR_ARG, "attention: ASYNC requires DEVICE_PTRS");
-    if (heads <= 0 || kv_heads <= 0 || heads % kv_heads)
-        return fail(INV_ERR_ARG, "attention: heads (%lld) must be a positive multiple of kv_heads (%lld)",
-                    (long long)heads, (long long)kv_heads);
-    if (seq_q < 0 || seq_k < 0) return fail(INV_ERR_ARG, "attention: negative sequence length");
-    if (head_dim != 64 && head_dim != 128)
-        return fail(INV_ERR_UNSUPPORTED, "attention: head_dim %lld (64 and 128 are supported)", (long long)head_dim);
-    if (!(scale > 0.0f) || scale > 3.0e38f) return fail(INV_ERR_ARG, "attention: scale must be positive and finite");
-    if (seq_q == 0) return INV_OK;
-    if (seq_k == 0) return fail(INV_ERR_ARG, "attention: seq_k is 0 (a softmax over no keys)");
-    if (!Q || !K || !V || !O) return fail(INV_ERR_ARG, "attention: Q, K, V or O is null");
-    if (seq_q > INT32_MAX / 2 || seq_k > INT32_MAX / 2 ||
-        ((seq_q + inv::kAttnBlockQ - 1) / inv::kAttnBlockQ) * heads > INT32_MAX)
-        return fail(INV_ERR_UNSUPPORTED, "attention: too many heads or tokens");
-    const int64_t hq = heads * head_dim, hk = kv_heads * head_dim;
-    const int64_t ldv = round_up(seq_k, inv::kAttnBlockK);
-    if (seq_k * hk * 2 >= ((int64_t)1 << 31) || head_dim * ldv * 2 >= ((int64_t)1 << 31))
-        return fail(INV_ERR_UNSUPPORTED, "attention: K or V above 2 GiB (32-bit buffer offsets)");
-    const bool dev = (flags & INV_FLAG_DEVICE_PTRS) != 0;
-    const size_t osz = out_dtype == INV_DT_F32 ? 4 : 2;
-    if (dev && !aligned(O, 16)) return fail(INV_ERR_ARG, "attention: device O must be 16-byte aligned");
+    return attention_impl(Q, K, V, O, in_dtype, out_dtype, heads, kv_heads, seq_q, seq_k, head_dim, scale, nullptr,
+                          flags);
+}
 
-    // bf16 operands: Q and K row-major as given (in place when already bf16 on
-    // the device), V transposed to [kv_heads*head_dim x ldv] with zero keys up to ldv.
-    const uint16_t *Qd = nullptr, *Kd = nullptr, *Vt = nullptr;
-    int64_t ldq = 0, ldk = 0, ldvt = 0;
-    TRY(stage_operand(Q, in_dtype, dev, false, seq_q, hq, hq, 1, 0, 8, g.aq, g.aqin, &Qd, &ldq));
-    TRY(stage_operand(K, in_dtype, dev, false, seq_k, hk, hk, 1, 0, 8, g.ak, g.akin, &Kd, &ldk));
-    TRY(stage_operand(V, in_dtype, dev, true, hk, seq_k, hk, 1, 0, inv::kAttnBlockK, g.avt, g.avin, &Vt, &ldvt));
-    void *Od = O;
-    if (!dev) {
-        TRY(ensure(g.yout, (size_t)(seq_q * hq) * osz));
-        Od = g.yout.p;
-    }
-    inv::AttnParams p{};
-    p.Q = Qd;
-    p.K = Kd;
-    p.Vt = Vt;
-    p.O = Od;
-    p.ldq = ldq;
-    p.ldk = ldk;
-    p.ldv = ldvt;
-    p.ldo = hq;
-    p.seq_q = (int)seq_q;
-    p.seq_k = (int)seq_k;
-    p.heads = (int)heads;
-    p.kv_heads = (int)kv_heads;
-    p.scale_log2 = scale * 1.44269504088896341f;
-    p.causal_offset = (int)(seq_k - seq_q);
-    const bool causal = (flags & INV_ATTN_CAUSAL) != 0;
-    if (g.stats) HIPCHK(hipEventRecord(g.st0, g.stream));
-    HIPCHK(inv::attention_launch(p, (int)head_dim, causal, out_dtype == INV_DT_BF16 ? 1 : 0, g.stream));
-    if (g.stats) {
-        HIPCHK(hipEventRecord(g.st1, g.stream));
-        HIPCHK(hipEventSynchronize(g.st1));
-        float ms = 0.f;
-        HIPCHK(hipEventElapsedTime(&ms, g.st0, g.st1));
-        g.gemm_ms += ms;
-        g.flops += 4.0 * attention_pairs(seq_q, seq_k, causal) * (double)head_dim * (double)heads;
-    }
-    g.calls++;
-    if (!dev) {
-        TRY(d2h_rows(O, Od, seq_q, (size_t)hq * osz, (size_t)hq * osz));
-    } else if (!(flags & INV_FLAG_ASYNC)) {
-        HIPCHK(hipStreamSynchronize(g.stream));
-    }
-    return INV_OK;
+int inv_hip_attention_masked(const void *Q, const void *K, const void *V, void *O, int in_dtype, int out_dtype,
+                             int64_t heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t head_dim,
+                             float scale, const int32_t *key_mask, int flags) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return attention_impl(Q, K, V, O, in_dtype, out_dtype, heads, kv_heads, seq_q, seq_k, head_dim, scale, key_mask,
+                          flags);
 }
 
 int inv_hip_set_sgemm_precision(int mode) {

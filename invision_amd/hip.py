@@ -76,6 +76,8 @@ _PROTOS = {
                                     c_int64, c_int64, c_int64, c_int, c_int]),
     "inv_hip_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int64, c_int64, c_int64,
                                   c_int64, c_int64, c_float, c_int]),
+    "inv_hip_attention_masked": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int64, c_int64,
+                                         c_int64, c_int64, c_int64, c_float, c_void_p, c_int]),
     "inv_hip_sgemm": (c_int, [c_int, c_int, c_int, c_int64, c_int64, c_int64, c_float, c_void_p, c_int64, c_void_p,
                               c_int64, c_float, c_void_p, c_int64]),
     "inv_hip_sbgemm": (c_int, [c_int, c_int, c_int, c_int64, c_int64, c_int64, c_float, c_void_p, c_int64, c_void_p,

@@ -65,12 +65,13 @@ def _check_host(a: np.ndarray, dtype, name: str) -> None:
 class DeviceArray:
     """A device buffer owned by the library (inv_hip_malloc)."""
 
-    _DT = {"f32": (np.float32, 4, hip.INV_DT_F32), "bf16": (np.uint16, 2, hip.INV_DT_BF16)}
+    # i32: attention key masks (no element type of the GEMM paths)
+    _DT = {"f32": (np.float32, 4, hip.INV_DT_F32), "bf16": (np.uint16, 2, hip.INV_DT_BF16), "i32": (np.int32, 4, None)}
 
     def __init__(self, shape, dtype: str = "f32"):
         init()
         if dtype not in self._DT:
-            raise ValueError("dtype must be 'f32' or 'bf16'")
+            raise ValueError("dtype must be 'f32', 'bf16' or 'i32'")
         self.shape = tuple(int(s) for s in shape)
         self.dtype = dtype
         self.np_dtype, self.itemsize, self.inv_dtype = self._DT[dtype]
@@ -82,7 +83,7 @@ class DeviceArray:
     @classmethod
     def from_host(cls, a: np.ndarray, dtype: Optional[str] = None) -> "DeviceArray":
         if dtype is None:
-            dtype = "bf16" if a.dtype == np.uint16 else "f32"
+            dtype = {np.dtype(np.uint16): "bf16", np.dtype(np.int32): "i32"}.get(a.dtype, "f32")
         d = cls(a.shape, dtype)
         d.copy_from(a)
         return d
@@ -320,12 +321,24 @@ def QNNAdaLNLinear(dst: np.ndarray, x: np.ndarray, shift: np.ndarray, scale: np.
             w.free()
 
 
+def _key_mask_host(key_mask, seq_k: int):
+    if key_mask is None:
+        return None
+    m = np.ascontiguousarray(key_mask, dtype=np.int32)
+    if m.shape != (seq_k,):
+        raise ValueError(f"key_mask must have seq_k = {seq_k} entries")
+    return m
+
+
 def attention(Q: np.ndarray, K: np.ndarray, V: np.ndarray, heads: int, head_dim: int, kv_heads: Optional[int] = None,
-              scale: Optional[float] = None, causal: bool = False, out_dtype: str = "f32") -> np.ndarray:
+              scale: Optional[float] = None, causal: bool = False, out_dtype: str = "f32",
+              key_mask: Optional[np.ndarray] = None) -> np.ndarray:
     """Host arrays: O[seq_q x heads*head_dim] = softmax(scale * Q.K^T) V per head.
 
     Q [seq_q x heads*head_dim], K and V [seq_k x kv_heads*head_dim], float32 or bf16
-    bits (uint16, all three alike); scale defaults to 1/sqrt(head_dim)."""
+    bits (uint16, all three alike); scale defaults to 1/sqrt(head_dim).  key_mask
+    (seq_k ints): keys with 0 are hidden from every query (Qwen3's attention
+    mask, src/quicknn_qwen3.pas:753)."""
     kv_heads = heads if kv_heads is None else kv_heads
     if Q.dtype not in (np.float32, np.uint16) or K.dtype != Q.dtype or V.dtype != Q.dtype:
         raise TypeError("Q, K and V must all be float32 or all bf16 bits (uint16)")
@@ -338,23 +351,36 @@ def attention(Q: np.ndarray, K: np.ndarray, V: np.ndarray, heads: int, head_dim:
     odt, onp = (hip.INV_DT_F32, np.float32) if out_dtype == "f32" else (hip.INV_DT_BF16, np.uint16)
     O = np.empty((Q.shape[0], heads * head_dim), dtype=onp)
     sc = 1.0 / float(np.sqrt(head_dim)) if scale is None else float(scale)
-    hip.call("inv_hip_attention", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), dt, odt, heads, kv_heads, Q.shape[0], K.shape[0],
-             head_dim, sc, hip.INV_ATTN_CAUSAL if causal else 0)
+    flags = hip.INV_ATTN_CAUSAL if causal else 0
+    m = _key_mask_host(key_mask, K.shape[0])
+    if m is None:
+        hip.call("inv_hip_attention", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), dt, odt, heads, kv_heads, Q.shape[0],
+                 K.shape[0], head_dim, sc, flags)
+    else:
+        hip.call("inv_hip_attention_masked", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), dt, odt, heads, kv_heads, Q.shape[0],
+                 K.shape[0], head_dim, sc, _ptr(m), flags)
     return O
 
 
 def attention_device(Q: DeviceArray, K: DeviceArray, V: DeviceArray, O: DeviceArray, heads: int, head_dim: int,
                      kv_heads: Optional[int] = None, scale: Optional[float] = None, causal: bool = False,
-                     asynchronous: bool = False) -> None:
-    """inv_hip_attention on resident buffers (the shapes as for attention())."""
+                     asynchronous: bool = False, key_mask: Optional[DeviceArray] = None) -> None:
+    """inv_hip_attention on resident buffers (the shapes as for attention();
+    key_mask an i32 DeviceArray of seq_k entries)."""
     kv_heads = heads if kv_heads is None else kv_heads
     if not (Q.dtype == K.dtype == V.dtype):
         raise TypeError("Q, K and V must share a dtype")
     sc = 1.0 / float(np.sqrt(head_dim)) if scale is None else float(scale)
     flags = hip.INV_FLAG_DEVICE_PTRS | (hip.INV_FLAG_ASYNC if asynchronous else 0)
     flags |= hip.INV_ATTN_CAUSAL if causal else 0
-    hip.call("inv_hip_attention", Q.ptr, K.ptr, V.ptr, O.ptr, Q.inv_dtype, O.inv_dtype, heads, kv_heads, Q.shape[0],
-             K.shape[0], head_dim, sc, flags)
+    if key_mask is None:
+        hip.call("inv_hip_attention", Q.ptr, K.ptr, V.ptr, O.ptr, Q.inv_dtype, O.inv_dtype, heads, kv_heads,
+                 Q.shape[0], K.shape[0], head_dim, sc, flags)
+    else:
+        if key_mask.dtype != "i32" or key_mask.shape != (K.shape[0],):
+            raise ValueError("key_mask must be an i32 DeviceArray of seq_k entries")
+        hip.call("inv_hip_attention_masked", Q.ptr, K.ptr, V.ptr, O.ptr, Q.inv_dtype, O.inv_dtype, heads, kv_heads,
+                 Q.shape[0], K.shape[0], head_dim, sc, key_mask.ptr, flags)
 
 
 def QNNFlashAttention(dst: np.ndarray, Q: np.ndarray, K: np.ndarray, V: np.ndarray, heads: int, seq_q: int,

@@ -91,9 +91,9 @@ def lib() -> ctypes.CDLL:
         for f in (L.orc_attention_f64, L.orc_attention_qnn):
             f.restype = c_int
         L.orc_attention_f64.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
-                                        c_int64, ctypes.c_double, c_int, c_int]
+                                        c_int64, ctypes.c_double, c_int, c_void_p, c_int]
         L.orc_attention_qnn.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
-                                        c_int64, c_float, c_int, c_int]
+                                        c_int64, c_float, c_int, c_void_p, c_int]
         L.orc_softmax_qnn.argtypes = [c_void_p, c_int64]
         L.orc_adaln.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64]
         L.orc_rmsnorm_rows.argtypes = [c_void_p, c_void_p, c_void_p, c_int64, c_int64]
@@ -252,26 +252,39 @@ def _attn_args(Q, K, V, heads, kv_heads, d):
     return Q, K, V, seq_q, seq_k
 
 
+def _key_mask(key_mask, seq_k):
+    if key_mask is None:
+        return None
+    m = np.ascontiguousarray(key_mask, dtype=np.int32)
+    if m.shape != (seq_k,):
+        raise ValueError(f"key_mask needs {seq_k} entries, got shape {m.shape}")
+    return m
+
+
 def attention_f64(Q, K, V, heads: int, kv_heads: int, d: int, scale: float, causal: bool = False,
-                  nthreads: int = 0) -> np.ndarray:
+                  key_mask=None, nthreads: int = 0) -> np.ndarray:
     """softmax(scale * Q_h K_g^T) V_g per head in fp64 (the reference's attention
-    loops, quicknn_transformers.pas:1150-1311; quicknn_qwen3.pas:727-769)."""
+    loops, quicknn_transformers.pas:1150-1311; quicknn_qwen3.pas:727-769); keys
+    with key_mask[j] == 0 are hidden (quicknncpu.pas:3017-3028); a query with no
+    visible key gets zeros."""
     Q, K, V, seq_q, seq_k = _attn_args(Q, K, V, heads, kv_heads, d)
+    m = _key_mask(key_mask, seq_k)
     O = np.empty((seq_q, heads * d), dtype=np.float64)
     rc = lib().orc_attention_f64(_p(Q), _p(K), _p(V), _p(O), heads, kv_heads, seq_q, seq_k, d, float(scale),
-                                 int(causal), nthreads)
+                                 int(causal), _p(m) if m is not None else None, nthreads)
     if rc:
         raise ValueError(f"oracle attention failed ({rc})")
     return O
 
 
 def attention_qnn(Q, K, V, heads: int, kv_heads: int, d: int, scale: float, causal: bool = False,
-                  nthreads: int = 0) -> np.ndarray:
+                  key_mask=None, nthreads: int = 0) -> np.ndarray:
     """The reference's fp32 BLAS path with its AVX2 softmax (orc_attention_qnn)."""
     Q, K, V, seq_q, seq_k = _attn_args(Q, K, V, heads, kv_heads, d)
+    m = _key_mask(key_mask, seq_k)
     O = np.empty((seq_q, heads * d), dtype=np.float32)
     rc = lib().orc_attention_qnn(_p(Q), _p(K), _p(V), _p(O), heads, kv_heads, seq_q, seq_k, d, float(scale),
-                                 int(causal), nthreads)
+                                 int(causal), _p(m) if m is not None else None, nthreads)
     if rc:
         raise ValueError(f"oracle attention failed ({rc})")
     return O

@@ -493,7 +493,8 @@ int orc_linear_bf16w(const float *X, const uint16_t *W, const float *bias, float
  * (quicknn_transformers.pas:1150-1311, 2228-2271; quicknn_qwen3.pas:727-769) and
  * of QNNFlashAttention (quicknncpu.pas:2763). */
 int orc_attention_f64(const float *Q, const float *K, const float *V, double *O, int64_t heads, int64_t kv_heads,
-                      int64_t seq_q, int64_t seq_k, int64_t d, double scale, int causal, int nthreads) {
+                      int64_t seq_q, int64_t seq_k, int64_t d, double scale, int causal, const int32_t *key_mask,
+                      int nthreads) {
     if (heads <= 0 || kv_heads <= 0 || heads % kv_heads) return -1;
     const int64_t hq = heads * d, hk = kv_heads * d, grp = heads / kv_heads, off = seq_k - seq_q;
     if (nthreads > 0) omp_set_num_threads(nthreads);
@@ -514,6 +515,7 @@ int orc_attention_f64(const float *Q, const float *K, const float *V, double *O,
                 const int64_t last = causal ? (i + off < seq_k - 1 ? i + off : seq_k - 1) : seq_k - 1;
                 double mx = -INFINITY;
                 for (int64_t j = 0; j <= last; ++j) {
+                    if (key_mask && !key_mask[j]) continue;
                     const float *k = K + j * hk + g * d;
                     double dot = 0.0;
                     for (int64_t e = 0; e < d; ++e) dot += (double)q[e] * (double)k[e];
@@ -522,12 +524,14 @@ int orc_attention_f64(const float *Q, const float *K, const float *V, double *O,
                 }
                 double sum = 0.0;
                 for (int64_t j = 0; j <= last; ++j) {
+                    if (key_mask && !key_mask[j]) continue;
                     w[j] = exp(w[j] - mx);
                     sum += w[j];
                 }
                 double *o = O + i * hq + h * d;
                 for (int64_t e = 0; e < d; ++e) o[e] = 0.0;
-                for (int64_t j = 0; j <= last; ++j) {
+                for (int64_t j = 0; j <= last && sum > 0.0; ++j) {
+                    if (key_mask && !key_mask[j]) continue;
                     const float *v = V + j * hk + g * d;
                     const double pj = w[j] / sum;
                     for (int64_t e = 0; e < d; ++e) o[e] += pj * (double)v[e];
@@ -576,10 +580,12 @@ void orc_softmax_qnn(float *x, int64_t n) {
 
 /* The reference's BLAS-bound attention as it runs (quicknn_transformers.pas:
  * 1163-1189; quicknn_qwen3.pas:741-768): scores = scale * Q_h . K_g^T summed in
- * fp32 (cblas_gemm with alpha = scale), -inf where causal masks, QNNSoftmaxRows
+ * fp32 (cblas_gemm with alpha = scale), -inf where causal or the key mask hides
+ * the key (QNNMatTriangularFill, quicknncpu.pas:3017-3028), QNNSoftmaxRows
  * (orc_softmax_qnn), O_h = P . V_g summed in fp32. */
 int orc_attention_qnn(const float *Q, const float *K, const float *V, float *O, int64_t heads, int64_t kv_heads,
-                      int64_t seq_q, int64_t seq_k, int64_t d, float scale, int causal, int nthreads) {
+                      int64_t seq_q, int64_t seq_k, int64_t d, float scale, int causal, const int32_t *key_mask,
+                      int nthreads) {
     if (heads <= 0 || kv_heads <= 0 || heads % kv_heads) return -1;
     const int64_t hq = heads * d, hk = kv_heads * d, grp = heads / kv_heads, off = seq_k - seq_q;
     if (nthreads > 0) omp_set_num_threads(nthreads);
@@ -601,7 +607,7 @@ int orc_attention_qnn(const float *Q, const float *K, const float *V, float *O, 
                     const float *k = K + j * hk + g * d;
                     float dot = 0.0f;
                     for (int64_t e = 0; e < d; ++e) dot += q[e] * k[e];
-                    w[j] = (causal && j > i + off) ? -INFINITY : scale * dot;
+                    w[j] = ((causal && j > i + off) || (key_mask && !key_mask[j])) ? -INFINITY : scale * dot;
                 }
                 orc_softmax_qnn(w, seq_k);
                 float *o = O + i * hq + h * d;

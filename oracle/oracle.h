@@ -78,13 +78,16 @@ void orc_gated_add(float *dst, const float *gate, const float *proj, int64_t seq
  *      src/quicknn_qwen3.pas:727-769; src/quicknncpu.pas:2421-2500, 2763 ------
  * Q [seq_q x heads*d], K/V [seq_k x kv_heads*d], O [seq_q x heads*d]; head h uses
  * kv head h / (heads / kv_heads); causal: key j visible to query i iff
- * j <= i + seq_k - seq_q. */
+ * j <= i + seq_k - seq_q; key_mask (nullable, seq_k entries): key j hidden
+ * from every query where key_mask[j] == 0 (QNNMatTriangularFill's mask,
+ * quicknncpu.pas:3017-3028).  orc_attention_f64 gives a query with no visible
+ * key zeros; orc_attention_qnn follows the reference (NaN there). */
 int orc_attention_f64(const float *Q, const float *K, const float *V, double *O, int64_t heads,
                       int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t d, double scale, int causal,
-                      int nthreads);
+                      const int32_t *key_mask, int nthreads);
 int orc_attention_qnn(const float *Q, const float *K, const float *V, float *O, int64_t heads,
                       int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t d, float scale, int causal,
-                      int nthreads);
+                      const int32_t *key_mask, int nthreads);
 /* sSoftmax_avx2 (ops_avx2.inc:552-760) with an exact 1/sum in place of rcpss. */
 void orc_softmax_qnn(float *x, int64_t n);
 

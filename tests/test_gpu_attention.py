@@ -35,18 +35,18 @@ def gen(seed, sq, sk, heads, kv_heads, d):
     return Q, K, V
 
 
-def check(O, Q, K, V, heads, kv_heads, d, scale, causal, out="f32", rows=None, ref_path=True):
+def check(O, Q, K, V, heads, kv_heads, d, scale, causal, out="f32", rows=None, ref_path=True, key_mask=None):
     Of = bf16_bits_to_f32(O) if out == "bf16" else O
     if rows is not None:
         Of, Q = Of[rows], Q[rows]
         assert not causal
     Qr, Kr, Vr = round_bf16(Q), round_bf16(K), round_bf16(V)
-    r64 = oracle.attention_f64(Qr, Kr, Vr, heads, kv_heads, d, scale, causal)
+    r64 = oracle.attention_f64(Qr, Kr, Vr, heads, kv_heads, d, scale, causal, key_mask=key_mask)
     e = oracle.normwise_err(Of, r64)
     extra = TOL_BF16_OUT if out == "bf16" else 0.0
     msg = f"  normwise err: vs oracle on bf16 inputs {e:.3e}"
     if ref_path:
-        rq = oracle.attention_qnn(Q, K, V, heads, kv_heads, d, scale, causal)
+        rq = oracle.attention_qnn(Q, K, V, heads, kv_heads, d, scale, causal, key_mask=key_mask)
         e_ref = oracle.normwise_err(Of, rq)
         msg += f", vs the reference's fp32 path {e_ref:.3e}"
     print(msg, flush=True)
@@ -182,3 +182,66 @@ def test_stats_count_the_evaluated_pairs(hiplib):
             hip.call("inv_hip_stats_enable", 0)
         pairs = sum(min(sk, max(0, i + sk - sq + 1)) for i in range(sq)) if causal else sq * sk
         assert q.stats()["flops"] == 4.0 * pairs * d * heads
+
+
+# ------------------------------------------------------------ key mask --
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads,kv_heads,sq,sk,d,causal", [(2, 2, 200, 333, 128, False), (4, 2, 130, 130, 64, True),
+                                                          (8, 2, 257, 257, 128, True), (2, 1, 77, 300, 64, False)])
+def test_key_mask_matches_oracle(hiplib, heads, kv_heads, sq, sk, d, causal):
+    """Keys with mask 0 hidden from every query (QNNMatTriangularFill's mask,
+    src/quicknncpu.pas:3017-3028): a random mask, key 0 kept so that no causal
+    row is empty."""
+    Q, K, V = gen(70, sq, sk, heads, kv_heads, d)
+    mask = (np.random.default_rng(7).random(sk) < 0.7).astype(np.int32)
+    mask[0] = 1
+    O = q.attention(Q, K, V, heads=heads, head_dim=d, kv_heads=kv_heads, causal=causal, key_mask=mask)
+    check(O, Q, K, V, heads, kv_heads, d, 1.0 / math.sqrt(d), causal, key_mask=mask)
+
+
+@pytest.mark.gpu
+def test_padding_mask_equals_the_unpadded_keys(hiplib):
+    """Right padding (the Qwen3 encoder's, src/quicknn_qwen3.pas:293-303): masking
+    keys n.. gives exactly the attention over the first n keys."""
+    heads, d, sq, sk, n = 3, 128, 150, 300, 201
+    Q, K, V = gen(71, sq, sk, heads, heads, d)
+    mask = (np.arange(sk) < n).astype(np.int32)
+    Om = q.attention(Q, K, V, heads=heads, head_dim=d, key_mask=mask)
+    On = q.attention(Q, np.ascontiguousarray(K[:n]), np.ascontiguousarray(V[:n]), heads=heads, head_dim=d)
+    np.testing.assert_array_equal(Om, On)
+
+
+@pytest.mark.gpu
+def test_qwen3_encoder_shape_padded_prompt(hiplib):
+    """Qwen3-4B text encoder: 32 query heads over 8 kv heads of 128, 512 tokens,
+    causal, a 137-token prompt padded to 512 (padding queries see the prompt)."""
+    heads, kvh, d, s, n = 32, 8, 128, 512, 137
+    Q, K, V = gen(72, s, s, heads, kvh, d)
+    mask = (np.arange(s) < n).astype(np.int32)
+    O = q.attention(as_bf16_bits(Q), as_bf16_bits(K), as_bf16_bits(V), heads=heads, head_dim=d, kv_heads=kvh,
+                    causal=True, key_mask=mask)
+    check(O, Q, K, V, heads, kvh, d, 1.0 / math.sqrt(d), True, key_mask=mask)
+
+
+@pytest.mark.gpu
+def test_key_mask_device_pointers_and_empty_rows(hiplib):
+    heads, d, sq, sk = 2, 64, 70, 90
+    Q, K, V = gen(73, sq, sk, heads, heads, d)
+    mask = (np.arange(sk) % 3 != 1).astype(np.int32)
+    mask[:5] = 0  # causal queries 0..4 (offset 20: keys up to 24 visible) keep keys 5..
+    ref = q.attention(Q, K, V, heads=heads, head_dim=d, causal=True, key_mask=mask)
+    qd, kd, vd = (q.DeviceArray.from_host(as_bf16_bits(a), "bf16") for a in (Q, K, V))
+    md = q.DeviceArray.from_host(mask)
+    od = q.DeviceArray((sq, heads * d), "f32")
+    q.attention_device(qd, kd, vd, od, heads=heads, head_dim=d, causal=True, key_mask=md)
+    np.testing.assert_array_equal(od.to_host(), ref)
+    # every key hidden: zeros (the reference's softmax gives NaN there)
+    Oz = q.attention(Q, K, V, heads=heads, head_dim=d, key_mask=np.zeros(sk, np.int32))
+    assert not np.any(Oz)
+    lib = hip.load()
+    bad = lib.inv_hip_attention_masked(qd.ptr, kd.ptr, vd.ptr, od.ptr, hip.INV_DT_BF16, hip.INV_DT_F32, heads, heads,
+                                       sq, sk, d, 0.125, md.ptr + 2, hip.INV_FLAG_DEVICE_PTRS)
+    assert bad == hip.INV_ERR_ARG and "key_mask" in hip.last_error()
+    for a in (qd, kd, vd, md, od):
+        a.free()

@@ -307,8 +307,9 @@ def test_adaln_and_rmsnorm_against_numpy_and_invariants():
 
 # ------------------------------------------------------------ attention ----
 
-def _np_attention(Q, K, V, heads, kv_heads, d, scale, causal=False):
-    """numpy float64 softmax(QK^T)V per head: an independent statement."""
+def _np_attention(Q, K, V, heads, kv_heads, d, scale, causal=False, key_mask=None):
+    """numpy float64 softmax(QK^T)V per head: an independent statement (rows with
+    no visible key are left out: callers avoid them)."""
     sq, sk = Q.shape[0], K.shape[0]
     O = np.zeros((sq, heads * d))
     for h in range(heads):
@@ -316,6 +317,8 @@ def _np_attention(Q, K, V, heads, kv_heads, d, scale, causal=False):
         S = Q[:, h * d:(h + 1) * d].astype(np.float64) @ K[:, g * d:(g + 1) * d].astype(np.float64).T * scale
         if causal:
             S[np.arange(sk)[None, :] > np.arange(sq)[:, None] + (sk - sq)] = -np.inf
+        if key_mask is not None:
+            S[:, np.asarray(key_mask) == 0] = -np.inf
         P = np.exp(S - S.max(axis=1, keepdims=True))
         O[:, h * d:(h + 1) * d] = (P / P.sum(axis=1, keepdims=True)) @ V[:, g * d:(g + 1) * d].astype(np.float64)
     return O
@@ -359,6 +362,44 @@ def test_attention_invariants():
     rep = lambda A: np.concatenate([A[:, (j // 2) * 8:(j // 2 + 1) * 8] for j in range(4)], axis=1)
     np.testing.assert_allclose(oracle.attention_f64(Qg, Kg, Vg, 4, 2, 8, 0.4),
                                oracle.attention_f64(Qg, rep(Kg), rep(Vg), 4, 4, 8, 0.4), atol=1e-12)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_key_mask(causal):
+    """QNNMatTriangularFill's mask (quicknncpu.pas:3017-3028): a key with
+    mask 0 is hidden from every query.  Pinned by the numpy statement, by
+    removing the masked keys outright, and by the reference's fp32 path."""
+    h, d, sq, sk = 2, 8, 9, 9
+    Q, K, V = _qkv(56, sq, sk, h, h, d)
+    mask = np.array([1, 1, 0, 1, 0, 0, 1, 1, 1], np.int32)
+    got = oracle.attention_f64(Q, K, V, h, h, d, 0.5, causal, key_mask=mask)
+    rows = slice(0, sq)
+    np.testing.assert_allclose(got[rows], _np_attention(Q, K, V, h, h, d, 0.5, causal, mask)[rows], atol=1e-12)
+    keep = np.flatnonzero(mask)
+    if not causal:  # the masked keys removed: the same attention
+        np.testing.assert_allclose(got, oracle.attention_f64(Q, K[keep], V[keep], h, h, d, 0.5), atol=1e-12)
+    else:  # query i: the kept keys up to i
+        for i in range(sq):
+            vis = keep[keep <= i]
+            np.testing.assert_allclose(got[i:i + 1], oracle.attention_f64(Q[i:i + 1], K[vis], V[vis], h, h, d, 0.5),
+                                       atol=1e-12)
+    assert oracle.normwise_err(oracle.attention_qnn(Q, K, V, h, h, d, 0.5, causal, key_mask=mask), got) < 1e-5
+    # planted: the mask read inverted, or ignored
+    assert oracle.normwise_err(oracle.attention_f64(Q, K, V, h, h, d, 0.5, causal, key_mask=1 - mask), got) > 4e-3
+    assert oracle.normwise_err(oracle.attention_f64(Q, K, V, h, h, d, 0.5, causal), got) > 4e-3
+
+
+def test_attention_query_with_no_visible_key():
+    """Right-padded keys under a causal mask leave no row empty; a mask that hides
+    every key of a query does: zeros in the fp64 oracle, NaN in the reference's
+    softmax (its max is -inf)."""
+    h, d = 1, 4
+    Q, K, V = _qkv(57, 3, 3, h, h, d)
+    mask = np.array([0, 1, 1], np.int32)
+    o = oracle.attention_f64(Q, K, V, h, h, d, 0.5, True, key_mask=mask)
+    assert np.all(o[0] == 0.0) and np.all(np.isfinite(o))
+    r = oracle.attention_qnn(Q, K, V, h, h, d, 0.5, True, key_mask=mask)
+    assert np.all(np.isnan(r[0])) and np.all(np.isfinite(r[1:]))
 
 
 def test_softmax_qnn_is_the_softmax_within_its_polynomial():
