@@ -234,6 +234,26 @@ int inv_hip_attention_masked(const void *Q, const void *K, const void *V, void *
                              int64_t seq_k, int64_t head_dim, float scale, const int32_t *key_mask,
                              int flags);
 
+/* ---- between the Q/K projections and attention ---------------------------- */
+#define INV_ROPE_NONE        0
+#define INV_ROPE_INTERLEAVED 1 /* pairs (2k, 2k+1), tables [seq x head_dim], column 2k */
+#define INV_ROPE_HALF        2 /* pairs (i, i + head_dim/2), tables [seq x head_dim/2], column i */
+
+/* In place on X [seq x heads*head_dim] (fp32, row-major): each head's RMSNorm
+ * with norm_weight [head_dim] (null: none; rstd = 1/sqrt(mean(x^2) + 1e-6),
+ * x * w * rstd), then the rotary embedding of token s from row s of the tables
+ * (INV_ROPE_NONE: none).  Replaces, in one pass over X:
+ *  - FLUX2: QNNQKRMSNorm then QNNApplyRoPE2D (src/quicknn_transformers.pas:
+ *    1405-1408, 1415-1422; src/quicknncpu.pas:2209-2246, 2968-2992), called
+ *    once for Q and once for K with INV_ROPE_INTERLEAVED;
+ *  - Qwen3: QNNHeadRSMNorm then QNNApplyRoPE3 (src/quicknn_qwen3.pas:718-723,
+ *    223-230; src/quicknncpu.pas:2892-2917) with INV_ROPE_HALF.
+ * head_dim 64 or 128 (else INV_ERR_UNSUPPORTED).  flags: INV_FLAG_DEVICE_PTRS
+ * (X, weight and tables on the device), INV_FLAG_ASYNC. */
+int inv_hip_head_norm_rope(float *X, int64_t seq, int64_t heads, int64_t head_dim,
+                           const float *norm_weight, int rope, const float *cos_table,
+                           const float *sin_table, int flags);
+
 /* ---- the CBLAS slots ------------------------------------------------------ */
 /* Exactly the signature of TQNNSingleOPS.cblas_sgemm (src/quicknncpu.pas:
  * 102-103): C = alpha * op(A) . op(B) + beta * C on host fp32 arrays, RowMajor

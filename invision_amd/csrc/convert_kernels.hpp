@@ -220,6 +220,79 @@ __global__ void __launch_bounds__(256) norm_rows_f32_bf16_reg(const float *__res
     if (threadIdx.x < (cols_pad >> 2) - ng) *(uint2 *)(d + 4 * (ng + threadIdx.x)) = make_uint2(0u, 0u);
 }
 
+// The steps between the Q/K projections and attention, in place on fp32
+// x [rows x D] (rows = tokens * heads, D = 64 * EPT): each head's RMSNorm
+// (QNNRMSNorm over its D values, src/quicknncpu.pas:2159-2185: x * w[d] * rstd,
+// rstd = 1 / sqrt(sum(x^2) / D + eps)), then the rotary embedding of token
+// row / heads:
+//  ROPE_INTERLEAVED: pairs (2k, 2k+1) with table column 2k, tables [tokens x D]
+//                    (QNNApplyRoPE2D, src/quicknncpu.pas:2968-2992);
+//  ROPE_HALF:        pairs (i, i + D/2) with column i, tables [tokens x D/2]
+//                    (QNNApplyRoPE2, src/quicknncpu.pas:2892-2917).
+// One wave per head row, EPT consecutive values per lane: the sum of squares is
+// a wave reduction; a pair's partner is in the same lane (interleaved, EPT 2),
+// in lane l ^ 1 (interleaved, EPT 1) or in lane l ^ 32 (half).
+enum { ROPE_NONE = 0, ROPE_INTERLEAVED = 1, ROPE_HALF = 2 };
+
+template <int EPT, int ROPE, bool NORM>
+__global__ void __launch_bounds__(256) head_norm_rope(float *__restrict__ x, int64_t rows, int heads,
+                                                      const float *__restrict__ w, const float *__restrict__ ct,
+                                                      const float *__restrict__ st, float eps) {
+    constexpr int D = 64 * EPT;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // the whole wave
+    const int lane = threadIdx.x & 63;
+    float *v = x + row * D + EPT * lane;
+    float e[EPT];
+    if constexpr (EPT == 2) {
+        const float2 t = *(const float2 *)v;
+        e[0] = t.x;
+        e[1] = t.y;
+    } else {
+        e[0] = v[0];
+    }
+    if constexpr (NORM) {
+        float sq = 0.0f;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) sq += e[j] * e[j];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
+        const float rstd = 1.0f / sqrtf(sq / (float)D + eps);
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) e[j] = e[j] * w[EPT * lane + j] * rstd;
+    }
+    if constexpr (ROPE != ROPE_NONE) {
+        const int64_t tok = row / heads;
+        if constexpr (ROPE == ROPE_INTERLEAVED) {
+            if constexpr (EPT == 2) {
+                const float c = ct[tok * D + 2 * lane], sn = st[tok * D + 2 * lane];
+                const float x0 = e[0], x1 = e[1];
+                e[0] = x0 * c - x1 * sn;
+                e[1] = x1 * c + x0 * sn;
+            } else {
+                const float p = __shfl_xor(e[0], 1);
+                const int col = lane & ~1;
+                const float c = ct[tok * D + col], sn = st[tok * D + col];
+                e[0] = (lane & 1) ? e[0] * c + p * sn : e[0] * c - p * sn;
+            }
+        } else {
+            constexpr int H = D / 2;
+            const bool lo = lane < 32;
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) {
+                const float p = __shfl_xor(e[j], 32);
+                const int i = EPT * (lane & 31) + j;  // column of the pair
+                const float c = ct[tok * H + i], sn = st[tok * H + i];
+                e[j] = lo ? e[j] * c - p * sn : p * sn + e[j] * c;
+            }
+        }
+    }
+    if constexpr (EPT == 2)
+        *(float2 *)v = make_float2(e[0], e[1]);
+    else
+        v[0] = e[0];
+}
+
 // dst[r, c] = src[r, c] (bf16) for c < cols, 0 up to cols_pad.  One thread per 8 outputs.
 __global__ void __launch_bounds__(256) copy_rows_bf16(const uint16_t *__restrict__ src, int64_t lds,
                                                       uint16_t *__restrict__ dst, int64_t ldd, int64_t rows,

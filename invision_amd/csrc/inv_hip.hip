@@ -83,6 +83,7 @@ struct State {
     Buf aq, ak, avt, aqin, akin, avin;  // attention operands (bf16) and their staging
     Buf nvec;                           // normalisation scale/shift vectors from host
     Buf amask;                          // attention key mask from host
+    Buf hx, hvec;                       // head norm / rotary: X and the weight + tables from host
     // Split/stream-K partial sums and arrival counters: uncached device memory
     // (coherent across XCDs without L2 maintenance).  Such memory is never
     // freed once a kernel has read it: outgrown buffers are retired, not freed.
@@ -968,6 +969,71 @@ int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_
     return INV_OK;
 }
 
+// Per-head RMSNorm and rotary embedding of Q or K in place (fp32).
+int head_norm_rope_impl(float *X, int64_t seq, int64_t heads, int64_t head_dim, const float *w, int rope,
+                        const float *ct, const float *st, int flags) {
+    TRY(check_init());
+    if (flags & ~(INV_FLAG_DEVICE_PTRS | INV_FLAG_ASYNC)) return fail(INV_ERR_ARG, "head_norm_rope: unknown flags 0x%x", flags);
+    if ((flags & INV_FLAG_ASYNC) && !(flags & INV_FLAG_DEVICE_PTRS))
+        return fail(INV_ERR_ARG, "head_norm_rope: ASYNC requires DEVICE_PTRS");
+    if (seq < 0 || heads <= 0) return fail(INV_ERR_ARG, "head_norm_rope: bad shape");
+    if (head_dim != 64 && head_dim != 128)
+        return fail(INV_ERR_UNSUPPORTED, "head_norm_rope: head_dim %lld (64 and 128 are supported)", (long long)head_dim);
+    if (rope != INV_ROPE_NONE && rope != INV_ROPE_INTERLEAVED && rope != INV_ROPE_HALF)
+        return fail(INV_ERR_ARG, "head_norm_rope: bad rope mode %d", rope);
+    if (rope != INV_ROPE_NONE && (!ct || !st)) return fail(INV_ERR_ARG, "head_norm_rope: rotary tables are null");
+    if (seq == 0 || (!w && rope == INV_ROPE_NONE)) return INV_OK;
+    if (!X) return fail(INV_ERR_ARG, "head_norm_rope: X is null");
+    const int64_t rows = seq * heads;
+    if (rows > ((int64_t)1 << 33)) return fail(INV_ERR_UNSUPPORTED, "head_norm_rope: too many rows");
+    const bool dev = (flags & INV_FLAG_DEVICE_PTRS) != 0;
+    const int64_t width = (rope == INV_ROPE_HALF) ? head_dim / 2 : head_dim;  // table columns per token
+    const size_t xb = (size_t)(rows * head_dim) * 4, tb = (size_t)(seq * width) * 4, wb = (size_t)head_dim * 4;
+    float *xd = X;
+    const float *wd = w, *cd = ct, *sd = st;
+    if (!dev) {
+        TRY(ensure(g.hx, xb));
+        TRY(h2d_rows(g.hx.p, X, 1, xb, xb));
+        xd = (float *)g.hx.p;
+        TRY(ensure(g.hvec, wb + 2 * tb));
+        char *vb = (char *)g.hvec.p;
+        if (w) TRY(h2d_rows(vb, w, 1, wb, wb));
+        if (rope != INV_ROPE_NONE) {
+            TRY(h2d_rows(vb + wb, ct, 1, tb, tb));
+            TRY(h2d_rows(vb + wb + tb, st, 1, tb, tb));
+        }
+        wd = w ? (const float *)vb : nullptr;
+        cd = (const float *)(vb + wb);
+        sd = (const float *)(vb + wb + tb);
+    } else if (!aligned(X, 8) || (w && !aligned(w, 4)) || (ct && !aligned(ct, 4)) || (st && !aligned(st, 4))) {
+        return fail(INV_ERR_ARG, "head_norm_rope: X must be 8-byte and the vectors 4-byte aligned");
+    }
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, g.stream, xd, rows, (int)heads, wd, cd, sd, 1e-6f);
+    };
+    using namespace inv;
+#define INV_HNR(EPT)                                                                                      \
+    do {                                                                                                  \
+        if (!wd) {                                                                                        \
+            if (rope == INV_ROPE_INTERLEAVED) go(head_norm_rope<EPT, ROPE_INTERLEAVED, false>);           \
+            else go(head_norm_rope<EPT, ROPE_HALF, false>);                                               \
+        } else if (rope == INV_ROPE_NONE) go(head_norm_rope<EPT, ROPE_NONE, true>);                      \
+        else if (rope == INV_ROPE_INTERLEAVED) go(head_norm_rope<EPT, ROPE_INTERLEAVED, true>);          \
+        else go(head_norm_rope<EPT, ROPE_HALF, true>);                                                    \
+    } while (0)
+    if (head_dim == 128) INV_HNR(2);
+    else INV_HNR(1);
+#undef INV_HNR
+    HIPCHK(hipGetLastError());
+    if (!dev) {
+        TRY(d2h_rows(X, xd, 1, xb, xb));
+    } else if (!(flags & INV_FLAG_ASYNC)) {
+        HIPCHK(hipStreamSynchronize(g.stream));
+    }
+    return INV_OK;
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -1018,7 +1084,7 @@ int inv_hip_shutdown(void) {
     for (auto *w : g.weights) free_weight(w);
     g.weights.clear();
     for (Buf *b : {&g.xin, &g.x16, &g.w16, &g.win, &g.yout, &g.cin, &g.bias, &g.gate, &g.aq, &g.ak, &g.avt, &g.aqin,
-                   &g.akin, &g.avin, &g.nvec, &g.amask}) release(*b);
+                   &g.akin, &g.avin, &g.nvec, &g.amask, &g.hx, &g.hvec}) release(*b);
     // g.partial / g.counters (uncached) stay allocated until the process ends.
     release_stream_objects();
     g.init = false;
@@ -1169,6 +1235,12 @@ int inv_hip_attention_masked(const void *Q, const void *K, const void *V, void *
     std::lock_guard<std::mutex> lk(g_mu);
     return attention_impl(Q, K, V, O, in_dtype, out_dtype, heads, kv_heads, seq_q, seq_k, head_dim, scale, key_mask,
                           flags);
+}
+
+int inv_hip_head_norm_rope(float *X, int64_t seq, int64_t heads, int64_t head_dim, const float *norm_weight,
+                           int rope, const float *cos_table, const float *sin_table, int flags) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return head_norm_rope_impl(X, seq, heads, head_dim, norm_weight, rope, cos_table, sin_table, flags);
 }
 
 int inv_hip_set_sgemm_precision(int mode) {

@@ -43,6 +43,9 @@ INV_FLAG_PRECISE = 0x4
 INV_ATTN_CAUSAL = 0x100
 INV_NORM_ADALN = 1
 INV_NORM_RMS = 2
+INV_ROPE_NONE = 0
+INV_ROPE_INTERLEAVED = 1
+INV_ROPE_HALF = 2
 
 INV_ST_MAX_DIMS = 8
 INV_ST_TRUNCATE = 0x1
@@ -78,6 +81,8 @@ _PROTOS = {
                                   c_int64, c_int64, c_float, c_int]),
     "inv_hip_attention_masked": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int64, c_int64,
                                          c_int64, c_int64, c_int64, c_float, c_void_p, c_int]),
+    "inv_hip_head_norm_rope": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int, c_void_p, c_void_p,
+                                       c_int]),
     "inv_hip_sgemm": (c_int, [c_int, c_int, c_int, c_int64, c_int64, c_int64, c_float, c_void_p, c_int64, c_void_p,
                               c_int64, c_float, c_void_p, c_int64]),
     "inv_hip_sbgemm": (c_int, [c_int, c_int, c_int, c_int64, c_int64, c_int64, c_float, c_void_p, c_int64, c_void_p,

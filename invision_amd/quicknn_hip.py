@@ -398,6 +398,71 @@ def QNNFlashAttention(dst: np.ndarray, Q: np.ndarray, K: np.ndarray, V: np.ndarr
              seq_q, seq_k, head_dim, float(scale), 0)
 
 
+# ---------------------------------------------------------------------------
+# Between the Q/K projections and attention
+# ---------------------------------------------------------------------------
+
+_ROPE = {None: hip.INV_ROPE_NONE, "interleaved": hip.INV_ROPE_INTERLEAVED, "half": hip.INV_ROPE_HALF}
+
+
+def head_norm_rope(x: np.ndarray, heads: int, head_dim: int, norm_weight: Optional[np.ndarray] = None,
+                   rope: Optional[str] = None, cos: Optional[np.ndarray] = None,
+                   sin: Optional[np.ndarray] = None, seq: Optional[int] = None) -> None:
+    """In place on the first seq rows of fp32 x [seq x heads*head_dim] (seq
+    defaults to all of x): each head's RMSNorm (weight [head_dim], or none),
+    then the rotary embedding ("interleaved": tables [seq x head_dim]; "half":
+    [seq x head_dim/2]; None: none)."""
+    _check_host(x, np.float32, "x")
+    seq = x.size // (heads * head_dim) if seq is None else int(seq)
+    if x.size < seq * heads * head_dim:
+        raise ValueError("x must hold seq x heads*head_dim values")
+    w = None if norm_weight is None else np.ascontiguousarray(norm_weight, dtype=np.float32)
+    if w is not None and w.size != head_dim:
+        raise ValueError("norm_weight must have head_dim entries")
+    c = s_ = None
+    if rope is not None:
+        width = head_dim if rope == "interleaved" else head_dim // 2
+        c, s_ = (np.ascontiguousarray(np.asarray(t, dtype=np.float32).reshape(-1)[:seq * width]) for t in (cos, sin))
+        if c.size != seq * width or s_.size != seq * width:
+            raise ValueError(f"rotary tables must hold seq x {width} values")
+    hip.call("inv_hip_head_norm_rope", _ptr(x), seq, heads, head_dim, _ptr(w) if w is not None else None, _ROPE[rope],
+             _ptr(c) if c is not None else None, _ptr(s_) if s_ is not None else None, 0)
+
+
+def QNNQKRMSNorm(Q: np.ndarray, K: np.ndarray, QWeights: np.ndarray, KWeights: np.ndarray, seq: int, heads: int,
+                 headDim: int) -> None:
+    """TQNNSingleOPS.QNNQKRMSNorm (src/quicknncpu.pas:2209-2246), in place."""
+    _bound(Q.size >= seq * heads * headDim and K.size >= seq * heads * headDim, "ERROR : QNNQKRMSNorm out of bound")
+    head_norm_rope(Q, heads, headDim, QWeights, seq=seq)
+    head_norm_rope(K, heads, headDim, KWeights, seq=seq)
+
+
+def QNNApplyRoPE2D(dst: np.ndarray, cos_freq: np.ndarray, sin_freq: np.ndarray, seq: int, heads: int, head_dim: int,
+                   dim: int) -> None:
+    """TQNNSingleOPS.QNNApplyRoPE2D (src/quicknncpu.pas:2968-2992), in place: pairs
+    (2k, 2k+1) with cos/sin[s*head_dim + 2k] (dim, the axis size, is unused there too)."""
+    _bound(dst.size >= seq * heads * head_dim, "ERROR : QNNApplyRoPE2D out of bound")
+    head_norm_rope(dst, heads, head_dim, None, "interleaved", cos_freq, sin_freq, seq=seq)
+
+
+def QNNApplyRoPE3(dst: np.ndarray, cosIn: np.ndarray, sinIn: np.ndarray, seqLen: int, numHeads: int,
+                  headDim: int) -> None:
+    """TQNNSingleOPS.QNNApplyRoPE3 (src/quicknncpu.pas:2910-2917), in place: pairs
+    (i, i + headDim/2) with cos/sin[s*headDim/2 + i]."""
+    _bound(dst.size >= seqLen * numHeads * headDim, "ERROR : QNNApplyRoPE3 out of bound")
+    head_norm_rope(dst, numHeads, headDim, None, "half", cosIn, sinIn, seq=seqLen)
+
+
+def QNNHeadRSMNorm(dst: np.ndarray, src: np.ndarray, weight: np.ndarray, seqLen: int, numHeads: int,
+                   headDim: int) -> None:
+    """QNNHeadRSMNorm (src/quicknn_qwen3.pas:223-230): dst = per-head RMSNorm(src)."""
+    _bound(src.size >= seqLen * numHeads * headDim and dst.size >= seqLen * numHeads * headDim,
+           "ERROR : QNNHeadRSMNorm out of bound")
+    if dst is not src:
+        np.copyto(dst.reshape(-1)[:seqLen * numHeads * headDim], src.reshape(-1)[:seqLen * numHeads * headDim])
+    head_norm_rope(dst, numHeads, headDim, weight, seq=seqLen)
+
+
 def set_sgemm_precision(mode: int) -> None:
     """INV_PREC_BF16 / INV_PREC_SPLIT_A / INV_PREC_SPLIT_AB for cblas_gemm."""
     init()

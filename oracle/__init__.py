@@ -97,6 +97,9 @@ def lib() -> ctypes.CDLL:
         L.orc_softmax_qnn.argtypes = [c_void_p, c_int64]
         L.orc_adaln.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64]
         L.orc_rmsnorm_rows.argtypes = [c_void_p, c_void_p, c_void_p, c_int64, c_int64]
+        for f in (L.orc_rope_interleaved, L.orc_rope_half):
+            f.restype = None
+            f.argtypes = [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64]
         L.orc_add_bias_rows.argtypes = [c_void_p, c_void_p, c_int64, c_int64]
         L.orc_has_avx2.restype = c_int
         L.orc_max_threads.restype = c_int
@@ -314,6 +317,29 @@ def rmsnorm_rows(x: np.ndarray, weight=None) -> np.ndarray:
     w = np.ascontiguousarray(weight, dtype=np.float32) if weight is not None else None
     lib().orc_rmsnorm_rows(_p(y), _p(x), _p(w) if w is not None else None, x.shape[0], x.shape[1])
     return y
+
+
+def rope(x: np.ndarray, cos_t: np.ndarray, sin_t: np.ndarray, heads: int, head_dim: int, mode: str) -> np.ndarray:
+    """Rotary embedding on a copy of x [seq x heads*head_dim]: mode "interleaved"
+    (QNNApplyRoPE2D, tables [seq x head_dim]) or "half" (QNNApplyRoPE3, tables
+    [seq x head_dim/2])."""
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    c = np.ascontiguousarray(cos_t, dtype=np.float32)
+    s = np.ascontiguousarray(sin_t, dtype=np.float32)
+    seq = y.shape[0]
+    width = head_dim if mode == "interleaved" else head_dim // 2
+    if y.shape[1] != heads * head_dim or c.shape != (seq, width) or s.shape != (seq, width):
+        raise ValueError("rope: shape mismatch")
+    f = lib().orc_rope_interleaved if mode == "interleaved" else lib().orc_rope_half
+    f(_p(y), _p(c), _p(s), seq, heads, head_dim)
+    return y
+
+
+def head_rmsnorm(x: np.ndarray, weight, heads: int, head_dim: int) -> np.ndarray:
+    """Per-head RMSNorm (QNNQKRMSNorm, quicknncpu.pas:2209-2246; QNNHeadRSMNorm,
+    quicknn_qwen3.pas:223-230): QNNRMSNorm over each head's head_dim values."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return rmsnorm_rows(x.reshape(-1, head_dim), weight).reshape(x.shape)
 
 
 def silu_qnn(x: np.ndarray, up=None):

@@ -660,3 +660,35 @@ void orc_rmsnorm_rows(float *dst, const float *src, const float *weight, int64_t
         for (int64_t j = 0; j < dim; ++j) y[j] = weight ? x[j] * weight[j] * inv : x[j] * inv;
     }
 }
+
+/* QNNApplyRoPE2D (quicknncpu.pas:2968-2992): per token s and head h, for each
+ * pair (d, d+1): x0 cos - x1 sin, x1 cos + x0 sin with cos/sin[s*hd + d]. */
+void orc_rope_interleaved(float *x, const float *cos_t, const float *sin_t, int64_t seq, int64_t heads, int64_t d) {
+    for (int64_t s = 0; s < seq; ++s)
+        for (int64_t h = 0; h < heads; ++h) {
+            float *v = x + (s * heads + h) * d;
+            for (int64_t e = 0; e + 1 < d; e += 2) {
+                const float c = cos_t[s * d + e], sn = sin_t[s * d + e];
+                const float x0 = v[e], x1 = v[e + 1];
+                v[e] = x0 * c - x1 * sn;
+                v[e + 1] = x1 * c + x0 * sn;
+            }
+        }
+}
+
+/* QNNApplyRoPE3 -> QNNApplyRoPE2 (quicknncpu.pas:2892-2917): per token s and
+ * head h, for i < d/2: x[i] cos[i] - x[i+d/2] sin[i], x[i] sin[i] + x[i+d/2] cos[i]
+ * with cos/sin[s*d/2 + i]. */
+void orc_rope_half(float *x, const float *cos_t, const float *sin_t, int64_t seq, int64_t heads, int64_t d) {
+    const int64_t half = d / 2;
+    for (int64_t s = 0; s < seq; ++s)
+        for (int64_t h = 0; h < heads; ++h) {
+            float *v = x + (s * heads + h) * d;
+            for (int64_t i = 0; i < half; ++i) {
+                const float c = cos_t[s * half + i], sn = sin_t[s * half + i];
+                const float x0 = v[i], x1 = v[i + half];
+                v[i] = x0 * c - x1 * sn;
+                v[i + half] = x0 * sn + x1 * c;
+            }
+        }
+}

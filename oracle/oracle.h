@@ -91,6 +91,14 @@ int orc_attention_qnn(const float *Q, const float *K, const float *V, float *O, 
 /* sSoftmax_avx2 (ops_avx2.inc:552-760) with an exact 1/sum in place of rcpss. */
 void orc_softmax_qnn(float *x, int64_t n);
 
+/* ---- rotary position embedding of Q or K, in place, x [seq x heads*d] ------
+ * orc_rope_interleaved: QNNApplyRoPE2D (quicknncpu.pas:2968-2992), FLUX2's:
+ *   pairs (2k, 2k+1) rotated by cos/sin[s*d + 2k] (tables [seq x d]);
+ * orc_rope_half: QNNApplyRoPE3 -> QNNApplyRoPE2 (quicknncpu.pas:2892-2917),
+ *   Qwen3's: pairs (i, i + d/2) rotated by cos/sin[s*d/2 + i] (tables [seq x d/2]). */
+void orc_rope_interleaved(float *x, const float *cos_t, const float *sin_t, int64_t seq, int64_t heads, int64_t d);
+void orc_rope_half(float *x, const float *cos_t, const float *sin_t, int64_t seq, int64_t heads, int64_t d);
+
 /* ---- QNNAdaLN (quicknncpu.pas:3042-3060), QNNRMSNormRows (:2159-2198) ---- */
 void orc_adaln(float *dst, const float *src, const float *shift, const float *scale, int64_t seq, int64_t hidden);
 void orc_rmsnorm_rows(float *dst, const float *src, const float *weight, int64_t rows, int64_t dim);

@@ -454,3 +454,59 @@ def test_checks_catch_planted_mistakes():
     assert oracle.normwise_err(oracle.linear_bf16w(Xo, W, b), good) > 1e-2
     Wr = np.ascontiguousarray(np.roll(W, 1, axis=0))  # output row n off by one
     assert oracle.normwise_err(oracle.linear_bf16w(X, Wr, b), good) > 1e-2
+
+
+# ------------------------------------------------- QK norm and rotary --
+
+def _angles(seq, width, seed):
+    th = np.random.default_rng(seed).uniform(-np.pi, np.pi, (seq, width))
+    return np.cos(th).astype(np.float32), np.sin(th).astype(np.float32), th
+
+
+@pytest.mark.parametrize("mode", ["interleaved", "half"])
+def test_rope_is_the_pairwise_complex_rotation(mode):
+    """QNNApplyRoPE2D pairs (2k, 2k+1) with table column 2k; QNNApplyRoPE3 pairs
+    (i, i + d/2) with column i.  Pinned by numpy complex products, the identity
+    table, norm preservation and composition of angles."""
+    seq, heads, d = 5, 3, 16
+    x = _rand((seq, heads * d), 60)
+    width = d if mode == "interleaved" else d // 2
+    c, s, th = _angles(seq, width, 61)
+    got = oracle.rope(x, c, s, heads, d, mode)
+    xh = x.reshape(seq, heads, d).astype(np.float64)
+    if mode == "interleaved":
+        z = (xh[..., 0::2] + 1j * xh[..., 1::2]) * (c[:, None, 0::2] + 1j * s[:, None, 0::2])
+        ref = np.empty_like(xh)
+        ref[..., 0::2], ref[..., 1::2] = z.real, z.imag
+    else:
+        z = (xh[..., :d // 2] + 1j * xh[..., d // 2:]) * (c[:, None, :] + 1j * s[:, None, :])
+        ref = np.concatenate([z.real, z.imag], axis=-1)
+    np.testing.assert_allclose(got.reshape(seq, heads, d), ref, atol=1e-5)
+    # identity table
+    np.testing.assert_array_equal(oracle.rope(x, np.ones_like(c), np.zeros_like(s), heads, d, mode), x)
+    # a rotation keeps each pair's length; two rotations add their angles
+    pairs = lambda a: (a.reshape(seq, heads, d)[..., 0::2], a.reshape(seq, heads, d)[..., 1::2]) if mode == "interleaved" \
+        else (a.reshape(seq, heads, d)[..., :d // 2], a.reshape(seq, heads, d)[..., d // 2:])
+    (a0, a1), (b0, b1) = pairs(x.astype(np.float64)), pairs(got.astype(np.float64))
+    np.testing.assert_allclose(a0 ** 2 + a1 ** 2, b0 ** 2 + b1 ** 2, rtol=1e-5, atol=1e-6)
+    c2, s2 = np.cos(2 * th).astype(np.float32), np.sin(2 * th).astype(np.float32)
+    np.testing.assert_allclose(oracle.rope(got, c, s, heads, d, mode), oracle.rope(x, c2, s2, heads, d, mode), atol=1e-5)
+    # planted: the opposite rotation, or the other pairing, is far off
+    assert np.max(np.abs(oracle.rope(x, c, -s, heads, d, mode) - got)) > 0.1
+    if mode == "half":
+        cw, sw = np.repeat(c, 2, axis=1), np.repeat(s, 2, axis=1)
+        assert np.max(np.abs(oracle.rope(x, cw, sw, heads, d, "interleaved") - got)) > 0.1
+
+
+def test_head_rmsnorm_normalises_each_head():
+    """QNNQKRMSNorm / QNNHeadRSMNorm: each head's head_dim values over their own
+    rms (EPSILON 1e-6), times the shared weight; not the whole row's rms."""
+    seq, heads, d = 4, 3, 8
+    x = _rand((seq, heads * d), 62) * np.float32(3.0)
+    w = _rand((d,), 63)
+    got = oracle.head_rmsnorm(x, w, heads, d)
+    xh = x.reshape(seq, heads, d).astype(np.float64)
+    ref = xh / np.sqrt((xh ** 2).mean(-1, keepdims=True) + 1e-6) * w
+    np.testing.assert_allclose(got.reshape(seq, heads, d), ref, rtol=1e-5, atol=1e-6)
+    whole = oracle.rmsnorm_rows(x, np.tile(w, heads))
+    assert np.max(np.abs(whole - got)) > 1e-2
