@@ -67,12 +67,20 @@ __global__ void __launch_bounds__(256) cvt_rows_f32_bf16(const float *__restrict
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = (c0 + e < cols) ? s[e] : 0.0f;
     }
-    uint16_t hi[8], lo[8];
+    uint16_t *d = dst + r * ldd + c0;
+    uint16_t hi[8];
+    if (lo_mask == 0) {  // the plain rounding: no lo parts to form
+#pragma unroll
+        for (int e = 0; e < 8; ++e) hi[e] = bf16_rne(v[e]);
+        const uint4 ohi = pack8(hi);
+        for (int sg = 0; sg < nseg; ++sg) *(uint4 *)(d + sg * cols_pad) = ohi;
+        return;
+    }
+    uint16_t lo[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) bf16_split(v[e], hi[e], lo[e]);
     const uint4 ohi = pack8(hi);
     const uint4 olo = pack8(lo);
-    uint16_t *d = dst + r * ldd + c0;
     for (int sg = 0; sg < nseg; ++sg) *(uint4 *)(d + sg * cols_pad) = ((lo_mask >> sg) & 1) ? olo : ohi;
 }
 
