@@ -181,11 +181,17 @@ def run_workload(name, steps, warmup, check=True, host_path=False, warmup_second
         # The reference's own calling convention: fp32 X and Y in host memory,
         # copied over PCIe on every call (pinned bounce buffers), X rounded on
         # the device.  Reported beside the device-resident rate, never as it.
+        # Y is the caller's buffer, written on every call (as the reference's
+        # dst TMemoryBlock), not a fresh array whose first touch would be timed.
         Xh = np.ascontiguousarray(X if xdt == "f32" else bf16_bits_to_f32(Xin))
-        q.linear(Xh, w, epilogue=epi)
+        Yh = np.zeros((M, R), np.float32)
+        host_call = lambda: hip.call("inv_hip_linear", Xh.ctypes.data, hip.INV_DT_F32, w.handle, None, Yh.ctypes.data,
+                                     hip.INV_DT_F32, M, K, R, hip.INV_EPI_NONE if epi == "none" else
+                                     (hip.INV_EPI_SILU if epi == "silu" else hip.INV_EPI_GELU_ERF), 0)
+        host_call()
         reps, th = 0, time.perf_counter()
         while reps < 3 or time.perf_counter() - th < 1.0:
-            q.linear(Xh, w, epilogue=epi)
+            host_call()
             reps += 1
         host_ms = (time.perf_counter() - th) * 1e3 / reps
         res["host_fp32_io_ms"] = host_ms

@@ -13,12 +13,16 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
+#include <condition_variable>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "attention.hpp"
@@ -64,6 +68,97 @@ namespace {
 
 constexpr uint32_t kWeightMagic = 0x57484950u;  // "WHIP"
 constexpr size_t kPinChunk = 32u << 20;
+
+// Host-side copies into and out of the pinned bounce buffers, spread over a
+// few threads: one thread's memcpy moves ~14 GB/s, well below what PCIe moves,
+// and with host fp32 activations (the reference's calling convention) these
+// copies are the whole cost of a call.  The calling thread takes slices too.
+class CopyPool {
+public:
+    ~CopyPool() { stop_all(); }
+    void start(int nthreads) {
+        for (int i = 0; i + 1 < nthreads; ++i) workers_.emplace_back([this] { loop(); });
+    }
+    void stop_all() {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        for (auto &t : workers_) t.join();
+        workers_.clear();
+        stop_ = false;
+    }
+    int threads() const { return (int)workers_.size() + 1; }
+    // fn(i) for every i in [0, count); returns when all are done and no worker
+    // holds fn any more.
+    void parallel_for(int count, const std::function<void(int)> &fn) {
+        if (workers_.empty() || count <= 1) {
+            for (int i = 0; i < count; ++i) fn(i);
+            return;
+        }
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            job_ = &fn;
+            total_ = count;
+            next_.store(0);
+            active_ = (int)workers_.size();
+            ++gen_;
+        }
+        cv_.notify_all();
+        work();
+        std::unique_lock<std::mutex> lk(mu_);
+        done_.wait(lk, [&] { return active_ == 0; });
+        job_ = nullptr;
+    }
+
+private:
+    void work() {
+        for (int i; (i = next_.fetch_add(1)) < total_;) (*job_)(i);
+    }
+    void loop() {
+        uint64_t seen = 0;
+        std::unique_lock<std::mutex> lk(mu_);
+        for (;;) {
+            cv_.wait(lk, [&] { return stop_ || gen_ != seen; });
+            if (stop_) return;
+            seen = gen_;
+            lk.unlock();
+            work();
+            lk.lock();
+            if (--active_ == 0) done_.notify_one();
+        }
+    }
+    std::vector<std::thread> workers_;
+    std::mutex mu_;
+    std::condition_variable cv_, done_;
+    const std::function<void(int)> *job_ = nullptr;
+    std::atomic<int> next_{0};
+    int total_ = 0, active_ = 0;
+    uint64_t gen_ = 0;
+    bool stop_ = false;
+};
+
+CopyPool g_copy;
+
+// memcpy of n bytes (or of `rows` rows of `width` bytes between pitches) on the pool.
+void par_copy_rows(char *dst, size_t dpitch, const char *src, size_t spitch, int64_t rows, size_t width) {
+    const size_t total = (size_t)rows * width;
+    const int parts = (int)std::min<size_t>((size_t)g_copy.threads() * 2, std::max<size_t>(1, total >> 20));
+    if (dpitch == width && spitch == width) {
+        const size_t per = (total / parts + 63) & ~(size_t)63;
+        g_copy.parallel_for(parts, [&](int i) {
+            const size_t off = (size_t)i * per;
+            if (off < total) memcpy(dst + off, src + off, std::min(per, total - off));
+        });
+    } else {
+        const int64_t per = (rows + parts - 1) / parts;
+        g_copy.parallel_for(parts, [&](int i) {
+            for (int64_t r = (int64_t)i * per; r < std::min<int64_t>(rows, (int64_t)(i + 1) * per); ++r)
+                memcpy(dst + r * dpitch, src + r * spitch, width);
+        });
+    }
+}
 
 struct Buf {
     void *p = nullptr;
@@ -167,7 +262,7 @@ int h2d_rows(void *dev, const void *host, int64_t rows, size_t width, size_t pit
             for (size_t off = 0; off < width; off += kPinChunk) {
                 size_t n = std::min(kPinChunk, width - off);
                 HIPCHK(hipEventSynchronize(g.pin_ev[k]));
-                memcpy(g.pin[k], src + r * pitch + off, n);
+                par_copy_rows((char *)g.pin[k], n, src + r * pitch + off, n, 1, n);
                 HIPCHK(hipMemcpyAsync(dst + r * width + off, g.pin[k], n, hipMemcpyHostToDevice, g.stream));
                 HIPCHK(hipEventRecord(g.pin_ev[k], g.stream));
                 k ^= 1;
@@ -179,11 +274,7 @@ int h2d_rows(void *dev, const void *host, int64_t rows, size_t width, size_t pit
         const int64_t nr = std::min(rows_per, rows - r0);
         HIPCHK(hipEventSynchronize(g.pin_ev[k]));
         char *pb = (char *)g.pin[k];
-        if (pitch == width) {
-            memcpy(pb, src + r0 * pitch, (size_t)nr * width);
-        } else {
-            for (int64_t r = 0; r < nr; ++r) memcpy(pb + r * width, src + (r0 + r) * pitch, width);
-        }
+        par_copy_rows(pb, width, src + r0 * pitch, pitch, nr, width);
         HIPCHK(hipMemcpyAsync(dst + r0 * width, pb, (size_t)nr * width, hipMemcpyHostToDevice, g.stream));
         HIPCHK(hipEventRecord(g.pin_ev[k], g.stream));
         k ^= 1;
@@ -216,11 +307,9 @@ int d2h_rows(void *host, const void *dev, int64_t rows, size_t width, size_t pit
         HIPCHK(hipEventSynchronize(g.pin_ev[i & 1]));
         const char *pb = (const char *)g.pin[i & 1];
         if (pc.nr == 1 && width > kPinChunk) {
-            memcpy(dst + pc.r0 * pitch + pc.off, pb, pc.n);
-        } else if (pitch == width) {
-            memcpy(dst + pc.r0 * pitch, pb, pc.n);
+            par_copy_rows(dst + pc.r0 * pitch + pc.off, pc.n, pb, pc.n, 1, pc.n);
         } else {
-            for (int64_t r = 0; r < pc.nr; ++r) memcpy(dst + (pc.r0 + r) * pitch, pb + r * width, width);
+            par_copy_rows(dst + pc.r0 * pitch, pitch, pb, width, pc.nr, width);
         }
         return INV_OK;
     };
@@ -1072,6 +1161,10 @@ int inv_hip_init(int device) {
     g.cu_count = prop.multiProcessorCount;
     g.clock_khz = prop.clockRate;
     snprintf(g.name, sizeof g.name, "%s (%s)", prop.name, prop.gcnArchName);
+    // host copy threads: INV_HIP_COPY_THREADS, else up to 8 of the host's
+    const char *ct = getenv("INV_HIP_COPY_THREADS");
+    const int hw = (int)std::max(1u, std::thread::hardware_concurrency());
+    g_copy.start(std::max(1, std::min(64, (ct && *ct) ? atoi(ct) : std::min(8, hw))));
     g.init = true;
     return INV_OK;
 }
@@ -1087,6 +1180,7 @@ int inv_hip_shutdown(void) {
                    &g.akin, &g.avin, &g.nvec, &g.amask, &g.hx, &g.hvec}) release(*b);
     // g.partial / g.counters (uncached) stay allocated until the process ends.
     release_stream_objects();
+    g_copy.stop_all();
     g.init = false;
     g.device = -1;
     g.stats = false;
