@@ -279,7 +279,9 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
             // tiles, rather than 64 multiplies executed on every one)
             asm volatile("" ::: "memory");
             const float m_new = grow ? mx : m_run;
-            const float alpha = exp2_hw(m_run - m_new);  // 0 on the first tile, 1 where the max stays
+            // 0 on the first tile, 1 where the max stays; a row that has seen no
+            // key yet (m_new = -inf) keeps its zero sums (-inf - -inf would be NaN)
+            const float alpha = (m_new == -__builtin_inff()) ? 1.0f : exp2_hw(m_run - m_new);
             l_run *= alpha;
 #pragma unroll
             for (int i = 0; i < ND; ++i) o[i] *= alpha;

@@ -245,3 +245,17 @@ def test_key_mask_device_pointers_and_empty_rows(hiplib):
     assert bad == hip.INV_ERR_ARG and "key_mask" in hip.last_error()
     for a in (qd, kd, vd, md, od):
         a.free()
+
+
+@pytest.mark.gpu
+def test_rows_without_keys_are_zero(hiplib):
+    """Queries before the diagonal's start (seq_q > seq_k, causal) see no key and
+    get zeros, also in waves whose other rows do see keys (their running max
+    moves while these rows' stays at -inf)."""
+    heads, d, sq, sk = 2, 64, 300, 100
+    Q, K, V = gen(75, sq, sk, heads, heads, d)
+    O = q.attention(Q, K, V, heads=heads, head_dim=d, causal=True)
+    empty = sq - sk  # query i sees keys up to i - 200
+    assert np.all(np.isfinite(O))
+    assert not np.any(O[:empty])
+    check(O[empty:], Q[empty:], K, V, heads, heads, d, 1.0 / math.sqrt(d), True)
