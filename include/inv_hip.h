@@ -254,6 +254,22 @@ int inv_hip_head_norm_rope(float *X, int64_t seq, int64_t heads, int64_t head_di
                            const float *norm_weight, int rope, const float *cos_table,
                            const float *sin_table, int flags);
 
+/* inv_hip_attention_masked on fp32 Q and K with each head's RMSNorm and the
+ * rotary embedding applied while they are staged for the MFMA (one read of
+ * each, no separate pass): the FLUX2 and Qwen3 sequence of
+ * inv_hip_head_norm_rope on Q, on K, then attention, in one call.
+ * q_/k_norm_weight [head_dim] or null; rope as for inv_hip_head_norm_rope with
+ * per-token tables for Q (seq_q rows) and K (seq_k rows; for FLUX2's joint
+ * attention the text rows then the image rows, like K itself); key_mask as for
+ * inv_hip_attention_masked.  Q, K, V fp32 (host or device per
+ * INV_FLAG_DEVICE_PTRS); no counterpart in the reference as one call. */
+int inv_hip_attention_qk_norm_rope(const float *Q, const float *K, const float *V, void *O,
+                                   int out_dtype, int64_t heads, int64_t kv_heads, int64_t seq_q,
+                                   int64_t seq_k, int64_t head_dim, float scale,
+                                   const float *q_norm_weight, const float *k_norm_weight, int rope,
+                                   const float *q_cos, const float *q_sin, const float *k_cos,
+                                   const float *k_sin, const int32_t *key_mask, int flags);
+
 /* ---- the CBLAS slots ------------------------------------------------------ */
 /* Exactly the signature of TQNNSingleOPS.cblas_sgemm (src/quicknncpu.pas:
  * 102-103): C = alpha * op(A) . op(B) + beta * C on host fp32 arrays, RowMajor

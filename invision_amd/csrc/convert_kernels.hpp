@@ -242,10 +242,13 @@ __global__ void __launch_bounds__(256) norm_rows_f32_bf16_reg(const float *__res
 // in lane l ^ 1 (interleaved, EPT 1) or in lane l ^ 32 (half).
 enum { ROPE_NONE = 0, ROPE_INTERLEAVED = 1, ROPE_HALF = 2 };
 
-template <int EPT, int ROPE, bool NORM>
+// BF16OUT: the result goes to y [rows x D] as bf16 (nearest-even) instead of
+// back into x, the Q/K operand staging of the fused attention entry.
+template <int EPT, int ROPE, bool NORM, bool BF16OUT = false>
 __global__ void __launch_bounds__(256) head_norm_rope(float *__restrict__ x, int64_t rows, int heads,
                                                       const float *__restrict__ w, const float *__restrict__ ct,
-                                                      const float *__restrict__ st, float eps) {
+                                                      const float *__restrict__ st, float eps,
+                                                      uint16_t *__restrict__ y = nullptr) {
     constexpr int D = 64 * EPT;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;  // the whole wave
@@ -295,10 +298,17 @@ __global__ void __launch_bounds__(256) head_norm_rope(float *__restrict__ x, int
             }
         }
     }
-    if constexpr (EPT == 2)
+    if constexpr (BF16OUT) {
+        uint16_t *o = y + row * D + EPT * lane;
+        if constexpr (EPT == 2)
+            *(uint32_t *)o = (uint32_t)bf16_rne(e[0]) | ((uint32_t)bf16_rne(e[1]) << 16);
+        else
+            o[0] = bf16_rne(e[0]);
+    } else if constexpr (EPT == 2) {
         *(float2 *)v = make_float2(e[0], e[1]);
-    else
+    } else {
         v[0] = e[0];
+    }
 }
 
 // dst[r, c] = src[r, c] (bf16) for c < cols, 0 up to cols_pad.  One thread per 8 outputs.

@@ -957,6 +957,81 @@ void release_stream_objects() {
     g.stream = nullptr;
 }
 
+// x [rows x head_dim] fp32 (rows = tokens * heads): per-head RMSNorm (w, or
+// none) then the rotary embedding (rope, tables ct/st), in place, or into y as
+// bf16 when y is given.
+int launch_head_norm_rope(float *x, uint16_t *y, int64_t rows, int64_t heads, int64_t head_dim, const float *w,
+                          int rope, const float *ct, const float *st) {
+    if (rows == 0) return INV_OK;
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, g.stream, x, rows, (int)heads, w, ct, st, 1e-6f, y);
+    };
+    using namespace inv;
+#define INV_HNR(EPT, OB)                                                                                  \
+    do {                                                                                                  \
+        if (!w) {                                                                                         \
+            if (rope == INV_ROPE_INTERLEAVED) go(head_norm_rope<EPT, ROPE_INTERLEAVED, false, OB>);       \
+            else if (rope == INV_ROPE_HALF) go(head_norm_rope<EPT, ROPE_HALF, false, OB>);                \
+            else go(head_norm_rope<EPT, ROPE_NONE, false, OB>);                                           \
+        } else if (rope == INV_ROPE_NONE) go(head_norm_rope<EPT, ROPE_NONE, true, OB>);                  \
+        else if (rope == INV_ROPE_INTERLEAVED) go(head_norm_rope<EPT, ROPE_INTERLEAVED, true, OB>);      \
+        else go(head_norm_rope<EPT, ROPE_HALF, true, OB>);                                                \
+    } while (0)
+    if (head_dim == 128) {
+        if (y) INV_HNR(2, true);
+        else INV_HNR(2, false);
+    } else {
+        if (y) INV_HNR(1, true);
+        else INV_HNR(1, false);
+    }
+#undef INV_HNR
+    HIPCHK(hipGetLastError());
+    return INV_OK;
+}
+
+// The per-head RMSNorm and rotary embedding applied to Q and K while they are
+// staged for attention (inv_hip_attention_qk_norm_rope).
+struct QkPrep {
+    const float *q_w, *k_w;  // RMSNorm weights [head_dim] or null
+    int rope;                // INV_ROPE_*
+    const float *q_cos, *q_sin, *k_cos, *k_sin;  // per-token tables or null
+};
+
+// fp32 X [seq x nh*D] (host or device) -> norm + rotary -> bf16 [seq x nh*D] in dst.
+// Host X, weight and tables are copied to the device first (vec: scratch for them).
+int stage_prepped(const float *X, bool dev, int64_t seq, int64_t nh, int64_t D, const float *w, int rope,
+                  const float *ct, const float *st, Buf &dst, Buf &tmp, Buf &vec, const uint16_t **out,
+                  int64_t *out_ld) {
+    const int64_t cols = nh * D;
+    const int64_t width = (rope == INV_ROPE_HALF) ? D / 2 : D;
+    const size_t xb = (size_t)(seq * cols) * 4, wb = (size_t)D * 4, tb = (size_t)(seq * width) * 4;
+    const float *src = X;
+    const float *wd = w, *cd = ct, *sd = st;
+    if (!dev) {
+        TRY(ensure(tmp, xb));
+        TRY(h2d_rows(tmp.p, X, 1, xb, xb));
+        src = (const float *)tmp.p;
+        TRY(ensure(vec, wb + 2 * tb));
+        char *vb = (char *)vec.p;
+        if (w) TRY(h2d_rows(vb, w, 1, wb, wb));
+        if (rope != INV_ROPE_NONE) {
+            TRY(h2d_rows(vb + wb, ct, 1, tb, tb));
+            TRY(h2d_rows(vb + wb + tb, st, 1, tb, tb));
+        }
+        wd = w ? (const float *)vb : nullptr;
+        cd = (const float *)(vb + wb);
+        sd = (const float *)(vb + wb + tb);
+    } else if (!aligned(X, 8) || (w && !aligned(w, 4)) || (ct && !aligned(ct, 4)) || (st && !aligned(st, 4))) {
+        return fail(INV_ERR_ARG, "attention: device Q/K must be 8-byte and the norm/rotary vectors 4-byte aligned");
+    }
+    TRY(ensure(dst, (size_t)(seq * cols) * 2));
+    TRY(launch_head_norm_rope(const_cast<float *>(src), (uint16_t *)dst.p, seq * nh, nh, D, wd, rope, cd, sd));
+    *out = (const uint16_t *)dst.p;
+    *out_ld = cols;
+    return INV_OK;
+}
+
 // Query-key pairs an attention call evaluates: all of them, or (causal) key j
 // <= i + offset for query i, offset = seq_k - seq_q.
 double attention_pairs(int64_t sq, int64_t sk, bool causal) {
@@ -974,7 +1049,7 @@ double attention_pairs(int64_t sq, int64_t sk, bool causal) {
 
 int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_dtype, int out_dtype, int64_t heads,
                    int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t head_dim, float scale,
-                   const int32_t *key_mask, int flags) {
+                   const int32_t *key_mask, int flags, const QkPrep *prep = nullptr) {
     TRY(check_init());
     if (in_dtype != INV_DT_F32 && in_dtype != INV_DT_BF16) return fail(INV_ERR_ARG, "attention: bad in_dtype %d", in_dtype);
     if (out_dtype != INV_DT_F32 && out_dtype != INV_DT_BF16)
@@ -1009,8 +1084,20 @@ int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_
     // the device), V transposed to [kv_heads*head_dim x ldv] with zero keys up to ldv.
     const uint16_t *Qd = nullptr, *Kd = nullptr, *Vt = nullptr;
     int64_t ldq = 0, ldk = 0, ldvt = 0;
-    TRY(stage_operand(Q, in_dtype, dev, false, seq_q, hq, hq, 1, 0, 8, g.aq, g.aqin, &Qd, &ldq));
-    TRY(stage_operand(K, in_dtype, dev, false, seq_k, hk, hk, 1, 0, 8, g.ak, g.akin, &Kd, &ldk));
+    if (prep) {
+        if (in_dtype != INV_DT_F32) return fail(INV_ERR_ARG, "attention: the Q/K norm and rotary need fp32 Q and K");
+        if (prep->rope != INV_ROPE_NONE && prep->rope != INV_ROPE_INTERLEAVED && prep->rope != INV_ROPE_HALF)
+            return fail(INV_ERR_ARG, "attention: bad rope mode %d", prep->rope);
+        if (prep->rope != INV_ROPE_NONE && (!prep->q_cos || !prep->q_sin || !prep->k_cos || !prep->k_sin))
+            return fail(INV_ERR_ARG, "attention: rotary tables are null");
+        TRY(stage_prepped((const float *)Q, dev, seq_q, heads, head_dim, prep->q_w, prep->rope, prep->q_cos,
+                          prep->q_sin, g.aq, g.aqin, g.hvec, &Qd, &ldq));
+        TRY(stage_prepped((const float *)K, dev, seq_k, kv_heads, head_dim, prep->k_w, prep->rope, prep->k_cos,
+                          prep->k_sin, g.ak, g.akin, g.hx, &Kd, &ldk));
+    } else {
+        TRY(stage_operand(Q, in_dtype, dev, false, seq_q, hq, hq, 1, 0, 8, g.aq, g.aqin, &Qd, &ldq));
+        TRY(stage_operand(K, in_dtype, dev, false, seq_k, hk, hk, 1, 0, 8, g.ak, g.akin, &Kd, &ldk));
+    }
     TRY(stage_operand(V, in_dtype, dev, true, hk, seq_k, hk, 1, 0, inv::kAttnBlockK, g.avt, g.avin, &Vt, &ldvt));
     void *Od = O;
     if (!dev) {
@@ -1097,24 +1184,7 @@ int head_norm_rope_impl(float *X, int64_t seq, int64_t heads, int64_t head_dim, 
     } else if (!aligned(X, 8) || (w && !aligned(w, 4)) || (ct && !aligned(ct, 4)) || (st && !aligned(st, 4))) {
         return fail(INV_ERR_ARG, "head_norm_rope: X must be 8-byte and the vectors 4-byte aligned");
     }
-    const dim3 grid((unsigned)((rows + 3) / 4));
-    auto go = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, g.stream, xd, rows, (int)heads, wd, cd, sd, 1e-6f);
-    };
-    using namespace inv;
-#define INV_HNR(EPT)                                                                                      \
-    do {                                                                                                  \
-        if (!wd) {                                                                                        \
-            if (rope == INV_ROPE_INTERLEAVED) go(head_norm_rope<EPT, ROPE_INTERLEAVED, false>);           \
-            else go(head_norm_rope<EPT, ROPE_HALF, false>);                                               \
-        } else if (rope == INV_ROPE_NONE) go(head_norm_rope<EPT, ROPE_NONE, true>);                      \
-        else if (rope == INV_ROPE_INTERLEAVED) go(head_norm_rope<EPT, ROPE_INTERLEAVED, true>);          \
-        else go(head_norm_rope<EPT, ROPE_HALF, true>);                                                    \
-    } while (0)
-    if (head_dim == 128) INV_HNR(2);
-    else INV_HNR(1);
-#undef INV_HNR
-    HIPCHK(hipGetLastError());
+    TRY(launch_head_norm_rope(xd, nullptr, rows, heads, head_dim, wd, rope, cd, sd));
     if (!dev) {
         TRY(d2h_rows(X, xd, 1, xb, xb));
     } else if (!(flags & INV_FLAG_ASYNC)) {
@@ -1335,6 +1405,17 @@ int inv_hip_head_norm_rope(float *X, int64_t seq, int64_t heads, int64_t head_di
                            int rope, const float *cos_table, const float *sin_table, int flags) {
     std::lock_guard<std::mutex> lk(g_mu);
     return head_norm_rope_impl(X, seq, heads, head_dim, norm_weight, rope, cos_table, sin_table, flags);
+}
+
+int inv_hip_attention_qk_norm_rope(const float *Q, const float *K, const float *V, void *O, int out_dtype,
+                                   int64_t heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t head_dim,
+                                   float scale, const float *q_norm_weight, const float *k_norm_weight, int rope,
+                                   const float *q_cos, const float *q_sin, const float *k_cos, const float *k_sin,
+                                   const int32_t *key_mask, int flags) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    const QkPrep prep{q_norm_weight, k_norm_weight, rope, q_cos, q_sin, k_cos, k_sin};
+    return attention_impl(Q, K, V, O, INV_DT_F32, out_dtype, heads, kv_heads, seq_q, seq_k, head_dim, scale, key_mask,
+                          flags, &prep);
 }
 
 int inv_hip_set_sgemm_precision(int mode) {

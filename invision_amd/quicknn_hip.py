@@ -429,6 +429,35 @@ def head_norm_rope(x: np.ndarray, heads: int, head_dim: int, norm_weight: Option
              _ptr(c) if c is not None else None, _ptr(s_) if s_ is not None else None, 0)
 
 
+def attention_qk_norm_rope(Q: np.ndarray, K: np.ndarray, V: np.ndarray, heads: int, head_dim: int,
+                           kv_heads: Optional[int] = None, scale: Optional[float] = None, causal: bool = False,
+                           q_norm_weight: Optional[np.ndarray] = None, k_norm_weight: Optional[np.ndarray] = None,
+                           rope: Optional[str] = None, q_cos=None, q_sin=None, k_cos=None, k_sin=None,
+                           key_mask: Optional[np.ndarray] = None, out_dtype: str = "f32") -> np.ndarray:
+    """Attention on fp32 host Q, K, V with each head's RMSNorm and the rotary
+    embedding of Q and K fused into their staging (inv_hip_attention_qk_norm_rope):
+    the same result as head_norm_rope on Q and K, then attention()."""
+    kv_heads = heads if kv_heads is None else kv_heads
+    Q, K, V = (np.ascontiguousarray(a, dtype=np.float32) for a in (Q, K, V))
+    sq, sk = Q.shape[0], K.shape[0]
+    if Q.shape[1] != heads * head_dim or K.shape[1] != kv_heads * head_dim or V.shape != K.shape:
+        raise ValueError("Q [seq_q x heads*head_dim], K and V [seq_k x kv_heads*head_dim]")
+    vec = lambda a, n: None if a is None else np.ascontiguousarray(np.asarray(a, dtype=np.float32).reshape(-1)[:n])
+    width = head_dim if rope == "interleaved" else head_dim // 2
+    qw, kw = vec(q_norm_weight, head_dim), vec(k_norm_weight, head_dim)
+    qc, qs = (vec(t, sq * width) for t in (q_cos, q_sin)) if rope else (None, None)
+    kc, ks = (vec(t, sk * width) for t in (k_cos, k_sin)) if rope else (None, None)
+    m = _key_mask_host(key_mask, sk)
+    odt, onp = (hip.INV_DT_F32, np.float32) if out_dtype == "f32" else (hip.INV_DT_BF16, np.uint16)
+    O = np.empty((sq, heads * head_dim), dtype=onp)
+    sc = 1.0 / float(np.sqrt(head_dim)) if scale is None else float(scale)
+    p = lambda a: _ptr(a) if a is not None else None
+    hip.call("inv_hip_attention_qk_norm_rope", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), odt, heads, kv_heads, sq, sk,
+             head_dim, sc, p(qw), p(kw), _ROPE[rope], p(qc), p(qs), p(kc), p(ks), p(m),
+             hip.INV_ATTN_CAUSAL if causal else 0)
+    return O
+
+
 def QNNQKRMSNorm(Q: np.ndarray, K: np.ndarray, QWeights: np.ndarray, KWeights: np.ndarray, seq: int, heads: int,
                  headDim: int) -> None:
     """TQNNSingleOPS.QNNQKRMSNorm (src/quicknncpu.pas:2209-2246), in place."""

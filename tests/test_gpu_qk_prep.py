@@ -122,3 +122,32 @@ def test_head_norm_rope_argument_errors(hiplib):
     assert lib.inv_hip_head_norm_rope(x.ctypes.data, 4, 2, 64, None, 7, c.ctypes.data, c.ctypes.data, 0) == \
         hip.INV_ERR_ARG and "rope mode" in hip.last_error()
     assert lib.inv_hip_head_norm_rope(x.ctypes.data, 4, 2, 64, None, 0, None, None, 0) == hip.INV_OK  # nothing to do
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads,kv_heads,sq,sk,d,mode,causal", [
+    (24, 24, 300, 428, 128, "interleaved", False),   # FLUX2-like joint: image queries over text + image keys
+    (32, 8, 257, 257, 128, "half", True),            # Qwen3: grouped kv heads, causal
+    (4, 2, 70, 90, 64, "interleaved", True),
+])
+def test_fused_qk_prep_attention_equals_the_two_steps(hiplib, heads, kv_heads, sq, sk, d, mode, causal):
+    """One call (norm + rotary applied while Q and K are staged) gives bit for bit
+    what head_norm_rope on Q and K followed by attention gives, and matches the
+    oracle's norm -> rotary -> attention chain."""
+    import math
+    Q, wq, qc, qs = gen(97, sq, heads, d, mode)
+    K, wk, kc, ks = gen(98, sk, kv_heads, d, mode)
+    V, _, _, _ = gen(99, sk, kv_heads, d, mode)
+    fused = q.attention_qk_norm_rope(Q, K, V, heads, d, kv_heads, causal=causal, q_norm_weight=wq,
+                                     k_norm_weight=wk, rope=mode, q_cos=qc, q_sin=qs, k_cos=kc, k_sin=ks)
+    Qs, Ks = Q.copy(), K.copy()
+    q.head_norm_rope(Qs, heads, d, wq, mode, qc, qs)
+    q.head_norm_rope(Ks, kv_heads, d, wk, mode, kc, ks)
+    two = q.attention(Qs, Ks, V, heads=heads, head_dim=d, kv_heads=kv_heads, causal=causal)
+    np.testing.assert_array_equal(fused, two)
+    Qo = reference(Q, wq, qc, qs, heads, d, mode)
+    Ko = reference(K, wk, kc, ks, kv_heads, d, mode)
+    from invision_amd.bf16 import round_bf16
+    r64 = oracle.attention_f64(round_bf16(Qo), round_bf16(Ko), round_bf16(V), heads, kv_heads, d, 1.0 / math.sqrt(d),
+                               causal)
+    assert oracle.normwise_err(fused, r64) <= 4e-3
