@@ -68,7 +68,12 @@ ATTN_WORKLOADS = {
                         4608, 128, False),
     "zimage_attention": ("Z-Image block attention, 4096 tokens", 30, 30, 4096, 4096, 128, False),
     "qwen3_prefill_attention": ("Qwen3-4B causal grouped-query attention, 512 tokens", 32, 8, 512, 512, 128, True),
+    # fp32 Q, K, V from the projections; each head's RMSNorm and the interleaved rotary
+    # embedding of Q and K applied while they are staged (inv_hip_attention_qk_norm_rope)
+    "flux2_qk_norm_rope_attention": ("FLUX2-Klein-4B QK norm + RoPE + joint attention, fp32 Q/K/V in", 24, 24, 4608,
+                                     4608, 128, False),
 }
+ATTN_PREP = {"flux2_qk_norm_rope_attention"}
 
 
 def log(*a):
@@ -268,13 +273,27 @@ def run_attention(name, steps, warmup_seconds=0.5, check=True):
     desc, heads, kvh, sq, sk, d, causal = ATTN_WORKLOADS[name]
     log(f"[bench] {name}: {desc} heads={heads} kv_heads={kvh} seq_q={sq} seq_k={sk} head_dim={d} causal={causal}")
     rng = np.random.default_rng(2)
-    Q, K, V = (as_bf16_bits(rng.standard_normal(sh, dtype=np.float32))
-               for sh in ((sq, heads * d), (sk, kvh * d), (sk, kvh * d)))
-    qd, kd, vd = (q.DeviceArray.from_host(a, "bf16") for a in (Q, K, V))
+    prep = name in ATTN_PREP
+    Qf, Kf, Vf = (rng.standard_normal(sh, dtype=np.float32) for sh in ((sq, heads * d), (sk, kvh * d), (sk, kvh * d)))
+    if prep:
+        wq, wk = (np.float32(1.0) + np.float32(0.1) * rng.standard_normal(d, dtype=np.float32) for _ in range(2))
+        th = rng.uniform(-np.pi, np.pi, (max(sq, sk), d // 2)).repeat(2, axis=1)  # pairs share an angle
+        cos_t, sin_t = np.cos(th).astype(np.float32), np.sin(th).astype(np.float32)
+        qd, kd, vd, wqd, wkd, cd, sd = (q.DeviceArray.from_host(a, "f32") for a in (Qf, Kf, Vf, wq, wk, cos_t, sin_t))
+        Q, K, V = Qf, Kf, Vf
+    else:
+        Q, K, V = (as_bf16_bits(a) for a in (Qf, Kf, Vf))
+        qd, kd, vd = (q.DeviceArray.from_host(a, "bf16") for a in (Q, K, V))
     od = q.DeviceArray((sq, heads * d), "bf16")
 
     def launch():
-        q.attention_device(qd, kd, vd, od, heads=heads, head_dim=d, kv_heads=kvh, causal=causal, asynchronous=True)
+        if prep:
+            hip.call("inv_hip_attention_qk_norm_rope", qd.ptr, kd.ptr, vd.ptr, od.ptr, hip.INV_DT_BF16, heads, kvh,
+                     sq, sk, d, 1.0 / float(np.sqrt(d)), wqd.ptr, wkd.ptr, hip.INV_ROPE_INTERLEAVED, cd.ptr, sd.ptr,
+                     cd.ptr, sd.ptr, None, hip.INV_FLAG_DEVICE_PTRS | hip.INV_FLAG_ASYNC)
+        else:
+            q.attention_device(qd, kd, vd, od, heads=heads, head_dim=d, kv_heads=kvh, causal=causal,
+                               asynchronous=True)
 
     warm, tw = 0, time.perf_counter()
     while warm < 3 or time.perf_counter() - tw < warmup_seconds:
@@ -300,16 +319,29 @@ def run_attention(name, steps, warmup_seconds=0.5, check=True):
         # fp64 spot check of a few query rows of head 0 (numpy, independent of the oracle)
         O = bf16_bits_to_f32(od.to_host())
         rows = np.unique(np.linspace(0, sq - 1, num=min(sq, 4)).astype(int))
-        qh = bf16_bits_to_f32(Q)[rows, :d].astype(np.float64)
-        kh = bf16_bits_to_f32(K)[:, :d].astype(np.float64)
-        vh = bf16_bits_to_f32(V)[:, :d].astype(np.float64)
+        if prep:
+            def norm_rope(x, w, tok):  # head 0: RMSNorm over d, then pairs (2k, 2k+1) rotated
+                x = x.astype(np.float64)
+                x = x / np.sqrt((x ** 2).mean(1, keepdims=True) + 1e-6) * w
+                c, s_ = cos_t[tok].astype(np.float64), sin_t[tok].astype(np.float64)
+                y = np.empty_like(x)
+                y[:, 0::2] = x[:, 0::2] * c[:, 0::2] - x[:, 1::2] * s_[:, 0::2]
+                y[:, 1::2] = x[:, 1::2] * c[:, 0::2] + x[:, 0::2] * s_[:, 0::2]
+                return y
+            qh = norm_rope(Qf[rows, :d], wq, rows)
+            kh = norm_rope(Kf[:, :d], wk, np.arange(sk))
+            vh = Vf[:, :d].astype(np.float64)
+        else:
+            qh = bf16_bits_to_f32(Q)[rows, :d].astype(np.float64)
+            kh = bf16_bits_to_f32(K)[:, :d].astype(np.float64)
+            vh = bf16_bits_to_f32(V)[:, :d].astype(np.float64)
         S = qh @ kh.T / math.sqrt(d)
         if causal:
             S[np.arange(sk)[None, :] > rows[:, None] + (sk - sq)] = -np.inf
         P = np.exp(S - S.max(1, keepdims=True))
         ref = (P / P.sum(1, keepdims=True)) @ vh
         res["parity_normwise_sampled_rows"] = float(np.max(np.abs(O[rows, :d] - ref)) / np.max(np.abs(ref)))
-    for a in (qd, kd, vd, od):
+    for a in (qd, kd, vd, od) + ((wqd, wkd, cd, sd) if prep else ()):
         a.free()
     return res
 
