@@ -288,9 +288,9 @@ def run_attention(name, steps, warmup_seconds=0.5, check=True):
 
     def launch():
         if prep:
-            hip.call("inv_hip_attention_qk_norm_rope", qd.ptr, kd.ptr, vd.ptr, od.ptr, hip.INV_DT_BF16, heads, kvh,
-                     sq, sk, d, 1.0 / float(np.sqrt(d)), wqd.ptr, wkd.ptr, hip.INV_ROPE_INTERLEAVED, cd.ptr, sd.ptr,
-                     cd.ptr, sd.ptr, None, hip.INV_FLAG_DEVICE_PTRS | hip.INV_FLAG_ASYNC)
+            hip.call("inv_hip_attention_qk_norm_rope", qd.ptr, 0, kd.ptr, 0, vd.ptr, 0, od.ptr, hip.INV_DT_BF16,
+                     heads, kvh, sq, sk, d, 1.0 / float(np.sqrt(d)), wqd.ptr, wkd.ptr, hip.INV_ROPE_INTERLEAVED,
+                     cd.ptr, sd.ptr, cd.ptr, sd.ptr, None, hip.INV_FLAG_DEVICE_PTRS | hip.INV_FLAG_ASYNC)
         else:
             q.attention_device(qd, kd, vd, od, heads=heads, head_dim=d, kv_heads=kvh, causal=causal,
                                asynchronous=True)
@@ -344,6 +344,69 @@ def run_attention(name, steps, warmup_seconds=0.5, check=True):
     for a in (qd, kd, vd, od) + ((wqd, wkd, cd, sd) if prep else ()):
         a.free()
     return res
+
+
+def run_block(steps, warmup_seconds=0.5):
+    """A FLUX2-Klein-4B double block's image stream at 1024x1024 (4608 tokens in the
+    joint attention, 24 heads of 128, MLP 9216), device-resident, in the
+    reference's order (src/quicknn_transformers.pas:1400-1460): AdaLN + QKV
+    projection (one GEMM), QK norm + RoPE + attention (one call), gated output
+    projection, AdaLN + SwiGLU gate/up (one GEMM), gated down projection.
+    FLOP: the five GEMMs' 2*M*N*K plus attention's 4*seq^2*D*heads."""
+    import ctypes
+    from invision_amd import hip
+    from invision_amd import quicknn_hip as q
+    S, H, heads, D, F = 4608, 3072, 24, 128, 9216
+    log(f"[bench] flux2_double_block_image_stream: tokens={S} hidden={H} heads={heads} mlp={F}")
+    rng = np.random.default_rng(3)
+    bf = lambda shape: (rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02))
+    wqkv = q.Weight(bf((3 * H, H)))
+    wo = q.Weight(bf((H, H)), rng.standard_normal(H, dtype=np.float32) * np.float32(0.01))
+    wgu = q.Weight.gate_up(q.as_bf16_bits(bf((F, H))), q.as_bf16_bits(bf((F, H))))
+    wd = q.Weight(bf((H, F)), rng.standard_normal(H, dtype=np.float32) * np.float32(0.01))
+    vec = lambda n, s: q.DeviceArray.from_host((rng.standard_normal(n, dtype=np.float32) * np.float32(s)), "f32")
+    x = q.DeviceArray.from_host(rng.standard_normal((S, H), dtype=np.float32), "f32")
+    sh1, sc1, g1, sh2, sc2, g2 = (vec(H, 0.1) for _ in range(6))
+    qw, kw = (q.DeviceArray.from_host(np.ones(D, np.float32) + rng.standard_normal(D, dtype=np.float32) * np.float32(0.1),
+                                      "f32") for _ in range(2))
+    th = rng.uniform(-np.pi, np.pi, (S, D // 2)).repeat(2, axis=1)
+    ct, st = (q.DeviceArray.from_host(f(th).astype(np.float32), "f32") for f in (np.cos, np.sin))
+    qkv = q.DeviceArray((S, 3 * H), "f32")
+    attn = q.DeviceArray((S, H), "bf16")
+    h = q.DeviceArray((S, F), "bf16")
+    dev = hip.INV_FLAG_DEVICE_PTRS | hip.INV_FLAG_ASYNC
+
+    def block():
+        hip.call("inv_hip_linear_norm", x.ptr, hip.INV_NORM_ADALN, sc1.ptr, sh1.ptr, q.EPSILON, wqkv.handle, None,
+                 qkv.ptr, hip.INV_DT_F32, S, H, 3 * H, hip.INV_EPI_NONE, dev)
+        # Q, K and V read in place from the thirds of the fused projection (token stride 3H)
+        hip.call("inv_hip_attention_qk_norm_rope", qkv.ptr, 3 * H, qkv.ptr + H * 4, 3 * H, qkv.ptr + 2 * H * 4, 3 * H,
+                 attn.ptr, hip.INV_DT_BF16, heads, heads, S, S, D, 1.0 / float(np.sqrt(D)), qw.ptr, kw.ptr,
+                 hip.INV_ROPE_INTERLEAVED, ct.ptr, st.ptr, ct.ptr, st.ptr, None, dev)
+        hip.call("inv_hip_linear_gated_add", attn.ptr, hip.INV_DT_BF16, wo.handle, None, g1.ptr, x.ptr, S, H, H, dev)
+        hip.call("inv_hip_linear_norm", x.ptr, hip.INV_NORM_ADALN, sc2.ptr, sh2.ptr, q.EPSILON, wgu.handle, None, h.ptr,
+                 hip.INV_DT_BF16, S, H, F, hip.INV_EPI_SWIGLU, dev)
+        hip.call("inv_hip_linear_gated_add", h.ptr, hip.INV_DT_BF16, wd.handle, None, g2.ptr, x.ptr, S, F, H, dev)
+
+    warm, tw = 0, time.perf_counter()
+    while warm < 3 or time.perf_counter() - tw < warmup_seconds:
+        block()
+        warm += 1
+        hip.call("inv_hip_synchronize")
+    ms = ctypes.c_float()
+    hip.call("inv_hip_timer_start")
+    for _ in range(steps):
+        block()
+    hip.call("inv_hip_timer_stop", ctypes.byref(ms))
+    t = ms.value / steps
+    gemm = 2.0 * S * H * (3 * H) + 2.0 * S * H * H + 2.0 * S * (2 * F) * H + 2.0 * S * H * F
+    flops = gemm + 4.0 * S * S * D * heads
+    for a in (x, sh1, sc1, g1, sh2, sc2, g2, qw, kw, ct, st, qkv, attn, h):
+        a.free()
+    for w in (wqkv, wo, wgu, wd):
+        w.free()
+    return {"name": "flux2_double_block_image_stream", "tokens": S, "hidden": H, "heads": heads, "mlp": F,
+            "warmup_steps": warm, "kernel_ms": t, "gflop": flops / 1e9, "tflops_kernel": flops / (t * 1e-3) / 1e12}
 
 
 def cpu_baseline(name):
@@ -558,6 +621,8 @@ def main():
         for name in ATTN_WORKLOADS:
             r = run_attention(name, max(5, args.steps // 4), warmup_seconds=min(args.warmup_seconds, 0.5))
             log(f"[bench] {json.dumps(r)}")
+        r = run_block(max(5, args.steps // 20), warmup_seconds=min(args.warmup_seconds, 0.5))
+        log(f"[bench] {json.dumps(r)}")
 
     ceiling = None if args.no_mfma_ceiling else mfma_ceiling(res["tflops_kernel"])
     desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[args.workload]

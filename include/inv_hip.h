@@ -262,10 +262,14 @@ int inv_hip_head_norm_rope(float *X, int64_t seq, int64_t heads, int64_t head_di
  * per-token tables for Q (seq_q rows) and K (seq_k rows; for FLUX2's joint
  * attention the text rows then the image rows, like K itself); key_mask as for
  * inv_hip_attention_masked.  Q, K, V fp32 (host or device per
- * INV_FLAG_DEVICE_PTRS); no counterpart in the reference as one call. */
-int inv_hip_attention_qk_norm_rope(const float *Q, const float *K, const float *V, void *O,
-                                   int out_dtype, int64_t heads, int64_t kv_heads, int64_t seq_q,
-                                   int64_t seq_k, int64_t head_dim, float scale,
+ * INV_FLAG_DEVICE_PTRS), each row-major with a token stride ldq/ldk/ldv in
+ * elements (0: packed, heads*head_dim), so the three thirds of a fused QKV
+ * projection's output are read in place (ld = 3*hidden); O is packed.  No
+ * counterpart in the reference as one call. */
+int inv_hip_attention_qk_norm_rope(const float *Q, int64_t ldq, const float *K, int64_t ldk,
+                                   const float *V, int64_t ldv, void *O, int out_dtype, int64_t heads,
+                                   int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t head_dim,
+                                   float scale,
                                    const float *q_norm_weight, const float *k_norm_weight, int rope,
                                    const float *q_cos, const float *q_sin, const float *k_cos,
                                    const float *k_sin, const int32_t *key_mask, int flags);

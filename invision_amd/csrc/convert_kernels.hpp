@@ -242,18 +242,19 @@ __global__ void __launch_bounds__(256) norm_rows_f32_bf16_reg(const float *__res
 // in lane l ^ 1 (interleaved, EPT 1) or in lane l ^ 32 (half).
 enum { ROPE_NONE = 0, ROPE_INTERLEAVED = 1, ROPE_HALF = 2 };
 
-// BF16OUT: the result goes to y [rows x D] as bf16 (nearest-even) instead of
-// back into x, the Q/K operand staging of the fused attention entry.
+// BF16OUT: the result goes to y [rows x D] (packed) as bf16 (nearest-even)
+// instead of back into x, the Q/K operand staging of the fused attention entry.
 template <int EPT, int ROPE, bool NORM, bool BF16OUT = false>
 __global__ void __launch_bounds__(256) head_norm_rope(float *__restrict__ x, int64_t rows, int heads,
                                                       const float *__restrict__ w, const float *__restrict__ ct,
                                                       const float *__restrict__ st, float eps,
-                                                      uint16_t *__restrict__ y = nullptr) {
+                                                      uint16_t *__restrict__ y, int64_t ldx) {
     constexpr int D = 64 * EPT;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;  // the whole wave
     const int lane = threadIdx.x & 63;
-    float *v = x + row * D + EPT * lane;
+    // token row / heads starts ldx floats after the previous one (heads * D: packed)
+    float *v = x + (row / heads) * ldx + (row % heads) * D + EPT * lane;
     float e[EPT];
     if constexpr (EPT == 2) {
         const float2 t = *(const float2 *)v;

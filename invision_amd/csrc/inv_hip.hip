@@ -961,11 +961,12 @@ void release_stream_objects() {
 // none) then the rotary embedding (rope, tables ct/st), in place, or into y as
 // bf16 when y is given.
 int launch_head_norm_rope(float *x, uint16_t *y, int64_t rows, int64_t heads, int64_t head_dim, const float *w,
-                          int rope, const float *ct, const float *st) {
+                          int rope, const float *ct, const float *st, int64_t ldx = 0) {
     if (rows == 0) return INV_OK;
+    if (ldx == 0) ldx = heads * head_dim;
     const dim3 grid((unsigned)((rows + 3) / 4));
     auto go = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, g.stream, x, rows, (int)heads, w, ct, st, 1e-6f, y);
+        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, g.stream, x, rows, (int)heads, w, ct, st, 1e-6f, y, ldx);
     };
     using namespace inv;
 #define INV_HNR(EPT, OB)                                                                                  \
@@ -996,11 +997,12 @@ struct QkPrep {
     const float *q_w, *k_w;  // RMSNorm weights [head_dim] or null
     int rope;                // INV_ROPE_*
     const float *q_cos, *q_sin, *k_cos, *k_sin;  // per-token tables or null
+    int64_t ldq, ldk, ldv;   // token strides of Q, K, V in elements (packed: heads*head_dim)
 };
 
 // fp32 X [seq x nh*D] (host or device) -> norm + rotary -> bf16 [seq x nh*D] in dst.
 // Host X, weight and tables are copied to the device first (vec: scratch for them).
-int stage_prepped(const float *X, bool dev, int64_t seq, int64_t nh, int64_t D, const float *w, int rope,
+int stage_prepped(const float *X, int64_t ldx, bool dev, int64_t seq, int64_t nh, int64_t D, const float *w, int rope,
                   const float *ct, const float *st, Buf &dst, Buf &tmp, Buf &vec, const uint16_t **out,
                   int64_t *out_ld) {
     const int64_t cols = nh * D;
@@ -1010,8 +1012,9 @@ int stage_prepped(const float *X, bool dev, int64_t seq, int64_t nh, int64_t D, 
     const float *wd = w, *cd = ct, *sd = st;
     if (!dev) {
         TRY(ensure(tmp, xb));
-        TRY(h2d_rows(tmp.p, X, 1, xb, xb));
+        TRY(h2d_rows(tmp.p, X, seq, (size_t)cols * 4, (size_t)ldx * 4));
         src = (const float *)tmp.p;
+        ldx = cols;
         TRY(ensure(vec, wb + 2 * tb));
         char *vb = (char *)vec.p;
         if (w) TRY(h2d_rows(vb, w, 1, wb, wb));
@@ -1022,11 +1025,12 @@ int stage_prepped(const float *X, bool dev, int64_t seq, int64_t nh, int64_t D, 
         wd = w ? (const float *)vb : nullptr;
         cd = (const float *)(vb + wb);
         sd = (const float *)(vb + wb + tb);
-    } else if (!aligned(X, 8) || (w && !aligned(w, 4)) || (ct && !aligned(ct, 4)) || (st && !aligned(st, 4))) {
-        return fail(INV_ERR_ARG, "attention: device Q/K must be 8-byte and the norm/rotary vectors 4-byte aligned");
+    } else if (!aligned(X, 8) || ldx % 2 || (w && !aligned(w, 4)) || (ct && !aligned(ct, 4)) || (st && !aligned(st, 4))) {
+        return fail(INV_ERR_ARG, "attention: device Q/K must be 8-byte aligned with an even leading dimension, "
+                                 "the norm/rotary vectors 4-byte aligned");
     }
     TRY(ensure(dst, (size_t)(seq * cols) * 2));
-    TRY(launch_head_norm_rope(const_cast<float *>(src), (uint16_t *)dst.p, seq * nh, nh, D, wd, rope, cd, sd));
+    TRY(launch_head_norm_rope(const_cast<float *>(src), (uint16_t *)dst.p, seq * nh, nh, D, wd, rope, cd, sd, ldx));
     *out = (const uint16_t *)dst.p;
     *out_ld = cols;
     return INV_OK;
@@ -1090,15 +1094,16 @@ int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_
             return fail(INV_ERR_ARG, "attention: bad rope mode %d", prep->rope);
         if (prep->rope != INV_ROPE_NONE && (!prep->q_cos || !prep->q_sin || !prep->k_cos || !prep->k_sin))
             return fail(INV_ERR_ARG, "attention: rotary tables are null");
-        TRY(stage_prepped((const float *)Q, dev, seq_q, heads, head_dim, prep->q_w, prep->rope, prep->q_cos,
-                          prep->q_sin, g.aq, g.aqin, g.hvec, &Qd, &ldq));
-        TRY(stage_prepped((const float *)K, dev, seq_k, kv_heads, head_dim, prep->k_w, prep->rope, prep->k_cos,
-                          prep->k_sin, g.ak, g.akin, g.hx, &Kd, &ldk));
+        TRY(stage_prepped((const float *)Q, prep->ldq, dev, seq_q, heads, head_dim, prep->q_w, prep->rope,
+                          prep->q_cos, prep->q_sin, g.aq, g.aqin, g.hvec, &Qd, &ldq));
+        TRY(stage_prepped((const float *)K, prep->ldk, dev, seq_k, kv_heads, head_dim, prep->k_w, prep->rope,
+                          prep->k_cos, prep->k_sin, g.ak, g.akin, g.hx, &Kd, &ldk));
     } else {
         TRY(stage_operand(Q, in_dtype, dev, false, seq_q, hq, hq, 1, 0, 8, g.aq, g.aqin, &Qd, &ldq));
         TRY(stage_operand(K, in_dtype, dev, false, seq_k, hk, hk, 1, 0, 8, g.ak, g.akin, &Kd, &ldk));
     }
-    TRY(stage_operand(V, in_dtype, dev, true, hk, seq_k, hk, 1, 0, inv::kAttnBlockK, g.avt, g.avin, &Vt, &ldvt));
+    TRY(stage_operand(V, in_dtype, dev, true, hk, seq_k, prep ? prep->ldv : hk, 1, 0, inv::kAttnBlockK, g.avt, g.avin,
+                      &Vt, &ldvt));
     void *Od = O;
     if (!dev) {
         TRY(ensure(g.yout, (size_t)(seq_q * hq) * osz));
@@ -1407,13 +1412,18 @@ int inv_hip_head_norm_rope(float *X, int64_t seq, int64_t heads, int64_t head_di
     return head_norm_rope_impl(X, seq, heads, head_dim, norm_weight, rope, cos_table, sin_table, flags);
 }
 
-int inv_hip_attention_qk_norm_rope(const float *Q, const float *K, const float *V, void *O, int out_dtype,
-                                   int64_t heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k, int64_t head_dim,
-                                   float scale, const float *q_norm_weight, const float *k_norm_weight, int rope,
-                                   const float *q_cos, const float *q_sin, const float *k_cos, const float *k_sin,
-                                   const int32_t *key_mask, int flags) {
+int inv_hip_attention_qk_norm_rope(const float *Q, int64_t ldq, const float *K, int64_t ldk, const float *V,
+                                   int64_t ldv, void *O, int out_dtype, int64_t heads, int64_t kv_heads, int64_t seq_q,
+                                   int64_t seq_k, int64_t head_dim, float scale, const float *q_norm_weight,
+                                   const float *k_norm_weight, int rope, const float *q_cos, const float *q_sin,
+                                   const float *k_cos, const float *k_sin, const int32_t *key_mask, int flags) {
     std::lock_guard<std::mutex> lk(g_mu);
-    const QkPrep prep{q_norm_weight, k_norm_weight, rope, q_cos, q_sin, k_cos, k_sin};
+    const int64_t hq = heads * head_dim, hk = kv_heads * head_dim;
+    ldq = ldq ? ldq : hq;
+    ldk = ldk ? ldk : hk;
+    ldv = ldv ? ldv : hk;
+    if (ldq < hq || ldk < hk || ldv < hk) return fail(INV_ERR_ARG, "attention: a leading dimension is below heads*head_dim");
+    const QkPrep prep{q_norm_weight, k_norm_weight, rope, q_cos, q_sin, k_cos, k_sin, ldq, ldk, ldv};
     return attention_impl(Q, K, V, O, INV_DT_F32, out_dtype, heads, kv_heads, seq_q, seq_k, head_dim, scale, key_mask,
                           flags, &prep);
 }

@@ -83,9 +83,10 @@ _PROTOS = {
                                          c_int64, c_int64, c_int64, c_float, c_void_p, c_int]),
     "inv_hip_head_norm_rope": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int, c_void_p, c_void_p,
                                        c_int]),
-    "inv_hip_attention_qk_norm_rope": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64,
-                                               c_int64, c_int64, c_int64, c_float, c_void_p, c_void_p, c_int,
-                                               c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int]),
+    "inv_hip_attention_qk_norm_rope": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                                               c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_float, c_void_p,
+                                               c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                               c_int]),
     "inv_hip_sgemm": (c_int, [c_int, c_int, c_int, c_int64, c_int64, c_int64, c_float, c_void_p, c_int64, c_void_p,
                               c_int64, c_float, c_void_p, c_int64]),
     "inv_hip_sbgemm": (c_int, [c_int, c_int, c_int, c_int64, c_int64, c_int64, c_float, c_void_p, c_int64, c_void_p,

@@ -452,8 +452,8 @@ def attention_qk_norm_rope(Q: np.ndarray, K: np.ndarray, V: np.ndarray, heads: i
     O = np.empty((sq, heads * head_dim), dtype=onp)
     sc = 1.0 / float(np.sqrt(head_dim)) if scale is None else float(scale)
     p = lambda a: _ptr(a) if a is not None else None
-    hip.call("inv_hip_attention_qk_norm_rope", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), odt, heads, kv_heads, sq, sk,
-             head_dim, sc, p(qw), p(kw), _ROPE[rope], p(qc), p(qs), p(kc), p(ks), p(m),
+    hip.call("inv_hip_attention_qk_norm_rope", _ptr(Q), 0, _ptr(K), 0, _ptr(V), 0, _ptr(O), odt, heads, kv_heads, sq,
+             sk, head_dim, sc, p(qw), p(kw), _ROPE[rope], p(qc), p(qs), p(kc), p(ks), p(m),
              hip.INV_ATTN_CAUSAL if causal else 0)
     return O
 

@@ -151,3 +151,27 @@ def test_fused_qk_prep_attention_equals_the_two_steps(hiplib, heads, kv_heads, s
     r64 = oracle.attention_f64(round_bf16(Qo), round_bf16(Ko), round_bf16(V), heads, kv_heads, d, 1.0 / math.sqrt(d),
                                causal)
     assert oracle.normwise_err(fused, r64) <= 4e-3
+
+
+@pytest.mark.gpu
+def test_fused_attention_reads_a_fused_qkv_in_place(hiplib):
+    """Q, K and V as the three thirds of one [seq x 3*hidden] projection output
+    (token stride 3*hidden) give exactly the packed-operand result."""
+    seq, heads, d = 200, 3, 64
+    hidden = heads * d
+    qkv, wq, c, s = gen(100, seq, 3 * heads, d, "interleaved")
+    wk = wq[::-1].copy()
+    Q, K, V = (np.ascontiguousarray(qkv[:, i * hidden:(i + 1) * hidden]) for i in range(3))
+    packed = q.attention_qk_norm_rope(Q, K, V, heads, d, q_norm_weight=wq, k_norm_weight=wk, rope="interleaved",
+                                      q_cos=c, q_sin=s, k_cos=c, k_sin=s, causal=True)
+    O = np.empty((seq, hidden), np.float32)
+    base = qkv.ctypes.data
+    hip.call("inv_hip_attention_qk_norm_rope", base, 3 * hidden, base + hidden * 4, 3 * hidden, base + 2 * hidden * 4,
+             3 * hidden, O.ctypes.data, hip.INV_DT_F32, heads, heads, seq, seq, d, 1.0 / np.sqrt(d), wq.ctypes.data,
+             wk.ctypes.data, hip.INV_ROPE_INTERLEAVED, c.ctypes.data, s.ctypes.data, c.ctypes.data, s.ctypes.data,
+             None, hip.INV_ATTN_CAUSAL)
+    np.testing.assert_array_equal(O, packed)
+    lib = hip.load()
+    assert lib.inv_hip_attention_qk_norm_rope(base, hidden - 1, base, 0, base, 0, O.ctypes.data, hip.INV_DT_F32,
+                                              heads, heads, seq, seq, d, 0.125, None, None, 0, None, None, None,
+                                              None, None, 0) == hip.INV_ERR_ARG
