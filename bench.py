@@ -347,8 +347,9 @@ def run_attention(name, steps, warmup_seconds=0.5, check=True):
 
 
 def run_block(steps, warmup_seconds=0.5):
-    """A FLUX2-Klein-4B double block's image stream at 1024x1024 (4608 tokens in the
-    joint attention, 24 heads of 128, MLP 9216), device-resident, in the
+    """A FLUX2-Klein-4B double block at 1024x1024 with its text and image streams
+    taken as one 4608-token stream under one weight set (24 heads of 128, MLP
+    9216), device-resident, in the
     reference's order (src/quicknn_transformers.pas:1400-1460): AdaLN + QKV
     projection (one GEMM), QK norm + RoPE + attention (one call), gated output
     projection, AdaLN + SwiGLU gate/up (one GEMM), gated down projection.
