@@ -28,7 +28,13 @@
  *  - QNNFlashAttention and the per-head attention loops
  *    (src/quicknncpu.pas:2763; src/quicknn_transformers.pas:1150-1311) by
  *    inv_hip_attention, and Qwen3's masked causal attention
- *    (src/quicknn_qwen3.pas:727-769) by inv_hip_attention_masked.
+ *    (src/quicknn_qwen3.pas:727-769) by inv_hip_attention_masked;
+ *  - QNNAdaLN / QNNRMSNorm before a projection (src/quicknncpu.pas:3042-3060,
+ *    2159-2198) by inv_hip_linear_norm;
+ *  - the per-head QK RMSNorm and rotary embedding before attention
+ *    (QNNQKRMSNorm + QNNApplyRoPE2D, QNNHeadRSMNorm + QNNApplyRoPE3;
+ *    src/quicknncpu.pas:2209-2246, 2892-2992) by inv_hip_head_norm_rope, or
+ *    fused into attention's operand staging by inv_hip_attention_qk_norm_rope.
  */
 #ifndef INV_HIP_H
 #define INV_HIP_H
