@@ -75,6 +75,14 @@ ATTN_WORKLOADS = {
 }
 ATTN_PREP = {"flux2_qk_norm_rope_attention"}
 
+# VAE convolutions (QNNConv2d): (description, batch, in_ch, out_ch, H, W, kH, kW, stride, padding).
+CONV_WORKLOADS = {
+    "vae_conv3x3_512ch_256px": ("FLUX2 VAE decoder ResNet conv at 256x256, 512 -> 512 channels", 1, 512, 512, 256,
+                                256, 3, 3, 1, 1),
+    "vae_conv3x3_128ch_1024px": ("FLUX2 VAE decoder ResNet conv at 1024x1024, 128 -> 128 channels", 1, 128, 128, 1024,
+                                 1024, 3, 3, 1, 1),
+}
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
@@ -346,6 +354,68 @@ def run_attention(name, steps, warmup_seconds=0.5, check=True):
     return res
 
 
+def run_conv(name, steps, warmup_seconds=0.5, check=True):
+    """inv_hip_conv2d on a device-resident fp32 NCHW image (im2col into the bf16
+    patch matrix, then the GEMM with the per-channel bias); FLOP = 2 * out_ch *
+    outH * outW * in_ch * kH * kW.  The patch matrix is written once per call:
+    outH * outW * round_up(K, 64) * 2 bytes."""
+    import ctypes
+    from invision_amd import hip
+    from invision_amd import quicknn_hip as q
+    from invision_amd.bf16 import round_bf16
+    desc, b, c, oc, H, W, kH, kW, s, p = CONV_WORKLOADS[name]
+    log(f"[bench] {name}: {desc} batch={b} in_ch={c} out_ch={oc} {H}x{W} k={kH}x{kW} stride={s} pad={p}")
+    rng = np.random.default_rng(4)
+    K = c * kH * kW
+    x = rng.standard_normal((b, c, H, W), dtype=np.float32)
+    w = rng.standard_normal((oc, K), dtype=np.float32) * np.float32(1.0 / np.sqrt(K))
+    bias = rng.standard_normal(oc, dtype=np.float32) * np.float32(0.01)
+    _, _, oH, oW = q.QNNConv2DShape(b, oc, H, W, kH, kW, p, s)
+    wt = q.Weight(w, bias)
+    xd = q.DeviceArray.from_host(x, "f32")
+    yd = q.DeviceArray((b, oc, oH, oW), "f32")
+    flags = hip.INV_FLAG_DEVICE_PTRS | hip.INV_FLAG_ASYNC
+
+    def launch():
+        hip.call("inv_hip_conv2d", xd.ptr, wt.handle, None, yd.ptr, c, oc, H, W, kH, kW, s, p, b, flags)
+
+    warm, tw = 0, time.perf_counter()
+    while warm < 3 or time.perf_counter() - tw < warmup_seconds:
+        launch()
+        warm += 1
+        hip.call("inv_hip_synchronize")
+    ms = ctypes.c_float()
+    hip.call("inv_hip_timer_start")
+    for _ in range(steps):
+        launch()
+    hip.call("inv_hip_timer_stop", ctypes.byref(ms))
+    hip.call("inv_hip_synchronize")
+    t = ms.value / steps
+    flops = 2.0 * b * oc * oH * oW * K
+    col_bytes = oH * oW * ((K + 63) // 64 * 64) * 2
+    res = {"name": name, "batch": b, "in_ch": c, "out_ch": oc, "H": H, "W": W, "kH": kH, "kW": kW, "stride": s,
+           "padding": p, "warmup_steps": warm, "kernel_ms": t, "gflop": flops / 1e9,
+           "tflops_kernel": flops / (t * 1e-3) / 1e12, "patch_matrix_bytes": col_bytes}
+    if check:
+        # fp64 spot check of 8 output pixels over every output channel (numpy, independent of the oracle)
+        y = yd.to_host()
+        xb = np.pad(round_bf16(x).astype(np.float64), ((0, 0), (0, 0), (p, p), (p, p)))
+        wr = round_bf16(w).astype(np.float64)
+        pix = np.unique(np.linspace(0, oH * oW - 1, num=8).astype(int))
+        err, top = 0.0, 0.0
+        for pp in pix:
+            oh, ow = divmod(int(pp), oW)
+            patch = xb[0, :, oh * s:oh * s + kH, ow * s:ow * s + kW].reshape(-1)
+            ref = wr @ patch + bias
+            err = max(err, float(np.abs(y[0, :, oh, ow] - ref).max()))
+            top = max(top, float(np.abs(ref).max()))
+        res["parity_normwise_sampled_pixels"] = err / top
+    xd.free()
+    yd.free()
+    wt.free()
+    return res
+
+
 def run_block(steps, warmup_seconds=0.5):
     """A FLUX2-Klein-4B double block at 1024x1024 with its text and image streams
     taken as one 4608-token stream under one weight set (24 heads of 128, MLP
@@ -479,6 +549,8 @@ def profile_run(args):
     log(f"[profile] copy calibration: 5 x copy_words16 of {n} bytes")
     if args.workload in ATTN_WORKLOADS:
         res = run_attention(args.workload, args.steps, warmup_seconds=args.warmup_seconds, check=False)
+    elif args.workload in CONV_WORKLOADS:
+        res = run_conv(args.workload, args.steps, warmup_seconds=args.warmup_seconds, check=False)
     else:
         res = run_workload(args.workload, args.steps, args.warmup, check=False, warmup_seconds=args.warmup_seconds)
     log(f"[profile] {json.dumps(res)}")
@@ -585,7 +657,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10, help="minimum warm-up steps")
     ap.add_argument("--warmup-seconds", type=float, default=1.5,
                     help="minimum seconds of back-to-back warm-up steps before timing")
-    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS),
+    ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS) + sorted(CONV_WORKLOADS),
                     help="GEMM shape for the bench line; attention shapes only with --profile-run")
     ap.add_argument("--all", action="store_true", help="also time every workload shape (stderr)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -608,8 +680,9 @@ def main():
     log(f"[bench] device: {info}")
     if args.profile_run:
         return profile_run(args)
-    if args.workload in ATTN_WORKLOADS:
-        print("the bench line is a GEMM shape; attention shapes run with --all or --profile-run", file=sys.stderr)
+    if args.workload in ATTN_WORKLOADS or args.workload in CONV_WORKLOADS:
+        print("the bench line is a GEMM shape; attention and convolution shapes run with --all or --profile-run",
+              file=sys.stderr)
         return 2
 
     res = run_workload(args.workload, args.steps, args.warmup, host_path=True, warmup_seconds=args.warmup_seconds)
@@ -624,6 +697,9 @@ def main():
             log(f"[bench] {json.dumps(r)}")
         r = run_block(max(5, args.steps // 20), warmup_seconds=min(args.warmup_seconds, 0.5))
         log(f"[bench] {json.dumps(r)}")
+        for name in CONV_WORKLOADS:
+            r = run_conv(name, max(5, args.steps // 20), warmup_seconds=min(args.warmup_seconds, 0.5))
+            log(f"[bench] {json.dumps(r)}")
 
     ceiling = None if args.no_mfma_ceiling else mfma_ceiling(res["tflops_kernel"])
     desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[args.workload]

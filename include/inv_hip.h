@@ -34,7 +34,8 @@
  *  - the per-head QK RMSNorm and rotary embedding before attention
  *    (QNNQKRMSNorm + QNNApplyRoPE2D, QNNHeadRSMNorm + QNNApplyRoPE3;
  *    src/quicknncpu.pas:2209-2246, 2892-2992) by inv_hip_head_norm_rope, or
- *    fused into attention's operand staging by inv_hip_attention_qk_norm_rope.
+ *    fused into attention's operand staging by inv_hip_attention_qk_norm_rope;
+ *  - the VAE's QNNConv2d (src/quicknncpu.pas:1958-2124) by inv_hip_conv2d.
  */
 #ifndef INV_HIP_H
 #define INV_HIP_H
@@ -279,6 +280,23 @@ int inv_hip_attention_qk_norm_rope(const float *Q, int64_t ldq, const float *K, 
                                    const float *q_norm_weight, const float *k_norm_weight, int rope,
                                    const float *q_cos, const float *q_sin, const float *k_cos,
                                    const float *k_sin, const int32_t *key_mask, int flags);
+
+/* ---- convolution (the VAE) ------------------------------------------------ */
+/* TQNNSingleOPS.QNNConv2d (src/quicknncpu.pas:176-177, 1958-2124; reached
+ * through QNNConv2d, src/quicknn_kernels.pas:990-1006, from the VAE's ResNet,
+ * attention, down/up-sampling and in/out convolutions, src/quicknn_vae.pas:
+ * 174-184, 269-310, 402-456, 556-627): dst [batch x out_ch x outH x outW] =
+ * conv(src [batch x in_ch x H x W]) + bias[out_ch], NCHW fp32, zero padding,
+ * outH = (H + 2*padding - kH)/stride + 1 (QNNConv2DShape,
+ * src/quicknn_kernels.pas:984-987), likewise outW.  weight is a handle of the
+ * reference's [out_ch x in_ch*kH*kW] fp32 filter (inv_hip_weight_upload_f32,
+ * N = out_ch, K = in_ch*kH*kW); bias [out_ch] (null: the handle's, if any).
+ * The image is rounded to bf16 (RNE) into a patch matrix and multiplied with
+ * fp32 accumulation.  flags: INV_FLAG_DEVICE_PTRS (src, dst, bias on the
+ * device), INV_FLAG_ASYNC. */
+int inv_hip_conv2d(const float *src, inv_weight_t weight, const float *bias, float *dst, int64_t in_ch,
+                   int64_t out_ch, int64_t H, int64_t W, int64_t kH, int64_t kW, int64_t stride,
+                   int64_t padding, int64_t batch, int flags);
 
 /* ---- the CBLAS slots ------------------------------------------------------ */
 /* Exactly the signature of TQNNSingleOPS.cblas_sgemm (src/quicknncpu.pas:

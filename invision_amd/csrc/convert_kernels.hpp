@@ -8,7 +8,9 @@
 //  * fp32 [R x C] -> bf16 [C x R] (transposed), for the CBLAS slot's
 //    Trans-A / NoTrans-B operands;
 //  * bf16 rows -> bf16 rows (re-pitch / pad) and bf16 transpose, for the bf16
-//    slot and unaligned bf16 activations.
+//    slot and unaligned bf16 activations;
+//  * an fp32 image -> its bf16 convolution patch matrix (im2col), for
+//    inv_hip_conv2d.
 // All are HBM-bound: 6 bytes (fp32 -> bf16) or 4 bytes (bf16) per element.
 #pragma once
 
@@ -409,6 +411,86 @@ __global__ void __launch_bounds__(256) transpose64_to_bf16(const SrcT *__restric
 #pragma unroll
         for (int e = 0; e < 8; ++e) h[e] = tile[(8 * rr + e) * PITCH + oc];
         *(uint4 *)(dst + (c0 + oc) * ldd + r0 + 8 * rr) = pack8(h);
+    }
+}
+
+// The patch matrix of a convolution, pixel-major: col[p][k] = bf16(src[ic][ih][iw])
+// with ih = oh*stride - pad + kr, iw = ow*stride - pad + kc (0 outside the
+// image), for the output pixel p = (oh - oh0)*outW + ow of output rows
+// [oh0, oh0 + npix/outW) and k = (ic*kH + kr)*kW + kc < K; columns K..ldc-1 are
+// zero.  It is the transpose of QNNConv2d's column buffer
+// (src/quicknncpu.pas:2063-2110), so that the GEMM reads both operands with K
+// contiguous.  A 512-thread workgroup makes an (IM2COL_PG * 64)-pixel x 64-k
+// block: wave w gathers k = 64*blockIdx.y + 8w .. +7 for IM2COL_PG groups of 64
+// consecutive pixels (one per lane, so reads along an image row coalesce; every
+// group's loads are issued before the first is used) into an LDS tile, then the
+// block is written out row by row, eight lanes per 128-byte row segment.  src
+// is one image [C x H x W] fp32; ldc % 64 == 0 and col 16-byte aligned; grid
+// (ceil(npix / (64 * IM2COL_PG)), ldc / 64).
+constexpr int IM2COL_PG = 4;
+__global__ void __launch_bounds__(512) im2col_bf16(const float *__restrict__ src, uint16_t *__restrict__ col, int H,
+                                                   int W, int kH, int kW, int stride, int pad, int outW, int oh0,
+                                                   int64_t npix, int K, int64_t ldc) {
+    constexpr int PITCH = 72;  // bf16 per LDS row: 64 + 8, so 16-byte writes of 64 rows spread over the banks
+    constexpr int ROWS = 64 * IM2COL_PG;
+    __shared__ __attribute__((aligned(16))) uint16_t tile[ROWS * PITCH];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t p0 = (int64_t)blockIdx.x * ROWS;
+    const int k0 = (int)blockIdx.y * 64 + wave * 8;
+    float v[IM2COL_PG][8];
+    if (k0 < K) {
+        const int khw = kH * kW;
+        const int ic0 = k0 / khw;
+        const int r0 = k0 - ic0 * khw;
+        const int kr0 = r0 / kW, kc0 = r0 - (r0 / kW) * kW;
+        // the group's first pixel; the others follow by 64 along the row (wrapping to the next rows)
+        const int64_t pl = p0 + lane;
+        int oh = oh0 + (int)(pl / outW), ow = (int)(pl % outW);
+#pragma unroll
+        for (int g = 0; g < IM2COL_PG; ++g) {
+            const bool in = p0 + g * 64 + lane < npix;
+            const int ih0 = oh * stride - pad, iw0 = ow * stride - pad;
+            int ic = ic0, kr = kr0, kc = kc0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int ih = ih0 + kr, iw = iw0 + kc;
+                v[g][e] = (in && k0 + e < K && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
+                              ? src[((int64_t)ic * H + ih) * W + iw]
+                              : 0.0f;
+                if (++kc == kW) {
+                    kc = 0;
+                    if (++kr == kH) {
+                        kr = 0;
+                        ++ic;
+                    }
+                }
+            }
+            ow += 64;
+            while (ow >= outW) {
+                ow -= outW;
+                ++oh;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < IM2COL_PG; ++g)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[g][e] = 0.0f;
+    }
+#pragma unroll
+    for (int g = 0; g < IM2COL_PG; ++g) {
+        uint16_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = bf16_rne(v[g][e]);
+        *(uint4 *)(tile + (g * 64 + lane) * PITCH + wave * 8) = pack8(h);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < IM2COL_PG; ++i) {
+        const int row = i * 64 + (threadIdx.x >> 3), c = threadIdx.x & 7;
+        if (p0 + row < npix)
+            *(uint4 *)(col + (p0 + row) * ldc + (int64_t)blockIdx.y * 64 + c * 8) =
+                *(const uint4 *)(tile + row * PITCH + c * 8);
     }
 }
 

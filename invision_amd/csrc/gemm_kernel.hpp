@@ -70,6 +70,7 @@ struct GemmParams {
     int has_bias, vec_store;
     int nout;             // EPI_SWIGLU: output columns (N = its padded gate+up row count)
     const float *colscale;  // [N] or null: Y = epi(alpha*acc + bias) * colscale[n] (+ beta*C)
+    const float *row_bias;  // [M] or null: added to row m with the bias (staged epilogue only)
     float *partial;       // split/stream-K partial sums (uncached device memory)
     unsigned *counters;   // arrival counters, one per tile, zero between calls (uncached)
 };
@@ -735,13 +736,29 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
 #pragma unroll
         for (int e = 0; e < 4; ++e) sc[e] = (n + e < p.N) ? p.colscale[n + e] : 0.f;
     }
+    // Per-row bias (a convolution's output channel): every row this lane
+    // stores, loaded here so that no load sits among the stores.
+    constexpr int NIT = 32 / RPI;
+    float rb[C::FM][NIT];
+#pragma unroll
+    for (int j = 0; j < C::FM; ++j)
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) rb[j][it] = 0.f;
+    if (SKM != SK_PUBLISH && p.row_bias) {
+#pragma unroll
+        for (int j = 0; j < C::FM; ++j)
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) {
+                const int m = m0 + wm * C::WTM + j * 32 + it * RPI + rsub;
+                rb[j][it] = (m < p.M) ? p.row_bias[m] : 0.f;
+            }
+    }
     // The bias has landed before the first store: a later wait for it would
     // also wait for every store issued before it.
     wait_vmcnt<0>();
     __syncthreads();  // every wave has finished with the ring
 #pragma unroll
     for (int j = 0; j < C::FM; ++j) {
-        constexpr int NIT = 32 / RPI;
         f32x4_t t[NIT];
         const int64_t slot_off = ((int64_t)(wave * C::FM + j) * 32 + rsub) * C::WTN + col;
         if constexpr (SKM == SK_FINISH) {
@@ -789,7 +806,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    v[e] = epilogue_op<EPI>(t[it][e] + bv[e]) * sc[e];
+                    v[e] = epilogue_op<EPI>(t[it][e] + bv[e] + rb[j][it]) * sc[e];
                     if constexpr (BETA) v[e] += p.beta * cv[it][e];
                 }
                 const int64_t off = (int64_t)(mrow + it * RPI) * p.ldy + n;
@@ -804,12 +821,13 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
             }
         } else {
             // edge tiles and unaligned outputs: element-wise bounds
+#pragma unroll
             for (int it = 0; it < NIT; ++it) {
                 const int m = mrow + it * RPI;
                 if (m >= p.M) continue;
                 float v[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = epilogue_op<EPI>(t[it][e] + bv[e]) * sc[e];
+                for (int e = 0; e < 4; ++e) v[e] = epilogue_op<EPI>(t[it][e] + bv[e] + rb[j][it]) * sc[e];
                 if constexpr (BETA) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)

@@ -179,6 +179,7 @@ struct State {
     Buf nvec;                           // normalisation scale/shift vectors from host
     Buf amask;                          // attention key mask from host
     Buf hx, hvec;                       // head norm / rotary: X and the weight + tables from host
+    Buf csrc, ccol, cdst;               // convolution: images from host, patch matrix, output for host
     // Split/stream-K partial sums and arrival counters: uncached device memory
     // (coherent across XCDs without L2 maintenance).  Such memory is never
     // freed once a kernel has read it: outgrown buffers are retired, not freed.
@@ -339,12 +340,13 @@ struct CfgMeta {
     int tn, tm, threads, acc_regs, bk, lds;
     bool reg_staged;  // RsCfg: register-staged main loop
     bool swiglu_ok;   // 256-row tiles over two wave columns with a staged epilogue
+    bool staged_epi;  // epilogue through LDS (the one that adds a per-row bias)
     hipError_t (*launch)(const inv::GemmParams &, int, int, int, hipStream_t);
 };
 #define INV_META(id)                                                                        \
     {INV_CFG_##id::TN,       INV_CFG_##id::TM,  INV_CFG_##id::NTHREADS, INV_CFG_##id::ACC_REGS, \
      INV_CFG_##id::BK,       INV_CFG_##id::LDS_BYTES, INV_CFG_##id::REG_STAGED, INV_CFG_##id::SWIGLU_OK,      \
-     &inv_gemm_launch_##id},
+     INV_CFG_##id::STAGED_EPI, &inv_gemm_launch_##id},
 const CfgMeta kCfg[INV_GEMM_NUM_CONFIGS] = {INV_GEMM_CONFIG_IDS(INV_META)};
 #undef INV_META
 constexpr int kNumCfg = INV_GEMM_NUM_CONFIGS;
@@ -362,6 +364,8 @@ int cfg_occupancy(const CfgMeta &m) { return std::max(1, std::min(2, (160 * 1024
 //  - at least 3/4 of a round of 256x256 tiles: the 256x256 register-staged tile
 //    (configuration 8), whose energy per FLOP is lowest; a partial last round
 //    costs little because the chip clocks up while CUs idle;
+//  - M <= 128 and half a round of 256x128 tiles: configuration 13, whose 128 X
+//    rows cover M (a 256x256 tile would spend half its MFMAs on zero rows);
 //  - else half a round of 256x128 tiles (configuration 13: 256 W rows, 128 X
 //    rows), else half a round of 128x128 tiles (configuration 15, two
 //    workgroups per CU);
@@ -381,6 +385,8 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
         c.cfg = 5;
     } else if (M <= 64) {
         c.cfg = 4;
+    } else if (M <= 128 && tiles_of(13) * 2 >= cus) {
+        c.cfg = 13;  // 128 X rows cover M: a 256-row tile would multiply zeros for half its MFMAs
     } else if (tiles_of(8) * 4 >= (int64_t)cus * 3) {
         c.cfg = 8;
     } else if (tiles_of(13) * 2 >= cus) {
@@ -415,7 +421,7 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
 int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, void *Y, int64_t ldy, int out,
              const float *bias, const float *Cin, int64_t ldc, float alpha, float beta, int64_t M, int64_t N,
              int64_t K, int epi, int64_t w_seg_k = 0, int64_t Kw = -1, int64_t nout = -1,
-             const float *colscale = nullptr) {
+             const float *colscale = nullptr, const float *row_bias = nullptr) {
     if (M == 0 || N == 0) return INV_OK;
     if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return fail(INV_ERR_ARG, "dimension too large");
     if (K % 8 || ldw % 8 || ldx % 8 || !aligned(W, 16) || !aligned(X, 16))
@@ -429,6 +435,8 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
         tc.mode = inv::GRID_TILES;
         if (beta != 0.0f) return fail(INV_ERR_UNSUPPORTED, "SwiGLU epilogue with beta != 0");
     }
+    if (row_bias && (epi == INV_EPI_SWIGLU || !kCfg[tc.cfg].staged_epi))
+        return fail(INV_ERR_UNSUPPORTED, "internal: a per-row bias needs the staged epilogue");
     inv::GemmParams p{};
     p.nout = (int)(nout < 0 ? N : nout);
     p.W = W;
@@ -453,6 +461,7 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
     p.beta = beta;
     p.has_bias = bias != nullptr;
     p.colscale = colscale;
+    p.row_bias = row_bias;
     const size_t esz = (out == inv::OUT_F32) ? 4 : 2;
     p.vec_store = (ldy % 4 == 0) && aligned(Y, 4 * esz) && (bias == nullptr || aligned(bias, 16));
     if (bias && !aligned(bias, 16)) return fail(INV_ERR_ARG, "internal: bias not 16-byte aligned");
@@ -1151,6 +1160,93 @@ int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_
 }
 
 // Per-head RMSNorm and rotary embedding of Q or K in place (fp32).
+// Convolution as a GEMM per image (QNNConv2d, src/quicknncpu.pas:1958-2124):
+// Y[oc][p] = sum_k Wt[oc][k] * col[p][k] + bias[oc], with the patch matrix col
+// built by im2col_bf16 (pixel-major, K contiguous) and the weights as the
+// GEMM's X operand, so the output lands in NCHW order with the bias added per
+// row.  Output rows are taken in chunks whose patch matrix fits kColCap bytes
+// (INV_HIP_CONV_COL_MB overrides it, in MiB).
+constexpr size_t kColCap = (size_t)1 << 30;
+
+int conv2d_impl(const float *src, inv_weight_t Wt, const float *bias, float *dst, int64_t in_ch, int64_t out_ch,
+                int64_t H, int64_t W, int64_t kH, int64_t kW, int64_t stride, int64_t padding, int64_t batch,
+                int flags) {
+    TRY(check_init());
+    if (!valid_weight(Wt)) return fail(INV_ERR_ARG, "conv2d: unknown weight handle");
+    if (flags & ~(INV_FLAG_DEVICE_PTRS | INV_FLAG_ASYNC)) return fail(INV_ERR_ARG, "conv2d: unknown flags 0x%x", flags);
+    if ((flags & INV_FLAG_ASYNC) && !(flags & INV_FLAG_DEVICE_PTRS))
+        return fail(INV_ERR_ARG, "conv2d: ASYNC requires DEVICE_PTRS");
+    if (in_ch <= 0 || out_ch <= 0 || H <= 0 || W <= 0 || kH <= 0 || kW <= 0 || stride <= 0 || padding < 0 || batch < 0)
+        return fail(INV_ERR_ARG, "conv2d: bad shape");
+    const int64_t outH = (H + 2 * padding - kH) / stride + 1, outW = (W + 2 * padding - kW) / stride + 1;
+    if (H + 2 * padding < kH || W + 2 * padding < kW) return fail(INV_ERR_ARG, "conv2d: kernel larger than the padded image");
+    const int64_t K = in_ch * kH * kW;
+    if (Wt->gated || Wt->N != out_ch || Wt->K != K)
+        return fail(INV_ERR_ARG, "conv2d: weight is %lld x %lld, the call needs %lld x %lld (out_ch x in_ch*kH*kW)",
+                    (long long)Wt->N, (long long)Wt->K, (long long)out_ch, (long long)K);
+    const int64_t P = outH * outW, img = in_ch * H * W;
+    if (H > INT32_MAX / 4 || W > INT32_MAX / 4 || kH > 65536 || kW > 65536 || stride > INT32_MAX / 4 ||
+        padding > INT32_MAX / 4 || K > ((int64_t)1 << 21) || img > ((int64_t)1 << 40) || P > INT32_MAX / 2)
+        return fail(INV_ERR_UNSUPPORTED, "conv2d: dimensions too large");
+    if (batch == 0) return INV_OK;
+    if (!src || !dst) return fail(INV_ERR_ARG, "conv2d: src or dst is null");
+    const bool dev = (flags & INV_FLAG_DEVICE_PTRS) != 0;
+    const int64_t ldc = round_up(K, 64);  // patch-matrix row pitch: whole 128-byte segments
+
+    // Bias: explicit argument first, else the handle's.
+    const float *bd = Wt->bias;
+    if (bias) {
+        if (dev && aligned(bias, 4)) {
+            bd = bias;
+        } else {
+            TRY(ensure(g.bias, (size_t)out_ch * 4));
+            if (dev)
+                HIPCHK(hipMemcpyAsync(g.bias.p, bias, (size_t)out_ch * 4, hipMemcpyDeviceToDevice, g.stream));
+            else
+                TRY(h2d_rows(g.bias.p, bias, 1, (size_t)out_ch * 4, (size_t)out_ch * 4));
+            bd = (const float *)g.bias.p;
+        }
+    }
+    const float *sd = src;
+    float *yd = dst;
+    const size_t sbytes = (size_t)(batch * img) * 4, ybytes = (size_t)(batch * out_ch * P) * 4;
+    if (!dev) {
+        TRY(ensure(g.csrc, sbytes));
+        TRY(h2d_rows(g.csrc.p, src, 1, sbytes, sbytes));
+        sd = (const float *)g.csrc.p;
+        TRY(ensure(g.cdst, ybytes));
+        yd = (float *)g.cdst.p;
+    } else if (!aligned(src, 4) || !aligned(dst, 4)) {
+        return fail(INV_ERR_ARG, "conv2d: src and dst must be 4-byte aligned");
+    }
+    const int64_t row_bytes = outW * ldc * 2;
+    const int64_t cap = std::max(1, env_int("INV_HIP_CONV_COL_MB", (int)(kColCap >> 20))) * ((int64_t)1 << 20);
+    const int64_t chunk_rows = std::max<int64_t>(1, std::min<int64_t>(outH, cap / row_bytes));
+    TRY(ensure(g.ccol, (size_t)(chunk_rows * row_bytes)));
+    uint16_t *col = (uint16_t *)g.ccol.p;
+    for (int64_t b = 0; b < batch; ++b) {
+        const float *in_b = sd + b * img;
+        float *out_b = yd + b * out_ch * P;
+        for (int64_t oh0 = 0; oh0 < outH; oh0 += chunk_rows) {
+            const int64_t rows = std::min(chunk_rows, outH - oh0), npix = rows * outW;
+            hipLaunchKernelGGL(inv::im2col_bf16, dim3((unsigned)((npix + 64 * inv::IM2COL_PG - 1) / (64 * inv::IM2COL_PG)), (unsigned)(ldc / 64)), dim3(512),
+                               0, g.stream, in_b, col, (int)H, (int)W, (int)kH, (int)kW, (int)stride, (int)padding,
+                               (int)outW, (int)oh0, npix, (int)K, ldc);
+            HIPCHK(hipGetLastError());
+            // Y[oc][oh0*outW + q] (row pitch P) = Wt[oc] . col[q] + bias[oc]
+            TRY(run_gemm(col, ldc, Wt->w, Wt->ldw, out_b + oh0 * outW, P, inv::OUT_F32, nullptr, nullptr, 0, 1.0f,
+                         0.0f, out_ch, npix, Wt->ldw, INV_EPI_NONE, 0, -1, -1, nullptr, bd));
+        }
+    }
+    g.calls++;
+    if (!dev) {
+        TRY(d2h_rows(dst, yd, 1, ybytes, ybytes));
+    } else if (!(flags & INV_FLAG_ASYNC)) {
+        HIPCHK(hipStreamSynchronize(g.stream));
+    }
+    return INV_OK;
+}
+
 int head_norm_rope_impl(float *X, int64_t seq, int64_t heads, int64_t head_dim, const float *w, int rope,
                         const float *ct, const float *st, int flags) {
     TRY(check_init());
@@ -1252,7 +1348,8 @@ int inv_hip_shutdown(void) {
     for (auto *w : g.weights) free_weight(w);
     g.weights.clear();
     for (Buf *b : {&g.xin, &g.x16, &g.w16, &g.win, &g.yout, &g.cin, &g.bias, &g.gate, &g.aq, &g.ak, &g.avt, &g.aqin,
-                   &g.akin, &g.avin, &g.nvec, &g.amask, &g.hx, &g.hvec}) release(*b);
+                   &g.akin, &g.avin, &g.nvec, &g.amask, &g.hx, &g.hvec, &g.csrc, &g.ccol, &g.cdst})
+        release(*b);
     // g.partial / g.counters (uncached) stay allocated until the process ends.
     release_stream_objects();
     g_copy.stop_all();
@@ -1410,6 +1507,13 @@ int inv_hip_head_norm_rope(float *X, int64_t seq, int64_t heads, int64_t head_di
                            int rope, const float *cos_table, const float *sin_table, int flags) {
     std::lock_guard<std::mutex> lk(g_mu);
     return head_norm_rope_impl(X, seq, heads, head_dim, norm_weight, rope, cos_table, sin_table, flags);
+}
+
+int inv_hip_conv2d(const float *src, inv_weight_t weight, const float *bias, float *dst, int64_t in_ch, int64_t out_ch,
+                   int64_t H, int64_t W, int64_t kH, int64_t kW, int64_t stride, int64_t padding, int64_t batch,
+                   int flags) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return conv2d_impl(src, weight, bias, dst, in_ch, out_ch, H, W, kH, kW, stride, padding, batch, flags);
 }
 
 int inv_hip_attention_qk_norm_rope(const float *Q, int64_t ldq, const float *K, int64_t ldk, const float *V,

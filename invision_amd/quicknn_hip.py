@@ -492,6 +492,69 @@ def QNNHeadRSMNorm(dst: np.ndarray, src: np.ndarray, weight: np.ndarray, seqLen:
     head_norm_rope(dst, numHeads, headDim, weight, seq=seqLen)
 
 
+# ---------------------------------------------------------------------------
+# Convolution (TQNNSingleOPS.QNNConv2d, src/quicknncpu.pas:1958-2124)
+# ---------------------------------------------------------------------------
+
+def QNNConv2DShape(batch: int, filters: int, srcH: int, srcW: int, kH: int, kW: int, padding: int,
+                   stride: int) -> list:
+    """Output dims [batch, filters, outH, outW] (src/quicknn_kernels.pas:984-987)."""
+    return [batch, filters, (srcH + 2 * padding - kH) // stride + 1, (srcW + 2 * padding - kW) // stride + 1]
+
+
+def _conv_weight(weights, out_ch: int, K: int, bias: Optional[np.ndarray] = None) -> Weight:
+    if isinstance(weights, Weight):
+        return weights
+    w = np.ascontiguousarray(weights, dtype=np.float32).reshape(-1)
+    _bound(w.size >= out_ch * K, "ERROR [Conv2D] : weights out of bound")
+    return Weight(w[:out_ch * K].reshape(out_ch, K))
+
+
+def conv2d_device(src: DeviceArray, weight: Weight, dst: DeviceArray, in_ch: int, out_ch: int, H: int, W: int,
+                  kH: int, kW: int, stride: int, padding: int, batch: int = 1, bias: Optional[DeviceArray] = None,
+                  asynchronous: bool = False) -> None:
+    """inv_hip_conv2d on device-resident NCHW fp32 images."""
+    flags = hip.INV_FLAG_DEVICE_PTRS | (hip.INV_FLAG_ASYNC if asynchronous else 0)
+    hip.call("inv_hip_conv2d", src.ptr, weight.handle, bias.ptr if bias is not None else None, dst.ptr, in_ch, out_ch,
+             H, W, kH, kW, stride, padding, batch, flags)
+
+
+def conv2d(src: np.ndarray, weights, bias: Optional[np.ndarray], in_ch: int, out_ch: int, H: int, W: int, kH: int,
+           kW: int, stride: int, padding: int, batch: int = 1) -> np.ndarray:
+    """Host arrays in and out: dst [batch x out_ch x outH x outW] = conv(src) + bias.
+
+    weights: a resident Weight of [out_ch x in_ch*kH*kW] or the host fp32
+    filter (uploaded for this call only)."""
+    dims = QNNConv2DShape(batch, out_ch, H, W, kH, kW, padding, stride)
+    dst = np.empty(dims, dtype=np.float32)
+    QNNConv2d(dst, src, weights, bias, in_ch, out_ch, H, W, kH, kW, stride, padding, batch)
+    return dst
+
+
+def QNNConv2d(dst: np.ndarray, src: np.ndarray, weights, bias: Optional[np.ndarray], in_ch: int, out_ch: int,
+              H: int, W: int, kH: int, kW: int, stride: int, padding: int, batch: int = 1) -> None:
+    """QNNConv2d (src/quicknn_kernels.pas:990-1006 -> src/quicknncpu.pas:1958-2124): NCHW fp32
+    dst = conv(src, weights [out_ch x in_ch*kH*kW]) + bias[out_ch] (bias may be None)."""
+    _check_host(dst, np.float32, "dst")
+    _check_host(src, np.float32, "src")
+    dims = QNNConv2DShape(batch, out_ch, H, W, kH, kW, padding, stride)
+    _bound(all(d > 0 for d in dims[1:]), "ERROR [Conv2D] : empty output")
+    _bound(dst.size >= int(np.prod(dims)), "ERROR [Conv2D] : Incorrect destination size")
+    _bound(src.size >= batch * in_ch * H * W, "ERROR [Conv2D] : source out of bound")
+    b = None
+    if bias is not None:
+        _check_host(bias, np.float32, "bias")
+        _bound(bias.size >= out_ch, "ERROR [Conv2D] : bias out of bound")
+        b = bias
+    w = _conv_weight(weights, out_ch, in_ch * kH * kW)
+    try:
+        hip.call("inv_hip_conv2d", _ptr(src), w.handle, _ptr(b) if b is not None else None, _ptr(dst), in_ch,
+                 out_ch, H, W, kH, kW, stride, padding, batch, 0)
+    finally:
+        if w is not weights:
+            w.free()
+
+
 def set_sgemm_precision(mode: int) -> None:
     """INV_PREC_BF16 / INV_PREC_SPLIT_A / INV_PREC_SPLIT_AB for cblas_gemm."""
     init()

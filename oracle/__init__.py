@@ -28,6 +28,11 @@ How each oracle function is pinned:
     numpy float64 softmax(QK^T)V per head; invariants (constant V, one key,
     equal keys, a vector added to every key, the causal prefix); the restated
     AVX2 softmax against the exact softmax within its polynomial's error.
+  * conv2d (quicknncpu.pas:1958-2124): numpy float64 im2col + matmul (an
+    independent formulation); a 1x1 convolution is the matmul of the filter
+    and the image; a centred delta filter with padding 1 reproduces the image;
+    a 2x2 all-ones filter with stride 2 gives the 2x2 block sums; zero
+    filters give the bias; the output shape is QNNConv2DShape's.
 """
 from __future__ import annotations
 
@@ -97,6 +102,7 @@ def lib() -> ctypes.CDLL:
         L.orc_softmax_qnn.argtypes = [c_void_p, c_int64]
         L.orc_adaln.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64]
         L.orc_rmsnorm_rows.argtypes = [c_void_p, c_void_p, c_void_p, c_int64, c_int64]
+        L.orc_conv2d_f64.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p] + [c_int64] * 9
         for f in (L.orc_rope_interleaved, L.orc_rope_half):
             f.restype = None
             f.argtypes = [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64]
@@ -367,6 +373,26 @@ def sgemm2_ref_nt(A: np.ndarray, B: np.ndarray, alpha: float = 1.0) -> np.ndarra
     C = np.zeros((M, N), dtype=np.float32)
     R.cpp_sgemm(NO_TRANS, TRANS, M, N, K, alpha, _p(A), K, _p(B), K, 0.0, _p(C), N, 0, M)
     return C
+
+
+def conv2d_shape(batch: int, filters: int, H: int, W: int, kH: int, kW: int, padding: int, stride: int):
+    """QNNConv2DShape (quicknn_kernels.pas:984-987)."""
+    return [batch, filters, (H + 2 * padding - kH) // stride + 1, (W + 2 * padding - kW) // stride + 1]
+
+
+def conv2d_f64(src: np.ndarray, weights: np.ndarray, bias, in_ch: int, out_ch: int, H: int, W: int, kH: int,
+               kW: int, stride: int, padding: int, batch: int = 1) -> np.ndarray:
+    """QNNConv2d (quicknncpu.pas:1958-2124) in its direct form, float64 sums:
+    src [batch x in_ch x H x W], weights [out_ch x in_ch*kH*kW], bias [out_ch]
+    or None; returns [batch x out_ch x outH x outW] float64."""
+    x = np.ascontiguousarray(src, dtype=np.float32).reshape(batch, in_ch, H, W)
+    w = np.ascontiguousarray(weights, dtype=np.float32).reshape(out_ch, in_ch * kH * kW)
+    b = np.ascontiguousarray(bias, dtype=np.float32) if bias is not None else None
+    shape = conv2d_shape(batch, out_ch, H, W, kH, kW, padding, stride)
+    y = np.empty(shape, dtype=np.float64)
+    lib().orc_conv2d_f64(_p(x), _p(w), _p(b) if b is not None else None, _p(y), in_ch, out_ch, H, W, kH, kW,
+                         stride, padding, batch)
+    return y
 
 
 def normwise_err(y: np.ndarray, ref: np.ndarray) -> float:

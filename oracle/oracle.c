@@ -692,3 +692,28 @@ void orc_rope_half(float *x, const float *cos_t, const float *sin_t, int64_t seq
             }
         }
 }
+
+/* QNNConv2d's direct form (quicknncpu.pas:2020-2039) in double; the output
+ * channels run over threads. */
+void orc_conv2d_f64(const float *src, const float *w, const float *bias, double *dst, int64_t in_ch,
+                    int64_t out_ch, int64_t H, int64_t W, int64_t kH, int64_t kW, int64_t stride,
+                    int64_t pad, int64_t batch) {
+    const int64_t outH = (H + 2 * pad - kH) / stride + 1, outW = (W + 2 * pad - kW) / stride + 1;
+    for (int64_t b = 0; b < batch; ++b) {
+#pragma omp parallel for schedule(dynamic, 1)
+        for (int64_t oc = 0; oc < out_ch; ++oc)
+            for (int64_t oh = 0; oh < outH; ++oh)
+                for (int64_t ow = 0; ow < outW; ++ow) {
+                    double sum = bias ? (double)bias[oc] : 0.0;
+                    for (int64_t ic = 0; ic < in_ch; ++ic)
+                        for (int64_t kr = 0; kr < kH; ++kr)
+                            for (int64_t kc = 0; kc < kW; ++kc) {
+                                const int64_t ih = oh * stride - pad + kr, iw = ow * stride - pad + kc;
+                                if (ih >= 0 && ih < H && iw >= 0 && iw < W)
+                                    sum += (double)src[((b * in_ch + ic) * H + ih) * W + iw] *
+                                           (double)w[oc * in_ch * kH * kW + (ic * kH + kr) * kW + kc];
+                            }
+                    dst[((b * out_ch + oc) * outH + oh) * outW + ow] = sum;
+                }
+    }
+}

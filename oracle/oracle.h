@@ -103,6 +103,16 @@ void orc_rope_half(float *x, const float *cos_t, const float *sin_t, int64_t seq
 void orc_adaln(float *dst, const float *src, const float *shift, const float *scale, int64_t seq, int64_t hidden);
 void orc_rmsnorm_rows(float *dst, const float *src, const float *weight, int64_t rows, int64_t dim);
 
+/* ---- QNNConv2d (quicknncpu.pas:1958-2124) ---------------------------------- */
+/* The direct convolution the reference states as its loop form
+ * (quicknncpu.pas:2020-2039), accumulated in double: dst[b][oc][oh][ow] =
+ * bias[oc] + sum over ic, kr, kc of src[b][ic][oh*stride - pad + kr][ow*stride
+ * - pad + kc] (zero outside the image) * w[oc][(ic*kH + kr)*kW + kc].  NCHW;
+ * outH/outW as QNNConv2DShape (quicknn_kernels.pas:984-987); bias may be null. */
+void orc_conv2d_f64(const float *src, const float *w, const float *bias, double *dst, int64_t in_ch,
+                    int64_t out_ch, int64_t H, int64_t W, int64_t kH, int64_t kW, int64_t stride,
+                    int64_t pad, int64_t batch);
+
 int orc_has_avx2(void);
 int orc_max_threads(void);
 

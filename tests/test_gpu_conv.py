@@ -1,0 +1,133 @@
+"""inv_hip_conv2d against the oracle's direct convolution (QNNConv2d,
+src/quicknncpu.pas:1958-2124; the VAE's call sites src/quicknn_vae.pas:174-184,
+269-310, 402-456, 556-627).
+
+The library rounds the fp32 image to bf16 (RNE) into its patch matrix; the
+filters here are bf16-exact (as a bf16 checkpoint's are).  Tolerances,
+normwise (max|d| / max|ref|):
+  - 2e-5 against the oracle (float64 sums) on the bf16-rounded image: fp32
+    accumulation order only;
+  - 3e-3 against the oracle on the fp32 image: the single bf16 rounding of the
+    image (1.5e-3 to 2.3e-3 measured on the CPU for these shapes).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from invision_amd import hip
+from invision_amd import quicknn_hip as q
+from invision_amd.bf16 import round_bf16
+
+TOL_BF16 = 2e-5
+TOL_REF = 3e-3
+
+
+def gen(seed, b, c, oc, H, W, kH, kW):
+    oracle.rng_seed(seed)
+    x = oracle.randn_scaled((b, c, H, W), 1.0, False).astype(np.float32)
+    w = oracle.bf16_to_f32(oracle.f32_to_bf16_rne(oracle.randn_scaled((oc, c * kH * kW), 0.05, False)))
+    bias = oracle.randn_scaled((oc,), 0.01, False).astype(np.float32)
+    return x, np.ascontiguousarray(w, dtype=np.float32), bias
+
+
+def check(y, x, w, bias, c, oc, H, W, kH, kW, s, p, b):
+    ref_b = oracle.conv2d_f64(round_bf16(x), w, bias, c, oc, H, W, kH, kW, s, p, b)
+    ref = oracle.conv2d_f64(x, w, bias, c, oc, H, W, kH, kW, s, p, b)
+    assert y.shape == ref.shape
+    e_b, e_r = oracle.normwise_err(y, ref_b), oracle.normwise_err(y, ref)
+    print(f"[conv2d] b{b} c{c} oc{oc} {H}x{W} k{kH}x{kW} s{s} p{p}: {e_b:.3e} (bf16 image), {e_r:.3e} (fp32)")
+    assert e_b <= TOL_BF16 and e_r <= TOL_REF
+
+
+SHAPES = [
+    (1, 3, 64, 32, 32, 3, 3, 1, 1),     # VAE conv_in: 3 channels, K = 27
+    (1, 64, 64, 24, 20, 3, 3, 1, 1),    # ResNet conv
+    (2, 32, 48, 16, 16, 1, 1, 1, 0),    # skip / attention 1x1, batch 2
+    (1, 32, 32, 17, 17, 3, 3, 2, 0),    # downsample: stride 2 on the padded image
+    (1, 64, 3, 32, 32, 3, 3, 1, 1),     # conv_out: 3 output channels (M = 3)
+    (1, 16, 40, 9, 11, 5, 3, 1, 2),     # ragged: kH != kW, odd sizes
+    (1, 128, 128, 48, 40, 3, 3, 1, 1),  # K = 1152
+    (1, 256, 96, 20, 24, 3, 3, 1, 1),   # K = 2304, out_ch not a multiple of 32
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,c,oc,H,W,kH,kW,s,p", SHAPES)
+def test_conv2d_matches_oracle(hiplib, b, c, oc, H, W, kH, kW, s, p):
+    x, w, bias = gen(11, b, c, oc, H, W, kH, kW)
+    with q.Weight(w) as wt:
+        y = q.conv2d(x, wt, bias, c, oc, H, W, kH, kW, s, p, b)
+    check(y, x, w, bias, c, oc, H, W, kH, kW, s, p, b)
+
+
+@pytest.mark.gpu
+def test_conv2d_mirror_and_handle_bias(hiplib):
+    b, c, oc, H, W, kH, kW, s, p = 1, 8, 16, 12, 10, 3, 3, 1, 1
+    x, w, bias = gen(12, b, c, oc, H, W, kH, kW)
+    dims = q.QNNConv2DShape(b, oc, H, W, kH, kW, p, s)
+    dst = np.zeros(dims, np.float32)
+    q.QNNConv2d(dst, x, w, bias, c, oc, H, W, kH, kW, s, p, b)  # host filter, uploaded for the call
+    check(dst, x, w, bias, c, oc, H, W, kH, kW, s, p, b)
+    with q.Weight(w, bias) as wt:  # the handle's bias when the call passes none
+        y = q.conv2d(x, wt, None, c, oc, H, W, kH, kW, s, p, b)
+    np.testing.assert_array_equal(y, dst)
+    y0 = q.conv2d(x, w, None, c, oc, H, W, kH, kW, s, p, b)  # no bias at all
+    check(y0, x, w, None, c, oc, H, W, kH, kW, s, p, b)
+
+
+@pytest.mark.gpu
+def test_conv2d_device_pointers_match_host(hiplib):
+    b, c, oc, H, W, kH, kW, s, p = 2, 16, 24, 14, 18, 3, 3, 1, 1
+    x, w, bias = gen(13, b, c, oc, H, W, kH, kW)
+    dims = q.QNNConv2DShape(b, oc, H, W, kH, kW, p, s)
+    with q.Weight(w) as wt:
+        yh = q.conv2d(x, wt, bias, c, oc, H, W, kH, kW, s, p, b)
+        xd = q.DeviceArray.from_host(x)
+        bd = q.DeviceArray.from_host(bias)
+        yd = q.DeviceArray(tuple(dims), "f32")
+        try:
+            q.conv2d_device(xd, wt, yd, c, oc, H, W, kH, kW, s, p, b, bias=bd)
+            np.testing.assert_array_equal(yd.to_host(), yh)
+        finally:
+            for a in (xd, bd, yd):
+                a.free()
+
+
+@pytest.mark.gpu
+def test_conv2d_row_chunks_match_one_pass(hiplib):
+    # A patch-matrix cap of 1 MiB splits the 64x56 output into bands of rows;
+    # every band is a GEMM over its own pixels, so the result is identical.
+    b, c, oc, H, W, kH, kW, s, p = 1, 32, 40, 64, 56, 3, 3, 1, 1
+    x, w, bias = gen(14, b, c, oc, H, W, kH, kW)
+    with q.Weight(w) as wt:
+        one = q.conv2d(x, wt, bias, c, oc, H, W, kH, kW, s, p, b)
+        os.environ["INV_HIP_CONV_COL_MB"] = "1"
+        try:
+            banded = q.conv2d(x, wt, bias, c, oc, H, W, kH, kW, s, p, b)
+        finally:
+            del os.environ["INV_HIP_CONV_COL_MB"]
+    np.testing.assert_array_equal(banded, one)
+    check(banded, x, w, bias, c, oc, H, W, kH, kW, s, p, b)
+
+
+@pytest.mark.gpu
+def test_conv2d_errors(hiplib):
+    x, w, bias = gen(15, 1, 4, 8, 6, 6, 3, 3)
+    with q.Weight(w) as wt:
+        with pytest.raises(hip.HipError) as e:  # filter is 8 x 36, call asks 8 x 4*1*1
+            q.conv2d(x, wt, bias, 4, 8, 6, 6, 1, 1, 1, 0)
+        assert e.value.code == hip.INV_ERR_ARG
+        with pytest.raises(AssertionError, match="empty output"):  # 7x7 kernel on a 6x6 image, no padding
+            q.conv2d(x, np.zeros((8, 4 * 49), np.float32), None, 4, 8, 6, 6, 7, 7, 1, 0)
+        with pytest.raises(hip.HipError) as e:  # the same through the C-ABI
+            hip.call("inv_hip_conv2d", x.ctypes.data, wt.handle, None, x.ctypes.data, 4, 8, 6, 6, 7, 7, 1, 0, 1, 0)
+        assert e.value.code == hip.INV_ERR_ARG
+        dst = np.zeros((1, 8, 6, 5), np.float32)  # one column short
+        with pytest.raises(AssertionError, match="Incorrect destination size"):
+            q.QNNConv2d(dst, x, wt, bias, 4, 8, 6, 6, 3, 3, 1, 1)
+        with pytest.raises(hip.HipError):
+            hip.call("inv_hip_conv2d", x.ctypes.data, wt.handle, None, dst.ctypes.data, 4, 8, 6, 6, 3, 3, 0, 1, 1, 0)
+        # batch 0 is a no-op
+        hip.call("inv_hip_conv2d", None, wt.handle, None, None, 4, 8, 6, 6, 3, 3, 1, 1, 0, 0)

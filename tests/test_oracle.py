@@ -510,3 +510,94 @@ def test_head_rmsnorm_normalises_each_head():
     np.testing.assert_allclose(got.reshape(seq, heads, d), ref, rtol=1e-5, atol=1e-6)
     whole = oracle.rmsnorm_rows(x, np.tile(w, heads))
     assert np.max(np.abs(whole - got)) > 1e-2
+
+
+# ---------------------------------------------------------- conv2d ----------
+
+def _conv_im2col_f64(x, w, bias, kH, kW, stride, pad):
+    """numpy float64 im2col + matmul: an independent formulation of QNNConv2d."""
+    b, c, H, W = x.shape
+    oc = w.shape[0]
+    outH, outW = (H + 2 * pad - kH) // stride + 1, (W + 2 * pad - kW) // stride + 1
+    xp = np.pad(x.astype(np.float64), ((0, 0), (0, 0), (pad, pad), (pad, pad)))
+    cols = np.empty((b, c, kH, kW, outH, outW))
+    for kr in range(kH):
+        for kc in range(kW):
+            cols[:, :, kr, kc] = xp[:, :, kr:kr + stride * (outH - 1) + 1:stride, kc:kc + stride * (outW - 1) + 1:stride]
+    y = np.einsum("ok,bkp->bop", w.astype(np.float64), cols.reshape(b, c * kH * kW, outH * outW))
+    if bias is not None:
+        y += bias.astype(np.float64)[None, :, None]
+    return y.reshape(b, oc, outH, outW)
+
+
+@pytest.mark.parametrize("b,c,oc,H,W,kH,kW,stride,pad", [
+    (1, 3, 4, 7, 6, 3, 3, 1, 1),
+    (2, 5, 3, 9, 8, 3, 3, 2, 0),
+    (1, 4, 6, 8, 8, 1, 1, 1, 0),
+    (1, 2, 3, 6, 7, 2, 3, 1, 2),
+    (2, 3, 2, 5, 5, 5, 5, 1, 2),
+])
+def test_conv2d_matches_im2col_matmul(b, c, oc, H, W, kH, kW, stride, pad):
+    rng = np.random.default_rng(b * 100 + c * 10 + kH)
+    x = rng.standard_normal((b, c, H, W)).astype(np.float32)
+    w = rng.standard_normal((oc, c * kH * kW)).astype(np.float32)
+    bias = rng.standard_normal(oc).astype(np.float32)
+    y = oracle.conv2d_f64(x, w, bias, c, oc, H, W, kH, kW, stride, pad, b)
+    assert list(y.shape) == oracle.conv2d_shape(b, oc, H, W, kH, kW, pad, stride)
+    np.testing.assert_allclose(y, _conv_im2col_f64(x, w, bias, kH, kW, stride, pad), rtol=1e-12, atol=1e-12)
+
+
+def test_conv2d_pointwise_is_the_filter_matmul():
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((2, 6, 5, 4)).astype(np.float32)
+    w = rng.standard_normal((3, 6)).astype(np.float32)
+    y = oracle.conv2d_f64(x, w, None, 6, 3, 5, 4, 1, 1, 1, 0, 2)
+    ref = np.matmul(w.astype(np.float64), x.astype(np.float64).reshape(2, 6, 20)).reshape(2, 3, 5, 4)
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_conv2d_centred_delta_filter_reproduces_the_image():
+    rng = np.random.default_rng(8)
+    c = 3
+    x = rng.standard_normal((1, c, 6, 5)).astype(np.float32)
+    w = np.zeros((c, c, 3, 3), np.float32)
+    for i in range(c):
+        w[i, i, 1, 1] = 1.0
+    y = oracle.conv2d_f64(x, w.reshape(c, -1), None, c, c, 6, 5, 3, 3, 1, 1, 1)
+    np.testing.assert_array_equal(y, x.astype(np.float64))
+    # shifted delta (kr=0, kc=2): y[oh][ow] = x[oh-1][ow+1], zero outside
+    w[:] = 0
+    w[0, 0, 0, 2] = 1.0
+    y = oracle.conv2d_f64(x[:, :1], w[:1, :1].reshape(1, -1), None, 1, 1, 6, 5, 3, 3, 1, 1, 1)
+    ref = np.zeros((6, 5))
+    ref[1:, :4] = x[0, 0, :5, 1:]
+    np.testing.assert_array_equal(y[0, 0], ref)
+
+
+def test_conv2d_stride2_ones_filter_gives_block_sums():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((1, 1, 8, 6)).astype(np.float32)
+    y = oracle.conv2d_f64(x, np.ones((1, 4), np.float32), None, 1, 1, 8, 6, 2, 2, 2, 0, 1)
+    ref = x.astype(np.float64).reshape(4, 2, 3, 2).sum(axis=(1, 3))
+    np.testing.assert_allclose(y[0, 0], ref, rtol=1e-12, atol=1e-12)
+
+
+def test_conv2d_zero_filter_gives_the_bias():
+    bias = np.array([1.5, -2.0, 0.25], np.float32)
+    y = oracle.conv2d_f64(np.ones((1, 2, 4, 4), np.float32), np.zeros((3, 18), np.float32), bias, 2, 3, 4, 4, 3, 3,
+                          1, 1, 1)
+    np.testing.assert_array_equal(y, np.broadcast_to(bias.astype(np.float64)[None, :, None, None], y.shape))
+
+
+def test_conv2d_checks_catch_planted_mistakes():
+    # A transposed filter (kr <-> kc) or a dropped padding offset must fail the
+    # independent formulation.
+    rng = np.random.default_rng(10)
+    x = rng.standard_normal((1, 2, 6, 6)).astype(np.float32)
+    w = rng.standard_normal((2, 2, 3, 3)).astype(np.float32)
+    good = _conv_im2col_f64(x, w.reshape(2, -1), None, 3, 3, 1, 1)
+    wrong_w = oracle.conv2d_f64(x, w.transpose(0, 1, 3, 2).reshape(2, -1), None, 2, 2, 6, 6, 3, 3, 1, 1, 1)
+    assert np.abs(wrong_w - good).max() > 1e-3
+    wrong_pad = oracle.conv2d_f64(np.pad(x, ((0, 0), (0, 0), (0, 2), (0, 2))), w.reshape(2, -1), None, 2, 2, 8, 8, 3,
+                                  3, 1, 0, 1)
+    assert np.abs(wrong_pad - good).max() > 1e-3
