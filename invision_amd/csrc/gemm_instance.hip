@@ -25,6 +25,13 @@ bool launch_epi(const inv::GemmParams &p, int epi, int out, dim3 grid, dim3 bloc
     } else if (epi == inv::EPI_GELU) {
         if (f32) launch_one<C, inv::EPI_GELU, inv::OUT_F32, MODE>(p, grid, block, s);
         else launch_one<C, inv::EPI_GELU, inv::OUT_BF16, MODE>(p, grid, block, s);
+    } else if (epi == inv::EPI_ROWBIAS) {
+        if constexpr (C::STAGED_EPI) {
+            if (f32) launch_one<C, inv::EPI_ROWBIAS, inv::OUT_F32, MODE>(p, grid, block, s);
+            else launch_one<C, inv::EPI_ROWBIAS, inv::OUT_BF16, MODE>(p, grid, block, s);
+            return true;
+        }
+        return false;
     } else if (epi == inv::EPI_SWIGLU) {
         // only one workgroup per tile, and only where the tile splits into gate | up wave columns
         if constexpr (C::SWIGLU_OK && MODE == inv::GRID_TILES) {

@@ -51,7 +51,9 @@ typedef __attribute__((address_space(3))) char lds_char_t;
 // EPI_SWIGLU: the weight holds gate and up rows interleaved in 128-row blocks
 // (a 256-row tile = 128 gate rows, then the 128 up rows of the same outputs);
 // Y[m][f] = silu(gate + bias) * (up + bias), Y is nout columns wide.
-enum EpiKind { EPI_NONE = 0, EPI_SILU = 1, EPI_GELU = 2, EPI_SWIGLU = 3 };
+// EPI_ROWBIAS: no activation; p.row_bias[m] is added to row m (a convolution's
+// output channel).  Staged epilogue only.
+enum EpiKind { EPI_NONE = 0, EPI_SILU = 1, EPI_GELU = 2, EPI_SWIGLU = 3, EPI_ROWBIAS = 4 };
 enum OutKind { OUT_F32 = 0, OUT_BF16 = 1 };
 
 struct GemmParams {
@@ -70,7 +72,7 @@ struct GemmParams {
     int has_bias, vec_store;
     int nout;             // EPI_SWIGLU: output columns (N = its padded gate+up row count)
     const float *colscale;  // [N] or null: Y = epi(alpha*acc + bias) * colscale[n] (+ beta*C)
-    const float *row_bias;  // [M] or null: added to row m with the bias (staged epilogue only)
+    const float *row_bias;  // EPI_ROWBIAS: [M], added to row m with the bias
     float *partial;       // split/stream-K partial sums (uncached device memory)
     unsigned *counters;   // arrival counters, one per tile, zero between calls (uncached)
 };
@@ -736,23 +738,21 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
 #pragma unroll
         for (int e = 0; e < 4; ++e) sc[e] = (n + e < p.N) ? p.colscale[n + e] : 0.f;
     }
-    // Per-row bias (a convolution's output channel): every row this lane
-    // stores, loaded here so that no load sits among the stores.
+    // EPI_ROWBIAS: the bias of every row this lane stores, loaded here so
+    // that no load sits among the stores.
     constexpr int NIT = 32 / RPI;
-    float rb[C::FM][NIT];
-#pragma unroll
-    for (int j = 0; j < C::FM; ++j)
-#pragma unroll
-        for (int it = 0; it < NIT; ++it) rb[j][it] = 0.f;
-    if (SKM != SK_PUBLISH && p.row_bias) {
+    constexpr bool RB = EPI == EPI_ROWBIAS;
+    float rb[RB ? C::FM : 1][RB ? NIT : 1];
+    if constexpr (RB) {
 #pragma unroll
         for (int j = 0; j < C::FM; ++j)
 #pragma unroll
             for (int it = 0; it < NIT; ++it) {
                 const int m = m0 + wm * C::WTM + j * 32 + it * RPI + rsub;
-                rb[j][it] = (m < p.M) ? p.row_bias[m] : 0.f;
+                rb[j][it] = (SKM != SK_PUBLISH && m < p.M) ? p.row_bias[m] : 0.f;
             }
     }
+
     // The bias has landed before the first store: a later wait for it would
     // also wait for every store issued before it.
     wait_vmcnt<0>();
@@ -792,6 +792,10 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
             for (int it = 0; it < NIT; ++it) *(f32x4_t *)(slot + slot_off + it * RPI * C::WTN) = t[it];
             continue;
         }
+        if constexpr (RB) {
+#pragma unroll
+            for (int it = 0; it < NIT; ++it) t[it] += rb[j][it];
+        }
         const int mrow = m0 + wm * C::WTM + j * 32 + rsub;  // row of it = 0; it adds RPI rows
         if (nvec && mrow + (NIT - 1) * RPI < p.M) {
             // every row of this lane in range, 16-byte aligned: no branches
@@ -806,7 +810,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    v[e] = epilogue_op<EPI>(t[it][e] + bv[e] + rb[j][it]) * sc[e];
+                    v[e] = epilogue_op<EPI>(t[it][e] + bv[e]) * sc[e];
                     if constexpr (BETA) v[e] += p.beta * cv[it][e];
                 }
                 const int64_t off = (int64_t)(mrow + it * RPI) * p.ldy + n;
@@ -821,13 +825,12 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
             }
         } else {
             // edge tiles and unaligned outputs: element-wise bounds
-#pragma unroll
             for (int it = 0; it < NIT; ++it) {
                 const int m = mrow + it * RPI;
                 if (m >= p.M) continue;
                 float v[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = epilogue_op<EPI>(t[it][e] + bv[e] + rb[j][it]) * sc[e];
+                for (int e = 0; e < 4; ++e) v[e] = epilogue_op<EPI>(t[it][e] + bv[e]) * sc[e];
                 if constexpr (BETA) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)

@@ -435,8 +435,8 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
         tc.mode = inv::GRID_TILES;
         if (beta != 0.0f) return fail(INV_ERR_UNSUPPORTED, "SwiGLU epilogue with beta != 0");
     }
-    if (row_bias && (epi == INV_EPI_SWIGLU || !kCfg[tc.cfg].staged_epi))
-        return fail(INV_ERR_UNSUPPORTED, "internal: a per-row bias needs the staged epilogue");
+    if (row_bias && (epi != INV_EPI_NONE || !kCfg[tc.cfg].staged_epi))
+        return fail(INV_ERR_UNSUPPORTED, "internal: a per-row bias needs the staged epilogue and no activation");
     inv::GemmParams p{};
     p.nout = (int)(nout < 0 ? N : nout);
     p.W = W;
@@ -498,7 +498,7 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
         p.counters = (unsigned *)g.counters.p;
     }
     if (g.stats) HIPCHK(hipEventRecord(g.st0, g.stream));
-    HIPCHK(cm.launch(p, epi, out, mode, g.stream));
+    HIPCHK(cm.launch(p, row_bias ? inv::EPI_ROWBIAS : epi, out, mode, g.stream));
     if (g.stats) {
         HIPCHK(hipEventRecord(g.st1, g.stream));
         HIPCHK(hipEventSynchronize(g.st1));
