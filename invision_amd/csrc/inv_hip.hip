@@ -1229,9 +1229,9 @@ int conv2d_impl(const float *src, inv_weight_t Wt, const float *bias, float *dst
         float *out_b = yd + b * out_ch * P;
         for (int64_t oh0 = 0; oh0 < outH; oh0 += chunk_rows) {
             const int64_t rows = std::min(chunk_rows, outH - oh0), npix = rows * outW;
-            hipLaunchKernelGGL(inv::im2col_bf16, dim3((unsigned)((npix + 64 * inv::IM2COL_PG - 1) / (64 * inv::IM2COL_PG)), (unsigned)(ldc / 64)), dim3(512),
-                               0, g.stream, in_b, col, (int)H, (int)W, (int)kH, (int)kW, (int)stride, (int)padding,
-                               (int)outW, (int)oh0, npix, (int)K, ldc);
+            const dim3 grid((unsigned)((npix + 64 * inv::IM2COL_PG - 1) / (64 * inv::IM2COL_PG)), (unsigned)(ldc / 64));
+            hipLaunchKernelGGL(inv::im2col_bf16, grid, dim3(512), 0, g.stream, in_b, col, (int)H, (int)W, (int)kH,
+                               (int)kW, (int)stride, (int)padding, (int)outW, (int)oh0, npix, (int)K, ldc);
             HIPCHK(hipGetLastError());
             // Y[oc][oh0*outW + q] (row pitch P) = Wt[oc] . col[q] + bias[oc]
             TRY(run_gemm(col, ldc, Wt->w, Wt->ldw, out_b + oh0 * outW, P, inv::OUT_F32, nullptr, nullptr, 0, 1.0f,
