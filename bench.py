@@ -75,12 +75,24 @@ ATTN_WORKLOADS = {
 }
 ATTN_PREP = {"flux2_qk_norm_rope_attention"}
 
-# VAE convolutions (QNNConv2d): (description, batch, in_ch, out_ch, H, W, kH, kW, stride, padding).
+# VAE convolutions (QNNConv2d): (description, batch, in_ch, out_ch, H, W, kH, kW, stride, padding).  The
+# decoder of a 1024x1024 image runs at 128, 256, 512 and 1024 pixels with 512, 512, 256 and 128
+# channels (base 128, multipliers 1, 2, 4, 4: src/quicknn_vae.pas:560-627, 934-943).
 CONV_WORKLOADS = {
     "vae_conv3x3_512ch_256px": ("FLUX2 VAE decoder ResNet conv at 256x256, 512 -> 512 channels", 1, 512, 512, 256,
                                 256, 3, 3, 1, 1),
     "vae_conv3x3_128ch_1024px": ("FLUX2 VAE decoder ResNet conv at 1024x1024, 128 -> 128 channels", 1, 128, 128, 1024,
                                  1024, 3, 3, 1, 1),
+    "vae_conv3x3_512ch_128px": ("VAE decoder mid-block ResNet conv at 128x128, 512 -> 512 channels", 1, 512, 512, 128,
+                                128, 3, 3, 1, 1),
+    "vae_conv3x3_256ch_512px": ("VAE decoder ResNet conv at 512x512, 256 -> 256 channels", 1, 256, 256, 512, 512, 3,
+                                3, 1, 1),
+    "vae_conv1x1_512ch_128px": ("VAE mid-block attention q/k/v projection (1x1) at 128x128, 512 channels", 1, 512,
+                                512, 128, 128, 1, 1, 1, 0),
+    "vae_conv1x1_256to128_1024px": ("VAE decoder ResNet skip (1x1) at 1024x1024, 256 -> 128 channels", 1, 256, 128,
+                                    1024, 1024, 1, 1, 1, 0),
+    "vae_conv_out_128to3_1024px": ("VAE decoder conv_out at 1024x1024, 128 -> 3 channels", 1, 128, 3, 1024, 1024, 3,
+                                   3, 1, 1),
 }
 
 

@@ -47,6 +47,9 @@ SHAPES = [
     (2, 32, 48, 16, 16, 1, 1, 1, 0),    # skip / attention 1x1, batch 2
     (1, 32, 32, 17, 17, 3, 3, 2, 0),    # downsample: stride 2 on the padded image
     (1, 64, 3, 32, 32, 3, 3, 1, 1),     # conv_out: 3 output channels (M = 3)
+    (2, 24, 5, 19, 17, 3, 3, 2, 1),     # 5 output channels, stride 2 with padding, batch 2
+    (1, 40, 1, 16, 16, 3, 3, 1, 2),     # one output channel, padding 2
+    (1, 40, 2, 16, 16, 5, 5, 1, 2),     # two output channels, 5x5
     (1, 16, 40, 9, 11, 5, 3, 1, 2),     # ragged: kH != kW, odd sizes
     (1, 128, 128, 48, 40, 3, 3, 1, 1),  # K = 1152
     (1, 256, 96, 20, 24, 3, 3, 1, 1),   # K = 2304, out_ch not a multiple of 32
