@@ -340,6 +340,15 @@ int inv_hip_stats_enable(int enable);
 int inv_hip_stats(int64_t *calls, double *gemm_ms, double *flops);
 int inv_hip_stats_reset(void);
 
+/* ---- the reference's sampler, for synthetic inputs (host only) ----------- */
+/* src/quicknn_sample.pas:212-276: xoshiro256** seeded by SplitMix64
+ * (rng_seed), uniform singles from 53-bit draws (rand), Box-Muller normals
+ * (random_normal).  The stream is per calling thread.  inv_hip_sample_randn draws
+ * n normals in order, each times sigma, rounded to bf16 (RNE, kept as fp32
+ * values) when round_bf16 is non-zero.  Need no device and no inv_hip_init. */
+int inv_hip_sample_seed(uint64_t seed);
+int inv_hip_sample_randn(float *dst, int64_t n, float sigma, int round_bf16);
+
 #ifdef __cplusplus
 }
 #endif

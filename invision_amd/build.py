@@ -46,9 +46,10 @@ def compile_jobs() -> list[tuple[list[str], str]]:
     jobs.append(([HIPCC] + COMMON_FLAGS + inc + ["-c", os.path.join(CSRC, "inv_hip.hip"), "-o", obj], obj))
     obj = os.path.join(BUILD_DIR, "attention.o")
     jobs.append(([HIPCC] + COMMON_FLAGS + inc + ["-c", os.path.join(CSRC, "attention.hip"), "-o", obj], obj))
-    obj = os.path.join(BUILD_DIR, "safetensors.o")  # host code only
-    jobs.append(([HIPCC, "-O2", "-std=c++17", "-fPIC", "-Wall"] + inc + ["-c", os.path.join(CSRC, "safetensors.cpp"),
-                                                                         "-o", obj], obj))
+    for host_src in ("safetensors.cpp", "sample.cpp"):  # host code only
+        obj = os.path.join(BUILD_DIR, host_src.replace(".cpp", ".o"))
+        jobs.append(([HIPCC, "-O2", "-std=c++17", "-fPIC", "-Wall"] + inc + ["-c", os.path.join(CSRC, host_src),
+                                                                             "-o", obj], obj))
     for cfg in range(NUM_GEMM_CONFIGS):
         obj = os.path.join(BUILD_DIR, f"gemm_cfg{cfg}.o")
         jobs.append(([HIPCC] + COMMON_FLAGS + inc + [f"-DINV_CFG_ID={cfg}", "-c",

@@ -106,6 +106,8 @@ _PROTOS = {
     "inv_hip_stats_enable": (c_int, [c_int]),
     "inv_hip_stats": (c_int, [POINTER(c_int64), POINTER(c_double), POINTER(c_double)]),
     "inv_hip_stats_reset": (c_int, []),
+    "inv_hip_sample_seed": (c_int, [ctypes.c_uint64]),
+    "inv_hip_sample_randn": (c_int, [c_void_p, c_int64, c_float, c_int]),
 }
 
 

@@ -49,6 +49,22 @@ def _ptr(a: np.ndarray) -> int:
     return a.ctypes.data
 
 
+def rng_seed(seed: int) -> None:
+    """The reference's rng_seed (src/quicknn_sample.pas:239-251) for this thread's
+    synthetic-input stream (inv_hip_sample_seed; host only, no device needed)."""
+    hip.call("inv_hip_sample_seed", int(seed) & 0xFFFFFFFFFFFFFFFF)
+
+
+def randn(shape, sigma: float = 1.0, round_bf16: bool = False) -> np.ndarray:
+    """prod(shape) normals from this thread's stream in order, times sigma (the
+    reference's randn/random_normal, src/quicknn_sample.pas:261-276), optionally
+    rounded to bf16 values (RNE); float32."""
+    n = int(np.prod(shape))
+    out = np.empty(n, dtype=np.float32)
+    hip.call("inv_hip_sample_randn", _ptr(out), n, float(sigma), 1 if round_bf16 else 0)
+    return out.reshape(shape)
+
+
 def _check_host(a: np.ndarray, dtype, name: str) -> None:
     if not isinstance(a, np.ndarray):
         raise TypeError(f"{name} must be a numpy array")

@@ -328,6 +328,28 @@ def test_c5_zimage_qkv_batched_cfg(hiplib):
     check(y, X, W, b, rows=sample_rows(M, 32))
 
 
+@pytest.mark.parametrize("which", ["out", "mlp_up", "mlp_down"])
+def test_c5_zimage_block_projections_batched_cfg(hiplib, which):
+    """The rest of a Z-Image block's GEMMs over 2 CFG branches (M = 2 x 4608): the attention
+    out-projection [3840 x 3840] and the MLP up [15360 x 3840] / down [3840 x 15360]
+    (src/quicknn_transformers.pas:2272, 2286-2295), with bias, bf16 X, fp32 Y; sampled rows
+    against the oracle plus a bit-for-bit repeat."""
+    M = 2 * 4608
+    K, N = {"out": (3840, 3840), "mlp_up": (3840, 15360), "mlp_down": (15360, 3840)}[which]
+    X, W, b = gen(7, M, K, N)
+    Xb = as_bf16_bits(X)
+    with q.Weight(W, b) as w:
+        xd = q.DeviceArray.from_host(Xb, "bf16")
+        yd = q.DeviceArray((M, N), "f32")
+        q.linear_device(xd, w, yd, M)
+        y = yd.to_host()
+        q.linear_device(xd, w, yd, M)
+        np.testing.assert_array_equal(yd.to_host(), y)
+        xd.free()
+        yd.free()
+    check(y, X, W, b, rows=sample_rows(M, 32))
+
+
 # ------------------------------------------------------------ device pointers
 
 def test_device_pointer_path_matches_host_path(hiplib):
