@@ -340,6 +340,22 @@ int inv_hip_stats_enable(int enable);
 int inv_hip_stats(int64_t *calls, double *gemm_ms, double *flops);
 int inv_hip_stats_reset(void);
 
+/* ---- linear layer without allocation -------------------------------------- */
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): inv_hip_linear with the same arguments, results and
+ * kernels, on device pointers only (flags must hold INV_FLAG_DEVICE_PTRS;
+ * INV_FLAG_ASYNC and INV_FLAG_PRECISE as for inv_hip_linear), that calls no
+ * hipMalloc, hipFree or allocating routine.  Its scratch memory (activations
+ * staged to bf16, a misaligned bias, split-K partial sums and counters) is a
+ * static device array of INV_NOALLOC_SCRATCH_BYTES, one per GPU, kept until
+ * the process ends and shared by every call on that GPU: calls run in order on
+ * the library stream, so they never overlap; work that would need more scratch
+ * returns INV_ERR_UNSUPPORTED (e.g. fp32 activations above 2^25 elements). */
+#define INV_NOALLOC_SCRATCH_BYTES (64u << 20)
+int inv_hip_linear_noalloc(const void *X, int x_dtype, inv_weight_t W, const float *bias, void *Y, int y_dtype,
+                           int64_t M, int64_t K, int64_t N, int epilogue, int flags);
+
 /* ---- the reference's sampler, for synthetic inputs (host only) ----------- */
 /* src/quicknn_sample.pas:212-276: xoshiro256** seeded by SplitMix64
  * (rng_seed), uniform singles from 53-bit draws (rand), Box-Muller normals

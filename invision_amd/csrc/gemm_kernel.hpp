@@ -73,9 +73,28 @@ struct GemmParams {
     int nout;             // EPI_SWIGLU: output columns (N = its padded gate+up row count)
     const float *colscale;  // [N] or null: Y = epi(alpha*acc + bias) * colscale[n] (+ beta*C)
     const float *row_bias;  // EPI_ROWBIAS: [M], added to row m with the bias
-    float *partial;       // split/stream-K partial sums (uncached device memory)
-    unsigned *counters;   // arrival counters, one per tile, zero between calls (uncached)
+    float *partial;       // split/stream-K partial sums
+    unsigned *counters;   // arrival counters, one per tile, zero between calls
+    int ws_cached;        // 0: partial/counters are uncached memory; 1: ordinary (cached) device memory
 };
+
+// A unit's arrival at its shared tile (thread 0, after a barrier that follows
+// every thread's partial stores and their vmcnt drain); returns how many units
+// arrived before it.
+//  Uncached workspace: stores bypass every L2 and are in memory once
+//  acknowledged, and the loads that read them are issued after this atomic
+//  has returned, so a relaxed agent-scope atomic suffices.
+//  Cached workspace: a partial may sit dirty in the writer XCD's L2 while the
+//  reader runs on another XCD, so the arrival is an acquire-release RMW at
+//  agent scope: its release half writes this XCD's L2 back before the
+//  increment (cumulative over the workgroup's stores through the barrier), its
+//  acquire half invalidates this XCD's caches before the last arriver reads
+//  the other units' partials.
+__device__ __forceinline__ unsigned tile_arrive(const GemmParams &p, int tile) {
+    if (p.ws_cached)
+        return __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     uint32_t u = __float_as_uint(f);
@@ -1055,15 +1074,13 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
             // sums every unit's rows in K order and finishes the tile.
             store_tile_staged<C, EPI, OUT, false, SK_PUBLISH, MODE>(p, lds, acc, m0, n0, wn, wm, lane, wave, &fix,
                                                                     unit_slot<MODE, C>(p, fix, fix.my_seg));
-            // Uncached workspace and counters: the stores are in memory once
-            // acknowledged, coherent across XCDs without fences.
+            // The slot stores are acknowledged before the arrival (tile_arrive).
             wait_vmcnt<0>();
             volatile __attribute__((address_space(3))) unsigned *s_last =
                 (volatile __attribute__((address_space(3))) unsigned *)lds;
             __syncthreads();  // every wave's staging reads and slot stores are done
             if (tid == 0) {
-                unsigned prev =
-                    __hip_atomic_fetch_add(&p.counters[fix.tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const unsigned prev = tile_arrive(p, fix.tile);
                 *s_last = (prev == (unsigned)(fix.nseg - 1)) ? 1u : 0u;
             }
             __syncthreads();
@@ -1093,11 +1110,7 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
                                      acc[i][j][4 * g + 3]};
                         *(f32x4_t *)(mine + ((((i * C::FM + j) * 4 + g) * C::NTHREADS + tid) * 4)) = v;
                     }
-            // The workspace and counters are uncached device memory: stores,
-            // loads and atomics go to memory, so they are coherent across XCDs
-            // without agent-scope fences (which would write back and
-            // invalidate this XCD's whole L2).  Publishing the partial needs
-            // only its stores to be acknowledged before the counter moves.
+            // The partial stores are acknowledged before the arrival (tile_arrive).
             wait_vmcnt<0>();
             // The flag lives in the (now idle) ring: the barrier below completes
             // every wave's LDS reads and partial stores before thread 0 acts.
@@ -1105,8 +1118,7 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
                 (volatile __attribute__((address_space(3))) unsigned *)lds;
             __syncthreads();
             if (tid == 0) {
-                unsigned prev =
-                    __hip_atomic_fetch_add(&p.counters[fix.tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const unsigned prev = tile_arrive(p, fix.tile);
                 *s_last = (prev == (unsigned)(fix.nseg - 1)) ? 1u : 0u;
             }
             __syncthreads();

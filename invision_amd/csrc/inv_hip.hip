@@ -190,10 +190,27 @@ struct State {
     int64_t calls = 0;
     double gemm_ms = 0.0, flops = 0.0;
     std::vector<inv_weight_s *> weights;
+    unsigned char *scratch = nullptr;  // device address of `scratch` on g.device
 };
 
 State g;
 std::mutex g_mu;
+
+// The no-allocation entry point's scratch: one array per GPU the library runs
+// on, held until the process ends.  Host code never uses its name as an
+// address (in host code it is a stand-in symbol): g.scratch holds the device
+// address from hipGetSymbolAddress, looked up at inv_hip_init.
+//   [0, kScratchCounters)                split-K arrival counters (u32)
+//   [kScratchCounters, +kScratchBias)     a bias staged to 16-byte alignment
+//   [kScratchCounters + kScratchBias, end)  staged activations, then split-K partial sums
+constexpr size_t kScratchCounters = 64u << 10;
+constexpr size_t kScratchBias = 256u << 10;
+static __device__ __align__(256) unsigned char scratch[INV_NOALLOC_SCRATCH_BYTES];
+
+__global__ void fill_zero_u32(unsigned *p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
 
 }  // namespace
 
@@ -418,10 +435,21 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
 }
 
 // W [N x ldw], X [M x ldx] bf16 device; K a multiple of 8 (zero padded).
+// Caller-provided split-K workspace in ordinary device memory (the
+// no-allocation entry point's scratch): partial sums and arrival counters,
+// the counters zero on entry.
+struct FixedWorkspace {
+    float *partial;
+    size_t partial_bytes;
+    unsigned *counters;
+    size_t counter_bytes;
+};
+
 int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, void *Y, int64_t ldy, int out,
              const float *bias, const float *Cin, int64_t ldc, float alpha, float beta, int64_t M, int64_t N,
              int64_t K, int epi, int64_t w_seg_k = 0, int64_t Kw = -1, int64_t nout = -1,
-             const float *colscale = nullptr, const float *row_bias = nullptr) {
+             const float *colscale = nullptr, const float *row_bias = nullptr,
+             const FixedWorkspace *fixed_ws = nullptr) {
     if (M == 0 || N == 0) return INV_OK;
     if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return fail(INV_ERR_ARG, "dimension too large");
     if (K % 8 || ldw % 8 || ldx % 8 || !aligned(W, 16) || !aligned(X, 16))
@@ -492,10 +520,30 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
     }
     if (mode != inv::GRID_TILES) {
         const int64_t slots = (mode == inv::GRID_SPLITK) ? ntiles * p.ksplit : 2 * (int64_t)p.ksplit;
-        TRY(ensure_uncached(g.partial, (size_t)(slots * cm.threads * cm.acc_regs) * sizeof(float), false));
-        TRY(ensure_uncached(g.counters, (size_t)ntiles * sizeof(unsigned), true));
-        p.partial = (float *)g.partial.p;
-        p.counters = (unsigned *)g.counters.p;
+        const size_t pbytes = (size_t)(slots * cm.threads * cm.acc_regs) * sizeof(float);
+        const size_t cbytes = (size_t)ntiles * sizeof(unsigned);
+        if (fixed_ws) {
+            if (pbytes > fixed_ws->partial_bytes || cbytes > fixed_ws->counter_bytes)
+                return fail(INV_ERR_UNSUPPORTED,
+                            "split-K needs %zu bytes of partial sums and %zu of counters; the no-allocation "
+                            "scratch (%d MiB) has %zu and %zu left", pbytes, cbytes,
+                            (int)(INV_NOALLOC_SCRATCH_BYTES >> 20), fixed_ws->partial_bytes, fixed_ws->counter_bytes);
+            p.partial = fixed_ws->partial;
+            p.counters = fixed_ws->counters;
+            p.ws_cached = 1;
+            // The counters start at zero (a fill kernel, not a memset node, so
+            // the call may be captured into a graph).
+            const int64_t nc = (int64_t)(cbytes / sizeof(unsigned));
+            hipLaunchKernelGGL(fill_zero_u32, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, g.stream, p.counters,
+                               nc);
+            HIPCHK(hipGetLastError());
+        } else {
+            TRY(ensure_uncached(g.partial, pbytes, false));
+            TRY(ensure_uncached(g.counters, cbytes, true));
+            p.partial = (float *)g.partial.p;
+            p.counters = (unsigned *)g.counters.p;
+            p.ws_cached = 0;
+        }
     }
     if (g.stats) HIPCHK(hipEventRecord(g.st0, g.stream));
     HIPCHK(cm.launch(p, row_bias ? inv::EPI_ROWBIAS : epi, out, mode, g.stream));
@@ -833,10 +881,9 @@ int stage_normalized(const char *who, const float *X, const NormArgs &nm, bool d
     return INV_OK;
 }
 
-int linear_impl(const char *who, const void *X, int x_dtype, inv_weight_t W, const float *bias, void *Y, int y_dtype,
-                int64_t M, int64_t K, int64_t N, int epilogue, int flags, bool accumulate, const float *gate,
-                const NormArgs *nm = nullptr) {
-    TRY(check_init());
+// Argument checks shared by the linear entry points (status, no side effects).
+int check_linear_args(const char *who, int x_dtype, inv_weight_t W, int y_dtype, int64_t M, int64_t K, int64_t N,
+                      int epilogue, int flags, bool accumulate, const float *bias) {
     if (!valid_weight(W)) return fail(INV_ERR_ARG, "%s: unknown weight handle", who);
     if (x_dtype != INV_DT_F32 && x_dtype != INV_DT_BF16) return fail(INV_ERR_ARG, "%s: bad x_dtype %d", who, x_dtype);
     if (y_dtype != INV_DT_F32 && y_dtype != INV_DT_BF16) return fail(INV_ERR_ARG, "%s: bad y_dtype %d", who, y_dtype);
@@ -854,9 +901,90 @@ int linear_impl(const char *who, const void *X, int x_dtype, inv_weight_t W, con
         return fail(INV_ERR_ARG, W->gated ? "linear: a gate/up weight needs INV_EPI_SWIGLU"
                                           : "linear: INV_EPI_SWIGLU needs a gate/up weight (inv_hip_weight_upload_gate_up)");
     if (W->gated && bias) return fail(INV_ERR_ARG, "%s: a gate/up weight takes its biases at upload", who);
+    if (M > INT32_MAX / 2) return fail(INV_ERR_ARG, "%s: M too large", who);
+    return INV_OK;
+}
+
+// inv_hip_linear on device pointers with no allocation: activations staged,
+// a misaligned bias copied and split-K partials parked in the library's
+// static scratch array (g.scratch), whose split-K counters are cleared by a
+// fill kernel before each GEMM that uses them.  Everything runs on the
+// library stream, so successive calls never overlap.
+int linear_noalloc_impl(const void *X, int x_dtype, inv_weight_t W, const float *bias, void *Y, int y_dtype,
+                        int64_t M, int64_t K, int64_t N, int epilogue, int flags) {
+    const char *who = "linear_noalloc";
+    TRY(check_init());
+    if (!g.scratch) return fail(INV_ERR_NOT_INIT, "%s: the scratch array has no device address", who);
+    TRY(check_linear_args(who, x_dtype, W, y_dtype, M, K, N, epilogue, flags, false, bias));
+    if (!(flags & INV_FLAG_DEVICE_PTRS))
+        return fail(INV_ERR_ARG, "%s: needs INV_FLAG_DEVICE_PTRS (host pointers would need bounce buffers)", who);
     if (M == 0) return INV_OK;
     if (!X || !Y) return fail(INV_ERR_ARG, "%s: X or Y is null", who);
-    if (M > INT32_MAX / 2) return fail(INV_ERR_ARG, "%s: M too large", who);
+    const int out = (y_dtype == INV_DT_F32) ? inv::OUT_F32 : inv::OUT_BF16;
+    unsigned char *const base = g.scratch;
+    unsigned char *const stage = base + kScratchCounters + kScratchBias;
+    const size_t stage_cap = INV_NOALLOC_SCRATCH_BYTES - kScratchCounters - kScratchBias;
+
+    // Activations: bf16 rows [M x ldx] with K contiguous, zero padded.
+    const bool precise = (flags & INV_FLAG_PRECISE) && x_dtype == INV_DT_F32;
+    const int64_t kseg = precise ? round_up(K, 64) : W->ldw;
+    const uint16_t *Xd = nullptr;
+    int64_t ldx = 0;
+    size_t used = 0;
+    if (x_dtype == INV_DT_BF16 && K == W->ldw && aligned(X, 16)) {
+        Xd = (const uint16_t *)X;
+        ldx = K;
+    } else {
+        ldx = precise ? 2 * kseg : W->ldw;
+        used = (size_t)round_up(M * ldx * 2, 256);
+        if (used > stage_cap)
+            return fail(INV_ERR_UNSUPPORTED, "%s: staging %lld x %lld activations needs %zu bytes, above the %d MiB "
+                        "no-allocation scratch", who, (long long)M, (long long)K, used,
+                        (int)(INV_NOALLOC_SCRATCH_BYTES >> 20));
+        uint16_t *d = (uint16_t *)stage;
+        if (x_dtype == INV_DT_F32) {
+            if (!aligned(X, 4)) return fail(INV_ERR_ARG, "%s: fp32 X not 4-byte aligned", who);
+            TRY(launch_cvt_rows_f32((const float *)X, K, d, ldx, M, K, precise ? kseg : W->ldw, precise ? 2 : 1,
+                                    precise ? 0x2 : 0));
+        } else {
+            if (!aligned(X, 2)) return fail(INV_ERR_ARG, "%s: bf16 X not 2-byte aligned", who);
+            TRY(launch_copy_rows_bf16((const uint16_t *)X, K, d, ldx, M, K, W->ldw));
+        }
+        Xd = d;
+    }
+
+    // Bias: explicit argument first, else the handle's; 16-byte aligned for the epilogue.
+    const float *bd = W->bias;
+    if (bias) {
+        if (aligned(bias, 16)) {
+            bd = bias;
+        } else {
+            if ((size_t)N * 4 > kScratchBias)
+                return fail(INV_ERR_UNSUPPORTED, "%s: a misaligned bias of %lld columns exceeds the scratch's bias "
+                            "area", who, (long long)N);
+            HIPCHK(hipMemcpyAsync(base + kScratchCounters, bias, (size_t)N * 4, hipMemcpyDeviceToDevice, g.stream));
+            bd = (const float *)(base + kScratchCounters);
+        }
+    }
+    const FixedWorkspace ws{(float *)(stage + used), stage_cap - used, (unsigned *)base, kScratchCounters};
+    if (precise)
+        TRY(run_gemm(W->w, W->ldw, Xd, ldx, Y, N, out, bd, nullptr, N, 1.0f, 0.0f, M, W->rows, 2 * kseg, epilogue,
+                     kseg, W->ldw, N, nullptr, nullptr, &ws));
+    else
+        TRY(run_gemm(W->w, W->ldw, Xd, ldx, Y, N, out, bd, nullptr, N, 1.0f, 0.0f, M, W->rows, W->ldw, epilogue, 0,
+                     -1, N, nullptr, nullptr, &ws));
+    g.calls++;
+    if (!(flags & INV_FLAG_ASYNC)) HIPCHK(hipStreamSynchronize(g.stream));
+    return INV_OK;
+}
+
+int linear_impl(const char *who, const void *X, int x_dtype, inv_weight_t W, const float *bias, void *Y, int y_dtype,
+                int64_t M, int64_t K, int64_t N, int epilogue, int flags, bool accumulate, const float *gate,
+                const NormArgs *nm = nullptr) {
+    TRY(check_init());
+    TRY(check_linear_args(who, x_dtype, W, y_dtype, M, K, N, epilogue, flags, accumulate, bias));
+    if (M == 0) return INV_OK;
+    if (!X || !Y) return fail(INV_ERR_ARG, "%s: X or Y is null", who);
     const bool dev = (flags & INV_FLAG_DEVICE_PTRS) != 0;
     const int out = (y_dtype == INV_DT_F32) ? inv::OUT_F32 : inv::OUT_BF16;
     const size_t ysz = (y_dtype == INV_DT_F32) ? 4 : 2;
@@ -1328,6 +1456,16 @@ int inv_hip_init(int device) {
         release_stream_objects();  // a later call may try again from scratch
         return rc;
     }
+    // The device address of this GPU's scratch array (the array's name is a
+    // host-side stand-in, never an address).
+    void *sp = nullptr;
+    const hipError_t se = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+    if (se != hipSuccess || !sp) {
+        (void)hipGetLastError();
+        release_stream_objects();
+        return fail(INV_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(se));
+    }
+    g.scratch = (unsigned char *)sp;
     g.device = device;
     g.cu_count = prop.multiProcessorCount;
     g.clock_khz = prop.clockRate;
@@ -1354,6 +1492,7 @@ int inv_hip_shutdown(void) {
     release_stream_objects();
     g_copy.stop_all();
     g.init = false;
+    g.scratch = nullptr;
     g.device = -1;
     g.stats = false;
     g.calls = 0;
@@ -1465,6 +1604,12 @@ int inv_hip_linear(const void *X, int x_dtype, inv_weight_t W, const float *bias
                    int64_t K, int64_t N, int epilogue, int flags) {
     std::lock_guard<std::mutex> lk(g_mu);
     return linear_impl("linear", X, x_dtype, W, bias, Y, y_dtype, M, K, N, epilogue, flags, false, nullptr);
+}
+
+int inv_hip_linear_noalloc(const void *X, int x_dtype, inv_weight_t W, const float *bias, void *Y, int y_dtype,
+                           int64_t M, int64_t K, int64_t N, int epilogue, int flags) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return linear_noalloc_impl(X, x_dtype, W, bias, Y, y_dtype, M, K, N, epilogue, flags);
 }
 
 int inv_hip_linear_gated_add(const void *X, int x_dtype, inv_weight_t W, const float *bias, const float *gate,

@@ -73,6 +73,8 @@ _PROTOS = {
     "inv_hip_weight_load_safetensors": (c_int, [c_char_p, c_char_p, c_char_p, c_int, POINTER(c_void_p)]),
     "inv_hip_linear": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int64,
                                c_int, c_int]),
+    "inv_hip_linear_noalloc": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64,
+                                       c_int64, c_int, c_int]),
     "inv_hip_linear_gated_add": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
                                          c_int64, c_int]),
     "inv_hip_linear_norm": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_int,
