@@ -20,6 +20,8 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <new>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -201,7 +203,12 @@ class HeaderParser {
             return eat('}');
         }
     }
-    bool skip_value() {
+    // Nesting deeper than this is refused (a header that is only brackets
+    // would otherwise recurse once per byte).
+    static constexpr int kMaxDepth = 64;
+
+    bool skip_value(int depth = 0) {
+        if (depth > kMaxDepth) return false;
         ws();
         char c = peek();
         if (c == '"') {
@@ -221,7 +228,7 @@ class HeaderParser {
                     ws();
                     if (!eat(':')) return false;
                 }
-                if (!skip_value()) return false;
+                if (!skip_value(depth + 1)) return false;
                 ws();
                 if (eat(',')) continue;
                 return eat(close);
@@ -294,14 +301,17 @@ struct MappedFile {
                 return fail(INV_ERR_ARG, "safetensors: tensor \"%s\" lies outside the file (truncated?)", kv.first.c_str());
             const int es = dtype_size(t.dtype);
             if (es) {
-                int64_t count = 1;
+                int64_t count = 1, bytes = 0;
                 for (int64_t d : t.shape) {
                     if (d < 0) return fail(INV_ERR_ARG, "safetensors: tensor \"%s\" has a negative dimension", kv.first.c_str());
-                    count *= d;
+                    if (__builtin_mul_overflow(count, d, &count))
+                        return fail(INV_ERR_ARG, "safetensors: tensor \"%s\": element count overflows", kv.first.c_str());
                 }
-                if (count * es != t.end - t.begin)
+                if (__builtin_mul_overflow(count, (int64_t)es, &bytes))
+                    return fail(INV_ERR_ARG, "safetensors: tensor \"%s\": byte count overflows", kv.first.c_str());
+                if (bytes != t.end - t.begin)
                     return fail(INV_ERR_ARG, "safetensors: tensor \"%s\" holds %lld bytes, its shape needs %lld",
-                                kv.first.c_str(), (long long)(t.end - t.begin), (long long)(count * es));
+                                kv.first.c_str(), (long long)(t.end - t.begin), (long long)bytes);
             }
         }
         if (map_data) {
@@ -367,8 +377,8 @@ std::vector<float> to_f32(const uint8_t *src, const std::string &dtype, int64_t 
 
 }  // namespace
 
-extern "C" int inv_hip_safetensors_info(const char *path, const char *name, int *dtype, int *ndim, int64_t *shape,
-                                        int64_t *data_offset) {
+static int safetensors_info_impl(const char *path, const char *name, int *dtype, int *ndim, int64_t *shape,
+                          int64_t *data_offset) {
     MappedFile f;
     int rc = f.open_file(path, false);
     if (rc != INV_OK) return rc;
@@ -382,8 +392,7 @@ extern "C" int inv_hip_safetensors_info(const char *path, const char *name, int 
     return INV_OK;
 }
 
-extern "C" int inv_hip_weight_load_safetensors(const char *path, const char *name, const char *bias_name, int flags,
-                                               inv_weight_t *out) {
+static int weight_load_impl(const char *path, const char *name, const char *bias_name, int flags, inv_weight_t *out) {
     if (!out) return fail(INV_ERR_ARG, "safetensors: null output handle");
     *out = nullptr;
     MappedFile f;
@@ -398,6 +407,10 @@ extern "C" int inv_hip_weight_load_safetensors(const char *path, const char *nam
         return fail(INV_ERR_UNSUPPORTED, "safetensors: \"%s\" has dtype %s (supported: BF16, F32, F16)", name,
                     t->dtype.c_str());
     const int64_t N = t->shape[0], K = t->shape[1];
+    // the limits of the upload entry points, checked before any host conversion buffer is sized
+    if (N <= 0 || K <= 0 || N > INT32_MAX / 2 || K > INT32_MAX / 2)
+        return fail(INV_ERR_ARG, "safetensors: \"%s\" is %lld x %lld: each dimension must be in [1, 2^30)", name,
+                    (long long)N, (long long)K);
     const bool gate_up = (flags & INV_ST_GATE_UP) != 0;
     if (gate_up && (N % 2))
         return fail(INV_ERR_ARG, "safetensors: \"%s\" has %lld rows, a fused gate|up weight needs an even count", name,
@@ -459,4 +472,28 @@ extern "C" int inv_hip_weight_load_safetensors(const char *path, const char *nam
         wb[(size_t)i] = (uint16_t)(u >> 16);
     }
     return inv_hip_weight_upload(wb.data(), N, K, bp, out);
+}
+
+// The C entry points: no exception crosses the ABI (an allocation failure in a
+// host conversion buffer becomes INV_ERR_OOM, anything else INV_ERR_ARG).
+extern "C" int inv_hip_safetensors_info(const char *path, const char *name, int *dtype, int *ndim, int64_t *shape,
+                                        int64_t *data_offset) {
+    try {
+        return safetensors_info_impl(path, name, dtype, ndim, shape, data_offset);
+    } catch (const std::bad_alloc &) {
+        return fail(INV_ERR_OOM, "safetensors: host memory exhausted");
+    } catch (const std::exception &e) {
+        return fail(INV_ERR_ARG, "safetensors: %s", e.what());
+    }
+}
+
+extern "C" int inv_hip_weight_load_safetensors(const char *path, const char *name, const char *bias_name, int flags,
+                                               inv_weight_t *out) {
+    try {
+        return weight_load_impl(path, name, bias_name, flags, out);
+    } catch (const std::bad_alloc &) {
+        return fail(INV_ERR_OOM, "safetensors: host memory exhausted");
+    } catch (const std::exception &e) {
+        return fail(INV_ERR_ARG, "safetensors: %s", e.what());
+    }
 }

@@ -107,6 +107,39 @@ def test_truncated_and_malformed_files(tmp_path):
                                                                   + hj + b"\0" * 4), "a")
 
 
+def test_crafted_headers_fail_cleanly(tmp_path):
+    """Headers built to overflow the shape or byte products, to pass huge dimensions with an empty
+    data range, or to nest without end return a status; nothing wraps, throws or recurses away."""
+    import ctypes
+    lib = hip.load()
+
+    def st(header):
+        hj = json.dumps(header).encode() if isinstance(header, dict) else header
+        return _write(tmp_path, "c.st", len(hj).to_bytes(8, "little") + hj + b"\0" * 8)
+
+    # 2^32 * 2^31 elements of F16 wrap a 64-bit byte count to 0, matching an empty data range
+    p = st({"w": {"dtype": "F16", "shape": [2 ** 32, 2 ** 31], "data_offsets": [0, 0]}})
+    assert "overflows" in _error(q.safetensors_info, p, "w")
+    # the element count itself overflows
+    p = st({"w": {"dtype": "BF16", "shape": [2 ** 40, 2 ** 30], "data_offsets": [0, 0]}})
+    assert "overflows" in _error(q.safetensors_info, p, "w")
+    # a zero-sized matrix with a huge row count: consistent bytes, refused before any conversion
+    h = ctypes.c_void_p()
+    for shape in ([2 ** 30, 0], [0, 8], [8, 2 ** 31]):
+        p = st({"w": {"dtype": "F16", "shape": shape, "data_offsets": [0, 2 * shape[0] * shape[1]]}})
+        if shape[0] * shape[1] * 2 > 8:
+            assert "outside the file" in _error(q.safetensors_info, p, "w")
+            continue
+        rc = lib.inv_hip_weight_load_safetensors(p.encode(), b"w", None, 0, ctypes.byref(h))
+        assert rc == hip.INV_ERR_ARG and "each dimension" in hip.last_error(), shape
+    # 200 nested arrays in the metadata: refused, not recursed into
+    deep = b'{"__metadata__": ' + b"[" * 200 + b"]" * 200 + b"}"
+    assert "bad header" in _error(q.safetensors_info, st(deep), "w")
+    shallow = b'{"__metadata__": ' + b"[" * 20 + b"]" * 20 + b', "a": {"dtype": "F32", "shape": [2], ' \
+              b'"data_offsets": [0, 8]}}'
+    assert q.safetensors_info(st(shallow), "a")["shape"] == (2,)
+
+
 def test_other_dtypes_are_reported_not_decoded(tmp_path):
     hj = json.dumps({"ids": {"dtype": "I64", "shape": [3], "data_offsets": [0, 24]}}).encode()
     p = _write(tmp_path, "i.st", len(hj).to_bytes(8, "little") + hj + b"\0" * 24)
