@@ -162,6 +162,28 @@ int inv_hip_weight_load_safetensors(const char *path, const char *name, const ch
 /* N and K of a handle. */
 int inv_hip_weight_shape(inv_weight_t w, int64_t *N, int64_t *K);
 
+/* ---- the device weight cache ---------------------------------------------- */
+/* The reference re-reads and re-widens every block's weights from the mapped
+ * file on every sampler step and frees them afterwards
+ * (src/quicknn_transformers.pas:1581-1602, src/quicknn_qwen3.pas:1087-1091,
+ * through getTensorDataMemBlock, src/safetensor.pas:584-683).
+ * inv_hip_weight_cache_get returns the resident handle of (file, tensor, bias
+ * tensor, flags) -- the file identified by device, inode, size and
+ * modification time, so a rewritten file is loaded again -- uploading it on
+ * the first request only (as inv_hip_weight_load_safetensors).  Each get holds
+ * one reference; inv_hip_weight_free on the handle releases it and leaves the
+ * weight resident.  With a budget (bytes; 0 = unlimited, the default), the
+ * least recently used unreferenced weights are evicted while the cache holds
+ * more; referenced ones never are.  inv_hip_weight_cache_clear frees every
+ * unreferenced entry and detaches the rest (freed by their last release).
+ * stats: entries, resident bytes, hits, misses and bytes uploaded so far. */
+int inv_hip_weight_cache_get(const char *path, const char *name, const char *bias_name, int flags,
+                             inv_weight_t *out);
+int inv_hip_weight_cache_set_budget(int64_t bytes);
+int inv_hip_weight_cache_clear(void);
+int inv_hip_weight_cache_stats(int64_t *entries, int64_t *bytes, int64_t *hits, int64_t *misses,
+                               int64_t *uploaded_bytes);
+
 /* ---- the linear layer ----------------------------------------------------- */
 /* Y[M x N] = epilogue(X[M x K] . W^T + bias), row-major, leading dims K and N.
  *  X: fp32 (rounded to bf16, ties to even, on the device) or bf16.

@@ -11,6 +11,9 @@
 #include "../../include/inv_hip.h"
 
 #include <hip/hip_runtime.h>
+#include <limits.h>
+#include <stdlib.h>
+#include <sys/stat.h>
 
 #include <algorithm>
 #include <atomic>
@@ -191,6 +194,18 @@ struct State {
     double gemm_ms = 0.0, flops = 0.0;
     std::vector<inv_weight_s *> weights;
     unsigned char *scratch = nullptr;  // device address of `scratch` on g.device
+    // The device weight cache: one entry per (file identity, tensor, bias, flags).
+    struct CacheEntry {
+        std::string key;
+        inv_weight_s *w;
+        uint64_t last_use;
+        size_t bytes;
+    };
+    std::vector<CacheEntry> cache;
+    size_t cache_bytes = 0;
+    int64_t cache_budget = 0;  // bytes; 0: unlimited
+    uint64_t cache_clock = 0;
+    int64_t cache_hits = 0, cache_misses = 0, cache_uploaded = 0;
 };
 
 State g;
@@ -222,6 +237,11 @@ struct inv_weight_s {
     int gated;     // gate/up pair for INV_EPI_SWIGLU: rows = 2 * N rounded up to 128 per half,
                    // interleaved in 128-row blocks (gate block b at rows 256b, its up block at 256b + 128)
     int64_t rows;  // device rows (N unless gated)
+    // Weight cache (inv_hip_weight_cache_get): a cached handle belongs to the
+    // cache; inv_hip_weight_free releases one reference instead of freeing.
+    bool cached = false;
+    bool detached = false;  // dropped from the cache while referenced: freed on its last release
+    int refs = 0;           // outstanding references from inv_hip_weight_cache_get
 };
 
 namespace {
@@ -671,6 +691,52 @@ int weight_upload_impl(const void *w, bool is_f32, int64_t N, int64_t K, const f
     auto *h = new inv_weight_s{kWeightMagic, dw, db, N, K, ldw, 0, N};
     g.weights.push_back(h);
     *out = h;
+    return INV_OK;
+}
+
+size_t weight_bytes(const inv_weight_s *w) {
+    return (size_t)(w->rows * w->ldw) * 2 + (w->bias ? (size_t)w->rows * 4 : 0);
+}
+
+void free_weight(inv_weight_s *w);
+
+// Free a handle the library still lists (g.weights).
+void drop_weight(inv_weight_s *w) {
+    auto it = std::find(g.weights.begin(), g.weights.end(), w);
+    if (it != g.weights.end()) g.weights.erase(it);
+    free_weight(w);
+}
+
+// Evict least-recently-used cache entries nobody references until the cache
+// fits its budget (entries in use are never evicted).
+void cache_trim() {
+    if (g.cache_budget <= 0) return;
+    while (g.cache_bytes > (size_t)g.cache_budget) {
+        int victim = -1;
+        for (size_t i = 0; i < g.cache.size(); ++i)
+            if (g.cache[i].w->refs == 0 && (victim < 0 || g.cache[i].last_use < g.cache[(size_t)victim].last_use))
+                victim = (int)i;
+        if (victim < 0) return;
+        (void)hipStreamSynchronize(g.stream);
+        g.cache_bytes -= g.cache[(size_t)victim].bytes;
+        drop_weight(g.cache[(size_t)victim].w);
+        g.cache.erase(g.cache.begin() + victim);
+    }
+}
+
+// The cache key: the file's identity (device, inode, size, modification time,
+// so a rewritten file is not served from the cache) and its resolved path,
+// the tensor and bias names and the load flags.
+int cache_key(const char *path, const char *name, const char *bias_name, int flags, std::string *key) {
+    struct stat st;
+    if (stat(path, &st) != 0) return fail(INV_ERR_ARG, "weight cache: cannot stat %s", path);
+    char real[PATH_MAX];
+    if (!realpath(path, real)) return fail(INV_ERR_ARG, "weight cache: cannot resolve %s", path);
+    char id[128];
+    snprintf(id, sizeof id, "%llu:%llu:%lld:%lld.%09ld", (unsigned long long)st.st_dev, (unsigned long long)st.st_ino,
+             (long long)st.st_size, (long long)st.st_mtim.tv_sec, (long)st.st_mtim.tv_nsec);
+    *key = std::string(id) + '\n' + real + '\n' + name + '\n' + (bias_name ? bias_name : "") + '\n' +
+           std::to_string(flags);
     return INV_OK;
 }
 
@@ -1485,6 +1551,11 @@ int inv_hip_shutdown(void) {
     (void)hipStreamSynchronize(g.stream);
     for (auto *w : g.weights) free_weight(w);
     g.weights.clear();
+    g.cache.clear();
+    g.cache_bytes = 0;
+    g.cache_budget = 0;
+    g.cache_clock = 0;
+    g.cache_hits = g.cache_misses = g.cache_uploaded = 0;
     for (Buf *b : {&g.xin, &g.x16, &g.w16, &g.win, &g.yout, &g.cin, &g.bias, &g.gate, &g.aq, &g.ak, &g.avt, &g.aqin,
                    &g.akin, &g.avin, &g.nvec, &g.amask, &g.hx, &g.hvec, &g.csrc, &g.ccol, &g.cdst})
         release(*b);
@@ -1586,9 +1657,100 @@ int inv_hip_weight_free(inv_weight_t w) {
     auto it = std::find(g.weights.begin(), g.weights.end(), w);
     if (it == g.weights.end()) return fail(INV_ERR_ARG, "unknown weight handle");
     (void)hipSetDevice(g.device);
+    if (w->cached) {
+        // a reference from inv_hip_weight_cache_get: the weight stays resident
+        if (w->refs > 0) --w->refs;
+        if (w->detached && w->refs == 0) {
+            (void)hipStreamSynchronize(g.stream);
+            drop_weight(w);
+        } else {
+            cache_trim();
+        }
+        return INV_OK;
+    }
     (void)hipStreamSynchronize(g.stream);
     free_weight(w);
     g.weights.erase(it);
+    return INV_OK;
+}
+
+int inv_hip_weight_cache_get(const char *path, const char *name, const char *bias_name, int flags,
+                             inv_weight_t *out) {
+    if (!out) return fail(INV_ERR_ARG, "weight cache: null output handle");
+    *out = nullptr;
+    if (!path || !name) return fail(INV_ERR_ARG, "weight cache: null path or tensor name");
+    std::string key;
+    TRY(cache_key(path, name, bias_name, flags, &key));
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        TRY(check_init());
+        for (auto &e : g.cache)
+            if (e.key == key) {
+                ++e.w->refs;
+                e.last_use = ++g.cache_clock;
+                ++g.cache_hits;
+                *out = e.w;
+                return INV_OK;
+            }
+    }
+    // A miss: load outside the lock (the upload takes it), then insert.
+    inv_weight_t h = nullptr;
+    TRY(inv_hip_weight_load_safetensors(path, name, bias_name, flags, &h));
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (auto &e : g.cache)
+        if (e.key == key) {  // another thread loaded the same tensor meanwhile
+            (void)hipStreamSynchronize(g.stream);
+            drop_weight(h);
+            ++e.w->refs;
+            e.last_use = ++g.cache_clock;
+            ++g.cache_hits;
+            *out = e.w;
+            return INV_OK;
+        }
+    h->cached = true;
+    h->refs = 1;
+    const size_t bytes = weight_bytes(h);
+    g.cache.push_back({key, h, ++g.cache_clock, bytes});
+    g.cache_bytes += bytes;
+    ++g.cache_misses;
+    g.cache_uploaded += (int64_t)bytes;
+    cache_trim();
+    *out = h;
+    return INV_OK;
+}
+
+int inv_hip_weight_cache_set_budget(int64_t bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    TRY(check_init());
+    if (bytes < 0) return fail(INV_ERR_ARG, "weight cache: negative budget");
+    g.cache_budget = bytes;
+    cache_trim();
+    return INV_OK;
+}
+
+int inv_hip_weight_cache_clear(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    TRY(check_init());
+    (void)hipStreamSynchronize(g.stream);
+    for (auto &e : g.cache) {
+        if (e.w->refs == 0)
+            drop_weight(e.w);
+        else
+            e.w->detached = true;  // freed by its last inv_hip_weight_free
+    }
+    g.cache.clear();
+    g.cache_bytes = 0;
+    return INV_OK;
+}
+
+int inv_hip_weight_cache_stats(int64_t *entries, int64_t *bytes, int64_t *hits, int64_t *misses,
+                               int64_t *uploaded_bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (entries) *entries = (int64_t)g.cache.size();
+    if (bytes) *bytes = (int64_t)g.cache_bytes;
+    if (hits) *hits = g.cache_hits;
+    if (misses) *misses = g.cache_misses;
+    if (uploaded_bytes) *uploaded_bytes = g.cache_uploaded;
     return INV_OK;
 }
 

@@ -68,6 +68,11 @@ _PROTOS = {
                                               POINTER(c_void_p)]),
     "inv_hip_weight_free": (c_int, [c_void_p]),
     "inv_hip_weight_shape": (c_int, [c_void_p, POINTER(c_int64), POINTER(c_int64)]),
+    "inv_hip_weight_cache_get": (c_int, [c_char_p, c_char_p, c_char_p, c_int, POINTER(c_void_p)]),
+    "inv_hip_weight_cache_set_budget": (c_int, [c_int64]),
+    "inv_hip_weight_cache_clear": (c_int, []),
+    "inv_hip_weight_cache_stats": (c_int, [POINTER(c_int64), POINTER(c_int64), POINTER(c_int64),
+                                           POINTER(c_int64), POINTER(c_int64)]),
     "inv_hip_safetensors_info": (c_int, [c_char_p, c_char_p, POINTER(c_int), POINTER(c_int), POINTER(c_int64),
                                          POINTER(c_int64)]),
     "inv_hip_weight_load_safetensors": (c_int, [c_char_p, c_char_p, c_char_p, c_int, POINTER(c_void_p)]),

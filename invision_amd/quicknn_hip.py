@@ -191,16 +191,19 @@ class Weight:
 
     @classmethod
     def from_safetensors(cls, path: str, name: str, bias_name: Optional[str] = None,
-                         truncate: bool = False, gate_up: bool = False) -> "Weight":
+                         truncate: bool = False, gate_up: bool = False, cached: bool = False) -> "Weight":
         """Upload the [N x K] tensor `name` (and 1-D `bias_name`) of a .safetensors
         file: the reference's getTensorDataMemBlockBF16 (src/safetensor.pas:650-683)
         feeding the device once.  BF16 is copied as is; F32/F16 are rounded to bf16
-        (ties to even, or truncated like the reference's SingleToBF16 with truncate)."""
+        (ties to even, or truncated like the reference's SingleToBF16 with truncate).
+        cached=True takes the handle from the library's weight cache: the first
+        request uploads, later ones for the same file and tensor return the resident
+        weight, and free() releases the reference instead of the memory."""
         init()
         h = ctypes.c_void_p()
         flags = (hip.INV_ST_TRUNCATE if truncate else 0) | (hip.INV_ST_GATE_UP if gate_up else 0)
-        hip.call("inv_hip_weight_load_safetensors", os.fsencode(path), name.encode(),
-                 bias_name.encode() if bias_name else None, flags, ctypes.byref(h))
+        hip.call("inv_hip_weight_cache_get" if cached else "inv_hip_weight_load_safetensors", os.fsencode(path),
+                 name.encode(), bias_name.encode() if bias_name else None, flags, ctypes.byref(h))
         self = cls.__new__(cls)
         self.handle = h.value
         n, k = ctypes.c_int64(), ctypes.c_int64()
@@ -790,6 +793,26 @@ class SafeTensorFiles:
                 continue
         raise KeyError(f"cannot find tensor \"{name}\" in {len(self.paths)} file(s)")
 
-    def linear_weight(self, name: str, bias_name: Optional[str] = None, truncate: bool = False) -> Weight:
-        """A device weight for a Linear layer (bias from the same shard)."""
-        return Weight.from_safetensors(self.find(name), name, bias_name, truncate)
+    def linear_weight(self, name: str, bias_name: Optional[str] = None, truncate: bool = False,
+                      cached: bool = True) -> Weight:
+        """A device weight for a Linear layer (bias from the same shard).  By default from the
+        library's weight cache: the reference loads every block's weights again on every
+        sampler step and frees them (src/quicknn_transformers.pas:1581-1602); here the first
+        request uploads and the rest reuse the resident copy (free() releases the reference)."""
+        return Weight.from_safetensors(self.find(name), name, bias_name, truncate, cached=cached)
+
+
+def weight_cache_stats() -> dict:
+    """Entries, resident bytes, hits, misses and bytes uploaded by the weight cache."""
+    v = [ctypes.c_int64() for _ in range(5)]
+    hip.call("inv_hip_weight_cache_stats", *(ctypes.byref(x) for x in v))
+    return dict(zip(("entries", "bytes", "hits", "misses", "uploaded_bytes"), (x.value for x in v)))
+
+
+def weight_cache_set_budget(nbytes: int) -> None:
+    """Evict least recently used, unreferenced cached weights above nbytes (0: no limit)."""
+    hip.call("inv_hip_weight_cache_set_budget", int(nbytes))
+
+
+def weight_cache_clear() -> None:
+    hip.call("inv_hip_weight_cache_clear")

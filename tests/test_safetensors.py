@@ -217,3 +217,65 @@ def test_f16_weight_and_bf16_bias(hiplib):
     with q.Weight.from_safetensors(FIX, "blocks.0.mlp.fc16.weight", "blocks.0.mlp.fc16.bias") as wf, \
             q.Weight(oracle.f32_to_bf16_rne(w), b) as wa:
         _same_products(wf, wa)
+
+
+# ------------------------------------------------------------ GPU: weight cache --
+
+@pytest.mark.gpu
+def test_weight_cache_uploads_once_per_file_and_tensor(hiplib, tmp_path):
+    """The reference loads a block's weights from the mapped file on every sampler step and frees
+    them (src/quicknn_transformers.pas:1581-1602).  Through the cache, the second and later
+    requests of the same tensor (also through the index-JSON shard map) return the resident
+    handle: no upload, the same products; free() releases the reference only."""
+    q.weight_cache_clear()
+    s0 = q.weight_cache_stats()
+    a = os.path.join(tmp_path, "model-00001-of-00002.safetensors")
+    b = os.path.join(tmp_path, "model-00002-of-00002.safetensors")
+    shutil.copy(FIX, a)
+    shutil.copy(FIX, b)  # the same bytes in another file: a different cache entry
+    with open(os.path.join(tmp_path, "model.safetensors.index.json"), "w") as f:
+        json.dump({"metadata": {}, "weight_map": {"blocks.0.attn.qkv.weight": os.path.basename(a),
+                                                  "blocks.0.attn.qkv.bias": os.path.basename(a),
+                                                  "blocks.0.mlp.fc32.weight": os.path.basename(b)}}, f)
+    files = q.SafeTensorFiles(str(tmp_path))
+    with q.Weight(EXP["w_bf16"], EXP["b_f32"]) as wa:
+        handles = []
+        for step in range(3):  # three "sampler steps": load, use, free
+            w = files.linear_weight("blocks.0.attn.qkv.weight", "blocks.0.attn.qkv.bias")
+            handles.append(w.handle)
+            _same_products(w, wa)
+            w.free()
+        assert len(set(handles)) == 1
+    s1 = q.weight_cache_stats()
+    wbytes = N * ((K + 7) // 8 * 8) * 2 + N * 4
+    assert s1["misses"] - s0["misses"] == 1 and s1["hits"] - s0["hits"] == 2
+    assert s1["uploaded_bytes"] - s0["uploaded_bytes"] == wbytes and s1["entries"] == 1
+    # another shard, another tensor: one more upload; the bias-less request is its own entry
+    w2 = files.linear_weight("blocks.0.mlp.fc32.weight")
+    w3 = q.Weight.from_safetensors(a, "blocks.0.attn.qkv.weight", cached=True)
+    s2 = q.weight_cache_stats()
+    assert s2["misses"] - s1["misses"] == 2 and s2["entries"] == 3
+    # a budget evicts unreferenced entries only, least recently used first
+    q.weight_cache_set_budget(1)
+    assert q.weight_cache_stats()["entries"] == 2  # the qkv weight with bias was released
+    w2.free()
+    w3.free()
+    assert q.weight_cache_stats()["entries"] == 0
+    q.weight_cache_set_budget(0)
+    # a rewritten file is a new entry (its modification time and size moved)
+    w4 = files.linear_weight("blocks.0.attn.qkv.weight", "blocks.0.attn.qkv.bias")
+    h4 = w4.handle
+    w4.free()
+    with open(a, "ab") as f:
+        f.write(b"\0" * 8)  # trailing bytes: the header and tensors are unchanged
+    w5 = files.linear_weight("blocks.0.attn.qkv.weight", "blocks.0.attn.qkv.bias")
+    assert q.weight_cache_stats()["misses"] - s2["misses"] == 2
+    w5.free()
+    assert h4 is not None
+    # clear while referenced: detached, freed on the last release; handles stay usable until then
+    w6 = files.linear_weight("blocks.0.mlp.fc32.weight")
+    q.weight_cache_clear()
+    assert q.weight_cache_stats()["entries"] == 0
+    with q.Weight(oracle.f32_to_bf16_rne(EXP["w32"])) as wa:
+        _same_products(w6, wa)
+    w6.free()
