@@ -179,6 +179,8 @@ __device__ __forceinline__ void grouped_tile(int L, int tiles_m, int tiles_n, in
 template <int TN_, int TM_, int WN_, int WM_, int BK_, int NST_>
 struct TileCfg {
     static constexpr bool REG_STAGED = false;
+    static constexpr int BH = 32;  // MFMA block: v_mfma_f32_32x32x16_bf16
+    typedef f32x16_t acc_t;
     static constexpr int TN = TN_, TM = TM_, WN = WN_, WM = WM_, BK = BK_, NST = NST_;
     static constexpr int NWAVES = WN * WM;
     static constexpr int NTHREADS = NWAVES * 64;
@@ -216,6 +218,9 @@ struct TileCfg {
 template <int TN_, int TM_, int WN_, int WM_, int NREG_ = 2, int PF_ = 1>
 struct RsCfg {
     static constexpr bool REG_STAGED = true;
+    static constexpr bool ASINGLE = false;
+    static constexpr int BH = 32;  // MFMA block: v_mfma_f32_32x32x16_bf16
+    typedef f32x16_t acc_t;
     static constexpr int TN = TN_, TM = TM_, WN = WN_, WM = WM_, BK = 64, NST = 2, NREG = NREG_;
     static constexpr int PF = PF_;  // fragment reads run PF 16-wide substeps ahead of the MFMAs
     static constexpr int NWAVES = WN * WM;
@@ -246,6 +251,54 @@ struct RsCfg {
     static constexpr bool STAGED_EPI = NWAVES * 32 * (WTN + 4) * 4 <= LDS_BYTES && 64 % (WTN / 4) == 0;
     static constexpr bool SWIGLU_OK = STAGED_EPI && TN == 256 && WN == 2;  // wave columns = gate | up
     static_assert(NREG * LOADS - 1 < 64, "vmcnt holds at most 63 outstanding loads");
+};
+
+// Register-staged configuration on v_mfma_f32_16x16x32_bf16: 16-row MFMA
+// blocks, so a wave tile may be any multiple of 16 (e.g. 128 x 112, whose 224
+// accumulator registers leave room that a 128 x 128 tile of 16x16 blocks does
+// not).  64-wide k-tiles as RsCfg, each two 32-wide substeps; fragments one
+// substep ahead (two register sets).  MFMA blocks of 16 rows give twice the
+// operand reads per FLOP of 32x32x16 but a quarter of the accumulator traffic.
+//  ASINGLE: the W (A operand) fragments are single-buffered: A fragment i of
+//  the next substep is read into the same registers right after the last MFMA
+//  of this substep that uses it (i-major order: A[i] is used by FM consecutive
+//  MFMAs), while the X fragments, used by every MFMA row, stay double-buffered.
+//  That frees FN*4 registers, enough for a second register stage of global
+//  prefetch.
+template <int TN_, int TM_, int WN_, int WM_, int NREG_ = 1, bool ASINGLE_ = false>
+struct Rs16Cfg {
+    static constexpr bool REG_STAGED = true;
+    static constexpr int BH = 16;  // MFMA block: v_mfma_f32_16x16x32_bf16
+    typedef f32x4_t acc_t;
+    static constexpr int TN = TN_, TM = TM_, WN = WN_, WM = WM_, BK = 64, NST = 2, NREG = NREG_;
+    static constexpr int PF = 1;
+    static constexpr bool ASINGLE = ASINGLE_;
+    static constexpr int NWAVES = WN * WM;
+    static constexpr int NTHREADS = NWAVES * 64;
+    static constexpr int WTN = TN / WN;
+    static constexpr int WTM = TM / WM;
+    static constexpr int FN = WTN / 16;
+    static constexpr int FM = WTM / 16;
+    static constexpr int SLOTS = 8;
+    static constexpr int ROWB = 128;
+    static constexpr int KSUB = 2;
+    static constexpr int A_BYTES = TN * ROWB;
+    static constexpr int B_BYTES = TM * ROWB;
+    static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+    static constexpr int LDS_BYTES = 2 * STAGE_BYTES;
+    static constexpr int A_LOADS = TN * SLOTS / NTHREADS;
+    static constexpr int B_LOADS = TM * SLOTS / NTHREADS;
+    static constexpr int LOADS = A_LOADS + B_LOADS;
+    static constexpr int ACC_REGS = FN * FM * 4;
+    static_assert(TN % (WN * 16) == 0 && TM % (WM * 16) == 0, "wave tile must be a multiple of 16");
+    static_assert((TN * SLOTS) % NTHREADS == 0 && (TM * SLOTS) % NTHREADS == 0, "copies must divide evenly");
+    static_assert((NTHREADS / SLOTS) % 16 == 0, "copy rows must advance in multiples of 16");
+    static_assert(LDS_BYTES <= 160 * 1024, "gfx950 has 160 KiB of LDS per CU");
+    static_assert(NREG == 1 || NREG == 2, "one or two register stages");
+    static_assert(NREG * LOADS - 1 < 64, "vmcnt holds at most 63 outstanding loads");
+    static constexpr bool STAGED_EPI = NWAVES * BH * (WTN + 4) * 4 <= LDS_BYTES && 64 % (WTN / 4) == 0;
+    static constexpr bool SWIGLU_OK = STAGED_EPI && TN == 256 && WN == 2;
+    static_assert(STAGED_EPI, "16x16 blocks have only the staged epilogue");
 };
 
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -300,6 +353,16 @@ __device__ __forceinline__ void load_frags(const lds_char_t *stage, int a_frag, 
     for (int i = 0; i < C::FN; ++i) fa[i] = *(const bf16x8_t *)(stage + a_frag + i * 32 * C::ROWB + coff);
 #pragma unroll
     for (int j = 0; j < C::FM; ++j) fb[j] = *(const bf16x8_t *)(stage + b_frag + j * 32 * C::ROWB + coff);
+}
+
+// One MFMA of the configuration's block shape: acc += A . B^T over 16 (32x32
+// blocks) or 32 (16x16 blocks) k.
+template <class C>
+__device__ __forceinline__ void mfma_step(typename C::acc_t &acc, const bf16x8_t &a, const bf16x8_t &b) {
+    if constexpr (C::BH == 32)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+    else
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
 }
 
 template <class C>
@@ -541,13 +604,19 @@ __device__ __forceinline__ void mainloop_ring(const GemmParams &p, lds_char_t *l
 template <class C>
 __device__ __forceinline__ void mainloop_rs(const GemmParams &p, lds_char_t *lds, __amdgpu_buffer_rsrc_t rsw,
                                             __amdgpu_buffer_rsrc_t rsx, int kt_begin, int kt_end,
-                                            f32x16_t (&acc)[C::FN][C::FM]) {
+                                            typename C::acc_t (&acc)[C::FN][C::FM]) {
     typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
     constexpr int BK = C::BK, ROWB = C::ROWB, SLOTS = C::SLOTS;
     constexpr int AL = C::A_LOADS, L = C::LOADS;
     constexpr int RPL = C::NTHREADS / SLOTS;  // rows covered by one copy chunk
-    constexpr int T = C::FN * C::FM;         // MFMAs per 16-wide substep
+    constexpr int T = C::FN * C::FM;         // MFMAs per substep
     constexpr int NR = C::FN + C::FM;        // fragment reads per substep
+    // MFMA block geometry: a lane reads 16 bytes (8 k) of row lane % BH of each
+    // block; the 64 / BH lane groups take consecutive 8-k chunks, so a substep
+    // covers CPS chunks (16 k for 32x32x16, 32 k for 16x16x32).
+    constexpr int BH = C::BH;
+    constexpr int CPS = 64 / BH;
+    static_assert(C::KSUB * CPS == SLOTS, "the substeps cover the 64-wide k-tile");
     constexpr int BAR = 1;                   // MFMA step of the last substep after which the barrier sits
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -566,15 +635,17 @@ __device__ __forceinline__ void mainloop_rs(const GemmParams &p, lds_char_t *lds
     const uint32_t a_step = (uint32_t)(RPL * p.ldw * 2);
     const uint32_t b_step = (uint32_t)(RPL * p.ldx * 2);
 
-    // Fragment side (as in the ring loop).
-    const int frow = lane & 31;
-    const int fh = lane >> 5;
+    // Fragment side: lane reads row (lane % BH) of each block, logical chunk
+    // CPS*kk + lane / BH, stored at slot chunk ^ key(row) (the key depends on
+    // the row mod 16, the same for every block).
+    const int frow = lane & (BH - 1);
+    const int fh = lane / BH;
     const int fkey = slot_key<SLOTS>(frow);
     const int a_frag = (wn * C::WTN + frow) * ROWB;
     const int b_frag = C::A_BYTES + (wm * C::WTM + frow) * ROWB;
     int coff[C::KSUB];
 #pragma unroll
-    for (int kk = 0; kk < C::KSUB; ++kk) coff[kk] = ((2 * kk + fh) ^ fkey) * 16;
+    for (int kk = 0; kk < C::KSUB; ++kk) coff[kk] = ((CPS * kk + fh) ^ fkey) * 16;
 
     const int wseg = p.w_seg_k / BK;
     int load_kt = kt_begin;
@@ -625,10 +696,16 @@ __device__ __forceinline__ void mainloop_rs(const GemmParams &p, lds_char_t *lds
     // of substep s (PF = 1: two buffers alternating; PF = 2: one per substep).
     constexpr int PF = C::PF;
     constexpr int NB = (PF == 1) ? 2 : C::KSUB;
-    bf16x8_t fa[NB][C::FN], fb[NB][C::FM];
+    constexpr bool AS = C::ASINGLE;
+    static_assert(!AS || PF == 1, "single-buffered A fragments are read one substep ahead");
+    constexpr int NBA = AS ? 1 : NB;
+    bf16x8_t fa[NBA][C::FN], fb[NB][C::FM];
     static_for<PF>([&](auto sc) {
         constexpr int s0 = decltype(sc)::value;
-        load_frags<C>(buf0, a_frag, b_frag, coff[s0], fa[s0], fb[s0]);
+#pragma unroll
+        for (int i = 0; i < C::FN; ++i) fa[s0][i] = *(const bf16x8_t *)(buf0 + a_frag + i * BH * ROWB + coff[s0]);
+#pragma unroll
+        for (int j = 0; j < C::FM; ++j) fb[s0][j] = *(const bf16x8_t *)(buf0 + b_frag + j * BH * ROWB + coff[s0]);
     });
     // The barrier precedes the first read of the next tile (substep KSUB-PF);
     // the ds_writes of the next tile all come before it.
@@ -649,18 +726,26 @@ __device__ __forceinline__ void mainloop_rs(const GemmParams &p, lds_char_t *lds
             static_for<T>([&](auto qc) {
                 constexpr int q = decltype(qc)::value;
                 constexpr int i = q / C::FM, j = q % C::FM;
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cb_i][i], fb[cb_i][j], acc[i][j], 0, 0, 0);
+                mfma_step<C>(acc[i][j], fa[AS ? 0 : cb_i][i], fb[cb_i][j]);
                 if constexpr (ks == BSUB && q == BAR) __syncthreads();
-                // fragment reads for substep rd
+                if constexpr (AS && j == C::FM - 1) {
+                    // the last use of A fragment i in this substep: read the next
+                    // substep's into the same registers (after the barrier in the
+                    // last substep, as i * FM + FM - 1 > BAR)
+                    static_assert(!(ks == BSUB) || C::FM - 1 > BAR, "A reads of the next tile follow the barrier");
+                    fa[0][i] = *(const bf16x8_t *)(rs + a_frag + i * BH * ROWB + rc);
+                }
+                // fragment reads for substep rd (the X fragments only, with AS)
                 static_for<NR>([&](auto rc2) {
                     constexpr int r = decltype(rc2)::value;
                     constexpr int at = (ks == BSUB) ? BAR + 1 + (r * (T - BAR - 1)) / NR : (r * T) / NR;
                     if constexpr (at == q) {
                         constexpr int fr = frag_read<C>(r);
-                        if constexpr (fr >= 0)
-                            fa[nb_i][fr] = *(const bf16x8_t *)(rs + a_frag + fr * 32 * ROWB + rc);
-                        else
-                            fb[nb_i][-1 - fr] = *(const bf16x8_t *)(rs + b_frag + (-1 - fr) * 32 * ROWB + rc);
+                        if constexpr (fr >= 0) {
+                            if constexpr (!AS) fa[nb_i][fr] = *(const bf16x8_t *)(rs + a_frag + fr * BH * ROWB + rc);
+                        } else {
+                            fb[nb_i][-1 - fr] = *(const bf16x8_t *)(rs + b_frag + (-1 - fr) * BH * ROWB + rc);
+                        }
                     }
                 });
                 // copy chunks: ds_write tile t+1, reload the registers with tile t+1+NREG
@@ -725,19 +810,44 @@ __device__ __forceinline__ void mainloop_rs(const GemmParams &p, lds_char_t *lds
 // VGPRs next to the main loop's registers).
 enum { SK_NONE = 0, SK_PUBLISH = 1, SK_FINISH = 2 };
 
+// Stage block column j of a wave's accumulators (every i) as BH rows of WTN
+// floats (times alpha) at st: lane holds D[n][m = frow] for 4 consecutive n,
+// at n = 8g + 4*fh (32x32 blocks, g = 0..3) or 4*fh (16x16 blocks).
+template <class C>
+__device__ __forceinline__ void stage_block(__attribute__((address_space(3))) float *st,
+                                            const typename C::acc_t (&acc)[C::FN][C::FM], int j, int lane,
+                                            float alpha) {
+    constexpr int SROW = C::WTN + 4;
+    const int frow = lane & (C::BH - 1);
+    const int fh = lane / C::BH;
+    typedef __attribute__((address_space(3))) f32x4_t lds_f32x4_t;
+#pragma unroll
+    for (int i = 0; i < C::FN; ++i) {
+        if constexpr (C::BH == 32) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *(lds_f32x4_t *)(st + frow * SROW + i * 32 + 8 * g + 4 * fh) =
+                    f32x4_t{alpha * acc[i][j][4 * g], alpha * acc[i][j][4 * g + 1], alpha * acc[i][j][4 * g + 2],
+                            alpha * acc[i][j][4 * g + 3]};
+        } else {
+            *(lds_f32x4_t *)(st + frow * SROW + i * 16 + 4 * fh) =
+                f32x4_t{alpha * acc[i][j][0], alpha * acc[i][j][1], alpha * acc[i][j][2], alpha * acc[i][j][3]};
+        }
+    }
+}
+
 template <class C, int EPI, int OUT, bool BETA, int SKM = SK_NONE, int MODE = 0>
 __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_t *lds,
-                                                  const f32x16_t (&acc)[C::FN][C::FM], int m0, int n0, int wn,
-                                                  int wm, int lane, int wave, const UnitFix *fix = nullptr,
+                                                  const typename C::acc_t (&acc)[C::FN][C::FM], int m0, int n0,
+                                                  int wn, int wm, int lane, int wave, const UnitFix *fix = nullptr,
                                                   float *slot = nullptr) {
     typedef __attribute__((address_space(3))) float lds_float_t;
+    constexpr int BH = C::BH;              // rows of an MFMA block (32 or 16)
     constexpr int SROW = C::WTN + 4;       // staged row pitch in floats
     constexpr int LPR = C::WTN / 4;        // lanes per row on the read side
     constexpr int RPI = 64 / LPR;          // rows per read instruction
-    static_assert(LPR * RPI == 64 && 32 % RPI == 0, "whole rows per wave-wide read");
-    const int frow = lane & 31;
-    const int fh = lane >> 5;
-    lds_float_t *st = (lds_float_t *)lds + wave * 32 * SROW;
+    static_assert(LPR * RPI == 64 && BH % RPI == 0, "whole rows per wave-wide read");
+    lds_float_t *st = (lds_float_t *)lds + wave * BH * SROW;
     const int col = (lane % LPR) * 4;
     const int rsub = lane / LPR;
     const int n = n0 + wn * C::WTN + col;
@@ -759,7 +869,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
     }
     // EPI_ROWBIAS: the bias of every row this lane stores, loaded here so
     // that no load sits among the stores.
-    constexpr int NIT = 32 / RPI;
+    constexpr int NIT = BH / RPI;
     constexpr bool RB = EPI == EPI_ROWBIAS;
     float rb[RB ? C::FM : 1][RB ? NIT : 1];
     if constexpr (RB) {
@@ -767,7 +877,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
         for (int j = 0; j < C::FM; ++j)
 #pragma unroll
             for (int it = 0; it < NIT; ++it) {
-                const int m = m0 + wm * C::WTM + j * 32 + it * RPI + rsub;
+                const int m = m0 + wm * C::WTM + j * BH + it * RPI + rsub;
                 rb[j][it] = (SKM != SK_PUBLISH && m < p.M) ? p.row_bias[m] : 0.f;
             }
     }
@@ -779,7 +889,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
 #pragma unroll
     for (int j = 0; j < C::FM; ++j) {
         f32x4_t t[NIT];
-        const int64_t slot_off = ((int64_t)(wave * C::FM + j) * 32 + rsub) * C::WTN + col;
+        const int64_t slot_off = ((int64_t)(wave * C::FM + j) * BH + rsub) * C::WTN + col;
         if constexpr (SKM == SK_FINISH) {
             for (int sp = 0; sp < fix->nseg; ++sp) {
                 const float *src = unit_slot<MODE, C>(p, *fix, sp) + slot_off;
@@ -791,13 +901,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
                 for (int it = 0; it < NIT; ++it) t[it] = (sp == 0) ? u[it] : t[it] + u[it];
             }
         } else {
-#pragma unroll
-            for (int i = 0; i < C::FN; ++i)
-#pragma unroll
-                for (int g = 0; g < 4; ++g)
-                    *(__attribute__((address_space(3))) f32x4_t *)(st + frow * SROW + i * 32 + 8 * g + 4 * fh) =
-                        f32x4_t{p.alpha * acc[i][j][4 * g], p.alpha * acc[i][j][4 * g + 1],
-                                p.alpha * acc[i][j][4 * g + 2], p.alpha * acc[i][j][4 * g + 3]};
+            stage_block<C>(st, acc, j, lane, p.alpha);
             // LDS operations of one wave execute in order: the reads below see the
             // writes above, and the next block's writes follow these reads.  All
             // reads (and C loads) of the block are issued before any store, so the
@@ -815,7 +919,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmParams &p, lds_char_
 #pragma unroll
             for (int it = 0; it < NIT; ++it) t[it] += rb[j][it];
         }
-        const int mrow = m0 + wm * C::WTM + j * 32 + rsub;  // row of it = 0; it adds RPI rows
+        const int mrow = m0 + wm * C::WTM + j * BH + rsub;  // row of it = 0; it adds RPI rows
         if (nvec && mrow + (NIT - 1) * RPI < p.M) {
             // every row of this lane in range, 16-byte aligned: no branches
             f32x4_t cv[BETA ? NIT : 1];
@@ -953,20 +1057,19 @@ __device__ __forceinline__ void store_tile_direct(const GemmParams &p, const f32
 // with the exact SiLU v / (1 + exp(-v)).  Needs SWIGLU_OK and beta == 0.
 template <class C, int OUT>
 __device__ __forceinline__ void store_tile_swiglu(const GemmParams &p, lds_char_t *lds,
-                                                  const f32x16_t (&acc)[C::FN][C::FM], int m0, int n0, int wn,
-                                                  int wm, int lane, int wave) {
+                                                  const typename C::acc_t (&acc)[C::FN][C::FM], int m0, int n0,
+                                                  int wn, int wm, int lane, int wave) {
     static_assert(C::SWIGLU_OK, "SwiGLU needs 256-row tiles split over two wave columns");
     typedef __attribute__((address_space(3))) float lds_float_t;
+    constexpr int BH = C::BH;
     constexpr int SROW = C::WTN + 4;
     constexpr int LPR = C::WTN / 4;   // 32 lanes per staged row
     constexpr int RPI = 64 / LPR;     // 2 rows per read instruction
-    constexpr int HALF = 16;          // rows of a 32-row block finished by each wave of the pair
+    constexpr int HALF = BH / 2;      // rows of a block finished by each wave of the pair
     constexpr int NIT = HALF / RPI;
-    const int frow = lane & 31;
-    const int fh = lane >> 5;
-    lds_float_t *own = (lds_float_t *)lds + wave * 32 * SROW;
-    const lds_float_t *gst = (const lds_float_t *)lds + (0 * C::WM + wm) * 32 * SROW;  // gate wave of this row band
-    const lds_float_t *ust = (const lds_float_t *)lds + (1 * C::WM + wm) * 32 * SROW;  // up wave
+    lds_float_t *own = (lds_float_t *)lds + wave * BH * SROW;
+    const lds_float_t *gst = (const lds_float_t *)lds + (0 * C::WM + wm) * BH * SROW;  // gate wave of this row band
+    const lds_float_t *ust = (const lds_float_t *)lds + (1 * C::WM + wm) * BH * SROW;  // up wave
     const int col = (lane % LPR) * 4;
     const int rsub = lane / LPR;
     const int f = n0 / 2 + col;  // output column
@@ -985,13 +1088,7 @@ __device__ __forceinline__ void store_tile_swiglu(const GemmParams &p, lds_char_
     __syncthreads();  // every wave has finished with the ring
 #pragma unroll
     for (int j = 0; j < C::FM; ++j) {
-#pragma unroll
-        for (int i = 0; i < C::FN; ++i)
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-                *(__attribute__((address_space(3))) f32x4_t *)(own + frow * SROW + i * 32 + 8 * g + 4 * fh) =
-                    f32x4_t{p.alpha * acc[i][j][4 * g], p.alpha * acc[i][j][4 * g + 1],
-                            p.alpha * acc[i][j][4 * g + 2], p.alpha * acc[i][j][4 * g + 3]};
+        stage_block<C>(own, acc, j, lane, p.alpha);
         __syncthreads();  // the pair's gate and up blocks are both staged
         f32x4_t gv[NIT], uv[NIT];
 #pragma unroll
@@ -1000,7 +1097,7 @@ __device__ __forceinline__ void store_tile_swiglu(const GemmParams &p, lds_char_
             gv[it] = *(const __attribute__((address_space(3))) f32x4_t *)(gst + r * SROW + col);
             uv[it] = *(const __attribute__((address_space(3))) f32x4_t *)(ust + r * SROW + col);
         }
-        const int mrow = m0 + wm * C::WTM + j * 32 + wn * HALF + rsub;
+        const int mrow = m0 + wm * C::WTM + j * BH + wn * HALF + rsub;
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
             const int m = mrow + it * RPI;
@@ -1054,13 +1151,14 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
 
     lds_char_t *lds = (lds_char_t *)smem;
 
-    f32x16_t acc[C::FN][C::FM];
+    typename C::acc_t acc[C::FN][C::FM];
+    constexpr int ACC_ELEMS = C::BH * C::BH / 64;  // accumulator registers per block and lane
 #pragma unroll
     for (int i = 0; i < C::FN; ++i)
 #pragma unroll
         for (int j = 0; j < C::FM; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+            for (int r = 0; r < ACC_ELEMS; ++r) acc[i][j][r] = 0.0f;
 
     if constexpr (C::REG_STAGED)
         mainloop_rs<C>(p, lds, rsw, rsx, kt_begin, kt_end, acc);
@@ -1095,7 +1193,7 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
                 __hip_atomic_store(&p.counters[fix.tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return;
         }
-    } else if constexpr (MODE != GRID_TILES) {
+    } else if constexpr (MODE != GRID_TILES && C::BH == 32) {
         if (fix.nseg > 1) {
             // Park this unit's partial sums, then let the last arriving unit of
             // the tile finish it.

@@ -56,6 +56,22 @@ def test_swiglu_matches_oracle(hiplib, M, K, F, bias, out):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("cfg", [2, 8, 16, 17])
+def test_swiglu_on_every_swiglu_tile(hiplib, monkeypatch, cfg):
+    """The SwiGLU epilogue on each tile configuration that splits into gate | up wave columns:
+    32x32 MFMA blocks (2, 8) and 16x16 blocks (16, 17: a 16-row block finished 8 rows per wave)."""
+    monkeypatch.setenv("INV_HIP_TILE_CFG", str(cfg))
+    M, K, F = 333, 1000, 520
+    X, Wg, Wu, bg, bu = gen(23, M, K, F, True)
+    with q.Weight.gate_up(Wg, Wu, bg, bu) as w:
+        y = q.linear(as_bf16_bits(X), w, epilogue="swiglu", out_dtype="f32")
+    rows = sample_rows(M, 64)
+    err = oracle.normwise_err(y[rows], oracle_swiglu(round_bf16(X[rows]), Wg, Wu, bg, bu))
+    print(f"  cfg {cfg}: normwise err vs oracle {err:.3e}", flush=True)
+    assert np.all(np.isfinite(y)) and err <= TOL_TIGHT
+
+
+@pytest.mark.gpu
 def test_swiglu_equals_two_projections_and_silu_mul(hiplib):
     """The fused result against the unfused path through the same library."""
     M, K, F = 200, 640, 384
