@@ -289,6 +289,34 @@ def run_workload(name, steps, warmup, check=True, host_path=False, warmup_second
     return res
 
 
+def gemm_constant_operands(name, seconds=1.5, steps=200):
+    """The same GEMM launch with every X and W element 2^-7 (exact in bf16): identical instructions
+    and memory traffic, operands that do not toggle.  Its rate against the random-operand rate shows
+    how much of the gap to peak is the data-dependent power of the matrix cores."""
+    import ctypes
+    from invision_amd import hip
+    from invision_amd import quicknn_hip as q
+    from invision_amd.bf16 import as_bf16_bits
+    desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[name]
+    w = q.Weight(as_bf16_bits(np.full((N, K), 2.0 ** -7, np.float32)), np.zeros(N, np.float32) if has_bias else None)
+    xd = q.DeviceArray.from_host(as_bf16_bits(np.full((M, K), 2.0 ** -7, np.float32)), "bf16")
+    yd = q.DeviceArray((M, N), ydt)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(25):
+            q.linear_device(xd, w, yd, M, asynchronous=True)
+        hip.call("inv_hip_synchronize")
+    ms = ctypes.c_float()
+    hip.call("inv_hip_timer_start")
+    for _ in range(steps):
+        q.linear_device(xd, w, yd, M, asynchronous=True)
+    hip.call("inv_hip_timer_stop", ctypes.byref(ms))
+    ok = bool(np.all(yd.to_host()[:4] == np.float32(K * 2.0 ** -14)))  # exact: K products of 2^-14
+    for a in (w, xd, yd):
+        a.free()
+    return {"tflops": round(2.0 * M * N * K / (ms.value / steps * 1e-3) / 1e12, 1), "exact": ok}
+
+
 def mfma_ceiling(gemm_tflops):
     """The register-only MFMA loop of libinv_probe.so on this GPU, now: the rate a
     GEMM on the same operand distributions could reach with zero memory traffic
@@ -650,32 +678,63 @@ BUSY_COUNTERS = ("GRBM_GUI_ACTIVE SQ_BUSY_CU_CYCLES SQ_VALU_MFMA_BUSY_CYCLES SQ_
 L2_COUNTERS = "TCC_HIT_sum TCC_MISS_sum"
 
 
-def profile_commands(workload, trace_dir, fetch_dir, write_dir, busy_dir=None, l2_dir=None, cold=False):
-    """The rocprofv3 runs a profile summary is made from (run from /tmp): a kernel trace, FETCH_SIZE,
-    WRITE_SIZE, and optionally the activity counters and the L2 hit counters, each in its own pass."""
+def profile_passes(workload, out_dir, cold=False):
+    """The rocprofv3 runs a profile summary is made from, each in its own process started from /tmp:
+    (name, argv, time limit in s).  A kernel trace over the timed launches, then one counter pass
+    each for FETCH_SIZE, WRITE_SIZE, the activity counters and the L2 hit counters."""
     bench = os.path.join(ROOT, "bench.py")
-    run = f"python3 {bench} --profile-run --workload {workload}" + (" --cold" if cold else "")
-    extra = {}
-    if busy_dir:
-        extra["busy"] = (f"cd /tmp && export TMPDIR=/tmp && timeout -s KILL 90 rocprofv3 --pmc {BUSY_COUNTERS} "
-                         f"-d {busy_dir} -o {workload} --output-format csv -- {run} --steps 20 --warmup 5")
-    if l2_dir:
-        extra["l2"] = (f"cd /tmp && export TMPDIR=/tmp && timeout -s KILL 60 rocprofv3 --pmc {L2_COUNTERS} "
-                       f"-d {l2_dir} -o {workload} --output-format csv -- {run} --steps 5 --warmup 1 "
-                       f"--warmup-seconds 0")
-    return {**extra,
-        "trace": f"cd /tmp && export TMPDIR=/tmp && rocprofv3 --kernel-trace --stats -d {trace_dir} -o {workload} "
-                 f"--output-format csv -- {run} --steps 50 --warmup 5",
-        "fetch": f"cd /tmp && export TMPDIR=/tmp && timeout -s KILL 60 rocprofv3 --pmc FETCH_SIZE -d {fetch_dir} "
-                 f"-o {workload} --output-format csv -- {run} --steps 5 --warmup 1 --warmup-seconds 0",
-        "write": f"cd /tmp && export TMPDIR=/tmp && timeout -s KILL 60 rocprofv3 --pmc WRITE_SIZE -d {write_dir} "
-                 f"-o {workload} --output-format csv -- {run} --steps 5 --warmup 1 --warmup-seconds 0",
-    }
+    run = ["python3", bench, "--profile-run", "--workload", workload] + (["--cold"] if cold else [])
+    short = ["--steps", "5", "--warmup", "1", "--warmup-seconds", "0"]
+
+    def pmc(name, counters, tail, limit):
+        return (name, ["rocprofv3", "--pmc"] + counters.split() + ["-d", os.path.join(out_dir, name), "-o", workload,
+                                                                  "--output-format", "csv", "--"] + run + tail, limit)
+    return [("trace", ["rocprofv3", "--kernel-trace", "--stats", "-d", os.path.join(out_dir, "trace"), "-o", workload,
+                       "--output-format", "csv", "--"] + run + ["--steps", "50", "--warmup", "5"], 240),
+            pmc("fetch", "FETCH_SIZE", short, 90),
+            pmc("write", "WRITE_SIZE", short, 90),
+            pmc("busy", BUSY_COUNTERS, ["--steps", "20", "--warmup", "5", "--warmup-seconds", "0.5"], 120),
+            pmc("l2", L2_COUNTERS, short, 90)]
+
+
+def shown(argv):
+    """A pass's command line as the summaries print it (the repository root as <repo>)."""
+    return "cd /tmp && TMPDIR=/tmp " + " ".join(argv).replace(ROOT, "<repo>")
+
+
+def profile_all(workload, out_dir, cold=False):
+    """Run every pass of profile_passes() as a child process (this process never touches the GPU),
+    then write the profiles/ summary; the raw trace and counter tables are deleted afterwards."""
+    import glob
+    import subprocess
+    os.makedirs(out_dir, exist_ok=True)
+    env = dict(os.environ, TMPDIR="/tmp")
+    dirs = {}
+    for name, argv, limit in profile_passes(workload, out_dir, cold):
+        log(f"[profile-all] {workload}{' cold' if cold else ''}: {name} pass", )
+        logf = os.path.join(out_dir, name + ".log")
+        try:
+            with open(logf, "w") as lf:
+                rc = subprocess.run(argv, cwd="/tmp", env=env, stdout=lf, stderr=subprocess.STDOUT,
+                                    timeout=limit).returncode
+        except subprocess.TimeoutExpired:
+            log(f"[profile-all] {name} pass exceeded {limit} s; stopping")
+            return 1
+        if rc != 0:
+            log(f"[profile-all] {name} pass failed ({rc}):\n" + "".join(open(logf).readlines()[-15:]))
+            return 1
+        dirs[name] = os.path.join(out_dir, name)
+    summarize_profile(workload, dirs["trace"], dirs["fetch"], dirs["write"], dirs["busy"], dirs["l2"], cold=cold,
+                      out_dir=out_dir)
+    for pat in ("*kernel_trace.csv", "*counter_collection.csv", "*agent_info.csv"):
+        for f in glob.glob(os.path.join(out_dir, "**", pat), recursive=True):
+            os.remove(f)
+    return 0
 
 
 def summarize_profile(workload, trace_dir, fetch_dir, write_dir, busy_dir=None, l2_dir=None, cold=False,
-                      kernel="gemm_nt_bf16_kernel", steps=50):
-    """Turn the three rocprofv3 runs of profile_commands() into profiles/gemm_<workload>_<MxKxN>.md and
+                      kernel="gemm_nt_bf16_kernel", steps=50, out_dir=None):
+    """Turn the rocprofv3 runs of profile_passes() into profiles/gemm_<workload>_<MxKxN>.md and
     profiles/gemm_<workload>_traffic.json (HBM bytes per launch, read by the bench line's roofline).
 
     FETCH_SIZE / WRITE_SIZE are scaled by what they read for copy_words16 over 512 MiB (512 MiB read and
@@ -726,7 +785,8 @@ def summarize_profile(workload, trace_dir, fetch_dir, write_dir, busy_dir=None, 
     durs = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in trace]
     timed = durs[-(steps + 30):-30] if len(durs) > steps + 30 else durs
     avg_ns = float(sum(timed)) / len(timed)
-    cmds = profile_commands(workload, trace_dir, fetch_dir, write_dir, busy_dir, l2_dir, cold)
+    passes = {name: shown(argv) for name, argv, _ in profile_passes(workload, os.path.dirname(trace_dir), cold)}
+    cmds = {k: passes[k] for k in ("trace", "fetch", "write", "busy", "l2")}
     tfl = flops / avg_ns / 1e3
     lines = [f"# {workload}: {desc}, Y[{M}x{N}] = X[{M}x{K}] . W[{N}x{K}]^T (rocprofv3)", "",
              "Kernel trace and stats:", "", "```", cmds["trace"], "```", "",
@@ -754,27 +814,27 @@ def summarize_profile(workload, trace_dir, fetch_dir, write_dir, busy_dir=None, 
         bc = named_counters(busy_dir, kernel)
         med = lambda c: statistics.median(v for v, _ in bc[c])
         dur = statistics.median(d for _, d in bc["GRBM_GUI_ACTIVE"])
-        gui = med("GRBM_GUI_ACTIVE")
-        # GRBM_GUI_ACTIVE sums the busy cycles of the 8 XCDs (a copy kernel reads 2.4-2.45 GHz this way)
-        clock_ghz = gui / 8.0 / dur
         cus = 256
-        cyc = gui / 8.0  # per-XCD busy cycles of the dispatch
-        mfma_busy = med("SQ_VALU_MFMA_BUSY_CYCLES") / (cyc * cus * 4)
+        mfma_cyc = med("SQ_VALU_MFMA_BUSY_CYCLES") / (cus * 4)  # per SIMD
         mops = med("SQ_INSTS_VALU_MFMA_MOPS_BF16") * 512.0
-        cu_busy = med("SQ_BUSY_CU_CYCLES") / (cyc * cus)
-        extra = {"clock_ghz": clock_ghz, "mfma_busy_frac": mfma_busy, "mfma_flops_counted": mops,
-                 "flops_expected": flops, "cu_busy_frac": cu_busy, "counter_pass_duration_ns": dur}
+        waves = med("SQ_WAVE_CYCLES")
+        extra = {"mfma_busy_cycles_per_simd": mfma_cyc, "mfma_flops_counted": mops, "flops_expected": flops,
+                 "lds_wait_frac_of_wave_cycles": med("SQ_WAIT_INST_LDS") / waves,
+                 "lds_bank_conflicts": med("SQ_LDS_BANK_CONFLICT"), "counter_pass_duration_ns": dur}
         lines += ["Activity counters (one pass, their own run):", "", "```", cmds["busy"], "```", "",
                   "| Counter | Median per dispatch |", "|---|---|"]
         lines += [f"| {c} | {med(c):.4g} |" for c in sorted(bc)]
-        lines += ["", f"- Dispatch duration under counter collection: {dur / 1e3:.1f} us (the trace above times "
-                      f"dispatches without counters).",
-                  f"- Effective clock: GRBM_GUI_ACTIVE / 8 XCDs / duration = {clock_ghz:.2f} GHz.",
-                  f"- MFMA busy: SQ_VALU_MFMA_BUSY_CYCLES / (busy cycles x {cus} CUs x 4 SIMDs) = "
-                  f"{mfma_busy * 100:.1f}% of the dispatch's cycles.",
-                  f"- Work check: SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 = {mops:.4g} FLOP against 2*M*N*K = "
-                  f"{flops:.4g} ({mops / flops:.3f}x; tiles past the edges multiply zero padding).",
-                  f"- CU busy: SQ_BUSY_CU_CYCLES / (busy cycles x {cus}) = {cu_busy * 100:.1f}%.", ""]
+        lines += ["", f"- Work check: SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 = {mops:.4g} FLOP against 2*M*N*K = "
+                      f"{flops:.4g} ({mops / flops:.3f}x; tiles past the matrix edges multiply zero padding).",
+                  f"- MFMA pipe: SQ_VALU_MFMA_BUSY_CYCLES / ({cus} CUs x 4 SIMDs) = {mfma_cyc:.4g} busy cycles per "
+                  f"SIMD (the MFMA count times its issue cycles); over the {avg_ns / 1e3:.1f} us launch that is "
+                  f"{mfma_cyc / (avg_ns * 2.4) * 100:.1f}% of the cycles at the 2.4 GHz peak clock "
+                  f"(= the fraction of dense peak) and {mfma_cyc / (avg_ns * 1.7) * 100:.1f}% at 1.7 GHz, the "
+                  f"clock the chip holds under random-operand MFMA load.",
+                  f"- LDS: SQ_WAIT_INST_LDS is {extra['lds_wait_frac_of_wave_cycles'] * 100:.1f}% of "
+                  f"SQ_WAVE_CYCLES; {extra['lds_bank_conflicts']:.0f} bank-conflict cycles.",
+                  f"- GRBM_GUI_ACTIVE spans the counting window, which extends past the dispatch, so no clock is "
+                  f"derived from it.", ""]
     if l2_dir:
         lc = named_counters(l2_dir, kernel)
         hit = statistics.median(v for v, _ in lc["TCC_HIT_sum"])
@@ -794,6 +854,10 @@ def summarize_profile(workload, trace_dir, fetch_dir, write_dir, busy_dir=None, 
                **extra,
                "note": "bytes between L2 and the fabric (HBM or Infinity Cache); counters scaled by a copy "
                        "kernel of known size"}, open(tj, "w"), indent=1)
+    if out_dir:
+        import shutil
+        shutil.copy(md, out_dir)
+        shutil.copy(tj, out_dir)
     print(open(md).read())
     return 0
 
@@ -818,8 +882,13 @@ def main():
                     help="with --profile-run: rotate over weight copies larger than twice the Infinity Cache")
     ap.add_argument("--summarize-profile", nargs="+", metavar="DIR",
                     help="TRACE_DIR FETCH_DIR WRITE_DIR [BUSY_DIR [L2_DIR]]: write profiles/ summaries for "
-                         "--workload from the rocprofv3 runs of profile_commands() (no GPU needed)")
+                         "--workload from the rocprofv3 runs of profile_passes() (no GPU needed)")
+    ap.add_argument("--profile-all", metavar="OUT_DIR",
+                    help="run every rocprofv3 pass for --workload (child processes; raw output under OUT_DIR) and "
+                         "write its profiles/ summary")
     args = ap.parse_args()
+    if args.profile_all:
+        return profile_all(args.workload, os.path.abspath(args.profile_all), cold=args.cold)
     if args.summarize_profile:
         dirs = list(args.summarize_profile) + [None] * (5 - len(args.summarize_profile))
         return summarize_profile(args.workload, *dirs[:5], cold=args.cold)
@@ -860,6 +929,11 @@ def main():
         failed += [r["name"] for r in extra if not r.get("parity_ok", True)]
 
     ceiling = None if args.no_mfma_ceiling else mfma_ceiling(res["tflops_kernel"])
+    if ceiling is not None and WORKLOADS[args.workload][5] == "none" and WORKLOADS[args.workload][6] == "bf16":
+        const = gemm_constant_operands(args.workload)
+        ceiling["gemm_constant_operands_tflops"] = const["tflops"]
+        ceiling["gemm_constant_operands_exact"] = const["exact"]
+        log(f"[bench] GEMM with constant operands: {const}")
     desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[args.workload]
     achieved = res["tflops_kernel"]
     traffic = None
