@@ -304,16 +304,18 @@ struct Rs16Cfg {
 #if defined(__HIP_DEVICE_COMPILE__)
 
 // LDS slot key of row r (depends on r mod 16 only, so the copy side and the
-// fragment side can both compute it from their low row bits).
-//  8 slots (128-byte rows): rows r and r+8 of an aligned 16-row window differ
-//    by one slot, and the 8 rows of each parity get 8 different slots;
+// fragment side can both compute it from their low row bits); chunk c of row r
+// is stored in slot c ^ key(r).
+//  8 slots (128-byte rows): key = (r >> 1) & 7.  Measured on gfx950 with the
+//    SQ_LDS_BANK_CONFLICT counter over ds_read_b128 of both fragment shapes
+//    (32x32x16: rows lane % 32, chunk lane / 32; 16x16x32: rows lane % 16,
+//    chunk lane / 16): no conflict cycles for either.  (r + ((r >> 3) & 1)) & 7
+//    is conflict-free for the first shape only, r & 7 for the second only.
 //  4 slots (64-byte rows): rows r, r+4, r+8, r+12 get 4 different slots.
-// Either way the 16 rows read by 16 consecutive lanes land on 16 different
-// 16-byte bank groups of the 256-byte bank window.
 template <int SLOTS>
 __device__ __forceinline__ int slot_key(int r) {
     if constexpr (SLOTS == 8)
-        return (r + ((r >> 3) & 1)) & 7;
+        return (r >> 1) & 7;
     else
         return (r >> 2) & 3;
 }

@@ -399,8 +399,11 @@ int cfg_occupancy(const CfgMeta &m) { return std::max(1, std::min(2, (160 * 1024
 // Pick a tile shape and how the grid covers it (rules from measurements on
 // MI355X, 256 CUs):
 //  - at least 3/4 of a round of 256x256 tiles: the 256x256 register-staged tile
-//    (configuration 8), whose energy per FLOP is lowest; a partial last round
-//    costs little because the chip clocks up while CUs idle;
+//    on 32x32 MFMAs (configuration 8) or the 256x224 one on 16x16 MFMAs
+//    (configuration 16), by last-round fill and edge padding: sustained, c2
+//    1131 -> 1190 TFLOP/s (756 tiles = 2.95 rounds against 648 = 2.53),
+//    4608x9216x3072 1217 -> 1315, 9216x15360x3840 1040 -> 1126, and
+//    9216x3840x11520 1170 against 1150 (both fill their last round alike);
 //  - M <= 128 and half a round of 256x128 tiles: configuration 13, whose 128 X
 //    rows cover M (a 256x256 tile would spend half its MFMAs on zero rows);
 //  - else half a round of 256x128 tiles (configuration 13: 256 W rows, 128 X
@@ -425,7 +428,16 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
     } else if (M <= 128 && tiles_of(13) * 2 >= cus) {
         c.cfg = 13;  // 128 X rows cover M: a 256-row tile would multiply zeros for half its MFMAs
     } else if (tiles_of(8) * 4 >= (int64_t)cus * 3) {
-        c.cfg = 8;
+        // 256x256 tiles on 32x32 MFMAs (8) or 256x224 on 16x16 (16), whichever leaves fewer
+        // CUs idle in the last round and fewer MFMAs on zero padding at the edges; 16 runs a
+        // full round about 2% slower (measured at equal fill).
+        auto score = [&](int cfg) {
+            const int64_t tm = (M + kCfg[cfg].tm - 1) / kCfg[cfg].tm, tn = (N + kCfg[cfg].tn - 1) / kCfg[cfg].tn;
+            const int64_t t = tm * tn, rounds = (t + cus - 1) / cus;
+            return (double)t / (double)(rounds * cus) * (double)M / (double)(tm * kCfg[cfg].tm) * (double)N /
+                   (double)(tn * kCfg[cfg].tn);
+        };
+        c.cfg = (0.98 * score(16) > score(8)) ? 16 : 8;
     } else if (tiles_of(13) * 2 >= cus) {
         c.cfg = 13;
     } else {

@@ -165,8 +165,8 @@ GRID_MODES = {  # INV_HIP_MODE / INV_HIP_KSPLIT / INV_HIP_SK_GRID
 }
 
 
-ALL_CFGS = list(range(18))  # INV_GEMM_NUM_CONFIGS in invision_amd/csrc/gemm_configs.hpp
-REG_STAGED_CFGS = [8, 9, 10, 11, 12, 13, 14, 15, 16, 17]  # 11-14, 16-17: unequal W and X copy-chunk counts
+ALL_CFGS = list(range(17))  # INV_GEMM_NUM_CONFIGS in invision_amd/csrc/gemm_configs.hpp
+REG_STAGED_CFGS = [8, 9, 10, 11, 12, 13, 14, 15, 16]  # 11-14, 16: unequal W and X copy-chunk counts
 
 
 @pytest.mark.parametrize("cfg", ALL_CFGS)

@@ -56,10 +56,10 @@ def test_swiglu_matches_oracle(hiplib, M, K, F, bias, out):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("cfg", [2, 8, 16, 17])
+@pytest.mark.parametrize("cfg", [2, 8, 16])
 def test_swiglu_on_every_swiglu_tile(hiplib, monkeypatch, cfg):
     """The SwiGLU epilogue on each tile configuration that splits into gate | up wave columns:
-    32x32 MFMA blocks (2, 8) and 16x16 blocks (16, 17: a 16-row block finished 8 rows per wave)."""
+    32x32 MFMA blocks (2, 8) and 16x16 blocks (16: a 16-row block finished 8 rows per wave)."""
     monkeypatch.setenv("INV_HIP_TILE_CFG", str(cfg))
     M, K, F = 333, 1000, 520
     X, Wg, Wu, bg, bu = gen(23, M, K, F, True)
