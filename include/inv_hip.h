@@ -100,7 +100,11 @@ typedef struct inv_weight_s *inv_weight_t; /* opaque device-resident weight */
 /* ---- lifetime ------------------------------------------------------------- */
 /* Select device `device` (ordinal among visible devices), check it is gfx950,
  * create the library stream.  Returns INV_ERR_NO_DEVICE when there is none, so
- * the caller keeps its CPU GEMM bound (src/quicknncpu.pas:3951-3955). */
+ * the caller keeps its CPU GEMM bound (src/quicknncpu.pas:3951-3955).  With
+ * INV_HIP_ALLOC_LIMIT_MB set in the environment, the device memory the library
+ * allocates from then on (workspaces, weights, inv_hip_malloc) is capped at
+ * that many MiB: a call that would pass the cap returns INV_ERR_OOM, as one
+ * whose hipMalloc fails does. */
 int inv_hip_init(int device);
 /* Free every weight, workspace and the stream (src/quicknncpu.pas:4073-4086). */
 int inv_hip_shutdown(void);
@@ -314,8 +318,13 @@ int inv_hip_attention_qk_norm_rope(const float *Q, int64_t ldq, const float *K, 
  * reference's [out_ch x in_ch*kH*kW] fp32 filter (inv_hip_weight_upload_f32,
  * N = out_ch, K = in_ch*kH*kW); bias [out_ch] (null: the handle's, if any).
  * The image is rounded to bf16 (RNE) into a patch matrix and multiplied with
- * fp32 accumulation.  flags: INV_FLAG_DEVICE_PTRS (src, dst, bias on the
- * device), INV_FLAG_ASYNC. */
+ * fp32 accumulation; an fp32 filter was rounded to bf16 by its upload too.
+ * Normwise deviation from the fp32 convolution: 1.5e-3 to 2.1e-3 with a
+ * bf16-exact filter, 2.2e-3 to 3.2e-3 with an fp32 one (the two roundings).
+ * The output follows the convolution's definition; the reference's default
+ * im2col loop differs from it for stride-1 shapes with padding != (kW-1)/2 and
+ * for 1x1 filters with stride or padding (src/quicknncpu.pas:2063-2110).
+ * flags: INV_FLAG_DEVICE_PTRS (src, dst, bias on the device), INV_FLAG_ASYNC. */
 int inv_hip_conv2d(const float *src, inv_weight_t weight, const float *bias, float *dst, int64_t in_ch,
                    int64_t out_ch, int64_t H, int64_t W, int64_t kH, int64_t kW, int64_t stride,
                    int64_t padding, int64_t batch, int flags);

@@ -26,6 +26,7 @@
 #include <mutex>
 #include <string>
 #include <thread>
+#include <unordered_map>
 #include <vector>
 
 #include "attention.hpp"
@@ -194,6 +195,13 @@ struct State {
     double gemm_ms = 0.0, flops = 0.0;
     std::vector<inv_weight_s *> weights;
     unsigned char *scratch = nullptr;  // device address of `scratch` on g.device
+    // Device memory the library holds (workspaces, weights, inv_hip_malloc
+    // buffers), and an optional cap on it (INV_HIP_ALLOC_LIMIT_MB at
+    // inv_hip_init; 0: none): an allocation past the cap fails with
+    // INV_ERR_OOM as a failed hipMalloc would.
+    std::unordered_map<void *, size_t> allocs;
+    size_t alloc_bytes = 0, alloc_cap = 0;
+    size_t alloc_base = 0;  // bytes held when inv_hip_init ran (the cap counts from there)
     // The device weight cache: one entry per (file identity, tensor, bias, flags).
     struct CacheEntry {
         std::string key;
@@ -249,20 +257,44 @@ namespace {
 inline int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// Every device allocation of the library goes through dev_alloc / dev_free
+// (the cap and the byte count).  uncached: hipDeviceMallocUncached memory.
+int dev_alloc(void **p, size_t bytes, const char *what, bool uncached = false) {
+    *p = nullptr;
+    if (g.alloc_cap && g.alloc_bytes - g.alloc_base + bytes > g.alloc_cap)
+        return fail(INV_ERR_OOM, "%s: %zu bytes would exceed the allocation cap (INV_HIP_ALLOC_LIMIT_MB: %zu of "
+                    "%zu bytes in use)", what, bytes, g.alloc_bytes - g.alloc_base, g.alloc_cap);
+    const hipError_t e = uncached ? hipExtMallocWithFlags(p, bytes, hipDeviceMallocUncached) : hipMalloc(p, bytes);
+    if (e != hipSuccess || !*p) {
+        (void)hipGetLastError();
+        *p = nullptr;
+        return fail(INV_ERR_OOM, "%s: device allocation of %zu bytes failed", what, bytes);
+    }
+    g.allocs[*p] = bytes;
+    g.alloc_bytes += bytes;
+    return INV_OK;
+}
+
+void dev_free(void *p) {
+    if (!p) return;
+    auto it = g.allocs.find(p);
+    if (it != g.allocs.end()) {
+        g.alloc_bytes -= it->second;
+        g.allocs.erase(it);
+    }
+    (void)hipFree(p);
+}
+
 int ensure(Buf &b, size_t bytes) {
     if (b.cap >= bytes) return INV_OK;
     if (b.p) {
         HIPCHK(hipStreamSynchronize(g.stream));
-        HIPCHK(hipFree(b.p));
+        dev_free(b.p);
         b.p = nullptr;
         b.cap = 0;
     }
     size_t nb = (size_t)round_up((int64_t)std::max<size_t>(bytes, 1), 2 << 20);
-    if (hipMalloc(&b.p, nb) != hipSuccess) {
-        (void)hipGetLastError();
-        b.p = nullptr;
-        return fail(INV_ERR_OOM, "device allocation of %zu bytes failed", nb);
-    }
+    TRY(dev_alloc(&b.p, nb, "workspace"));
     b.cap = nb;
     return INV_OK;
 }
@@ -272,10 +304,7 @@ int ensure_uncached(Buf &b, size_t bytes, bool zero) {
     if (b.cap >= bytes) return INV_OK;
     size_t nb = (size_t)round_up((int64_t)std::max<size_t>(bytes, 1), 2 << 20);
     void *p = nullptr;
-    if (hipExtMallocWithFlags(&p, nb, hipDeviceMallocUncached) != hipSuccess) {
-        (void)hipGetLastError();
-        return fail(INV_ERR_OOM, "uncached device allocation of %zu bytes failed", nb);
-    }
+    TRY(dev_alloc(&p, nb, "split-K workspace", true));
     if (zero) HIPCHK(hipMemsetAsync(p, 0, nb, g.stream));
     if (b.p) g.retired_uncached.push_back(b.p);
     b.p = p;
@@ -284,7 +313,7 @@ int ensure_uncached(Buf &b, size_t bytes, bool zero) {
 }
 
 void release(Buf &b) {
-    if (b.p) (void)hipFree(b.p);
+    dev_free(b.p);
     b.p = nullptr;
     b.cap = 0;
 }
@@ -651,13 +680,10 @@ int upload_bias(const float *bias, int64_t N, float **out) {
     *out = nullptr;
     if (!bias) return INV_OK;
     float *d = nullptr;
-    if (hipMalloc(&d, (size_t)N * 4) != hipSuccess) {
-        (void)hipGetLastError();
-        return fail(INV_ERR_OOM, "bias allocation failed");
-    }
+    TRY(dev_alloc((void **)&d, (size_t)N * 4, "bias"));
     int rc = h2d_rows(d, bias, 1, (size_t)N * 4, (size_t)N * 4);
     if (rc) {
-        (void)hipFree(d);
+        dev_free(d);
         return rc;
     }
     *out = d;
@@ -673,10 +699,7 @@ int weight_upload_impl(const void *w, bool is_f32, int64_t N, int64_t K, const f
     if (N > INT32_MAX / 2 || K > INT32_MAX / 2) return fail(INV_ERR_ARG, "weight too large");
     const int64_t ldw = round_up(K, 8);
     uint16_t *dw = nullptr;
-    if (hipMalloc(&dw, (size_t)(N * ldw) * 2) != hipSuccess) {
-        (void)hipGetLastError();
-        return fail(INV_ERR_OOM, "weight allocation of %lld bytes failed", (long long)(N * ldw * 2));
-    }
+    TRY(dev_alloc((void **)&dw, (size_t)(N * ldw) * 2, "weight"));
     int rc = INV_OK;
     if (is_f32) {
         rc = ensure(g.win, (size_t)(N * K) * 4);
@@ -696,8 +719,8 @@ int weight_upload_impl(const void *w, bool is_f32, int64_t N, int64_t K, const f
         if (e != hipSuccess) rc = fail(INV_ERR_HIP, "weight upload: %s", hipGetErrorString(e));
     }
     if (rc) {
-        (void)hipFree(dw);
-        if (db) (void)hipFree(db);
+        dev_free(dw);
+        dev_free(db);
         return rc;
     }
     auto *h = new inv_weight_s{kWeightMagic, dw, db, N, K, ldw, 0, N};
@@ -753,8 +776,8 @@ int cache_key(const char *path, const char *name, const char *bias_name, int fla
 }
 
 void free_weight(inv_weight_s *w) {
-    if (w->w) (void)hipFree(w->w);
-    if (w->bias) (void)hipFree(w->bias);
+    dev_free(w->w);
+    dev_free(w->bias);
     w->magic = 0;
     delete w;
 }
@@ -1547,7 +1570,16 @@ int inv_hip_init(int device) {
     g.device = device;
     g.cu_count = prop.multiProcessorCount;
     g.clock_khz = prop.clockRate;
-    snprintf(g.name, sizeof g.name, "%s (%s)", prop.name, prop.gcnArchName);
+    g.alloc_cap = (size_t)std::max(0, env_int("INV_HIP_ALLOC_LIMIT_MB", 0)) << 20;
+    g.alloc_base = g.alloc_bytes;
+    // the product name when the runtime reports one, else the architecture and CU count
+    char pname[256] = {0};
+    if (hipDeviceGetName(pname, sizeof pname, device) != hipSuccess) (void)hipGetLastError();
+    const char *nm = pname[0] ? pname : prop.name;
+    if (nm[0])
+        snprintf(g.name, sizeof g.name, "%s (%s)", nm, prop.gcnArchName);
+    else
+        snprintf(g.name, sizeof g.name, "AMD GPU %s, %d CUs", prop.gcnArchName, prop.multiProcessorCount);
     // host copy threads: INV_HIP_COPY_THREADS, else up to 8 of the host's
     const char *ct = getenv("INV_HIP_COPY_THREADS");
     const int hw = (int)std::max(1u, std::thread::hardware_concurrency());
@@ -1614,10 +1646,7 @@ int inv_hip_weight_upload_gate_up(const uint16_t *gate_bf16, const uint16_t *up_
     if (F > INT32_MAX / 8 || K > INT32_MAX / 2) return fail(INV_ERR_ARG, "gate/up weight too large");
     const int64_t ldw = round_up(K, 8), fpad = round_up(F, 128), rows = 2 * fpad;
     uint16_t *dw = nullptr;
-    if (hipMalloc(&dw, (size_t)(rows * ldw) * 2) != hipSuccess) {
-        (void)hipGetLastError();
-        return fail(INV_ERR_OOM, "gate/up weight allocation of %lld bytes failed", (long long)(rows * ldw * 2));
-    }
+    TRY(dev_alloc((void **)&dw, (size_t)(rows * ldw) * 2, "gate/up weight"));
     int rc = INV_OK;
     if (hipMemsetAsync(dw, 0, (size_t)(rows * ldw) * 2, g.stream) != hipSuccess)
         rc = fail(INV_ERR_HIP, "gate/up weight: clearing failed");
@@ -1652,8 +1681,8 @@ int inv_hip_weight_upload_gate_up(const uint16_t *gate_bf16, const uint16_t *up_
         if (e != hipSuccess) rc = fail(INV_ERR_HIP, "gate/up weight upload: %s", hipGetErrorString(e));
     }
     if (rc) {
-        (void)hipFree(dw);
-        if (db) (void)hipFree(db);
+        dev_free(dw);
+        dev_free(db);
         return rc;
     }
     auto *h = new inv_weight_s{kWeightMagic, dw, db, F, K, ldw, 1, rows};
@@ -1875,13 +1904,7 @@ int inv_hip_malloc(void **ptr, size_t bytes) {
     std::lock_guard<std::mutex> lk(g_mu);
     TRY(check_init());
     if (!ptr) return fail(INV_ERR_ARG, "malloc: null out pointer");
-    *ptr = nullptr;
-    if (hipMalloc(ptr, std::max<size_t>(bytes, 1)) != hipSuccess) {
-        (void)hipGetLastError();
-        *ptr = nullptr;
-        return fail(INV_ERR_OOM, "device allocation of %zu bytes failed", bytes);
-    }
-    return INV_OK;
+    return dev_alloc(ptr, std::max<size_t>(bytes, 1), "malloc");
 }
 
 int inv_hip_free(void *ptr) {
@@ -1889,7 +1912,8 @@ int inv_hip_free(void *ptr) {
     TRY(check_init());
     if (!ptr) return INV_OK;
     HIPCHK(hipStreamSynchronize(g.stream));
-    HIPCHK(hipFree(ptr));
+    if (!g.allocs.count(ptr)) return fail(INV_ERR_ARG, "free: %p was not allocated by inv_hip_malloc", ptr);
+    dev_free(ptr);
     return INV_OK;
 }
 

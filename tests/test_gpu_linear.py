@@ -389,3 +389,92 @@ def test_error_paths_return_status_not_abort(hiplib):
     # M = 0 is a no-op
     with q.Weight(W) as w:
         assert lib.inv_hip_linear(X.ctypes.data, 3, w.handle, None, y.ctypes.data, 3, 0, 16, 8, 0, 0) == hip.INV_OK
+
+
+# ------------------------------------------------------------ failure handling
+
+def test_allocation_cap_returns_oom_from_every_entry_point(hiplib, monkeypatch):
+    """INV_HIP_ALLOC_LIMIT_MB caps what the library allocates after inv_hip_init: the linear layer,
+    attention and convolution entry points report INV_ERR_OOM (with the cap in the message) where
+    their staging would pass it, and nothing is left half-done (the reference's bind-time fallback,
+    src/quicknncpu.pas:3951-3980, needs a clean status to fall back on)."""
+    import ctypes
+    lib = hip.load()
+    q.shutdown()
+    monkeypatch.setenv("INV_HIP_ALLOC_LIMIT_MB", "48")
+    try:
+        q.init()
+        X, W, b = gen(41, 64, 256, 128)
+        with q.Weight(W, b) as w:  # small: under the cap
+            y = q.linear(X, w)
+            check(y, X, W, b)
+        # fp32 X of 4096 x 4096 needs a 64 MiB staging buffer: refused
+        M = K = 4096
+        Xb = np.zeros((M, K), np.float32)
+        Wb = np.zeros((16, K), np.uint16)
+        with q.Weight(Wb) as w:
+            Y = np.zeros((M, 16), np.float32)
+            rc = lib.inv_hip_linear(Xb.ctypes.data, hip.INV_DT_F32, w.handle, None, Y.ctypes.data, hip.INV_DT_F32,
+                                    M, K, 16, 0, 0)
+            assert rc == hip.INV_ERR_OOM and "INV_HIP_ALLOC_LIMIT_MB" in hip.last_error(), hip.last_error()
+        # attention over 8192 tokens x 16 heads x 128 needs ~3 x 32 MiB of staged operands
+        S, H, D = 8192, 16, 128
+        Q = np.zeros((S, H * D), np.float32)
+        O = np.zeros((S, H * D), np.float32)
+        rc = lib.inv_hip_attention(Q.ctypes.data, Q.ctypes.data, Q.ctypes.data, O.ctypes.data, hip.INV_DT_F32,
+                                   hip.INV_DT_F32, H, H, S, S, D, ctypes.c_float(0.088), 0)
+        assert rc == hip.INV_ERR_OOM and "INV_HIP_ALLOC_LIMIT_MB" in hip.last_error(), hip.last_error()
+        # a convolution whose patch matrix (64 x 9 x 512 x 512 x 2 bytes) passes the cap
+        cin, cout, HW = 64, 8, 512
+        with q.Weight(np.zeros((cout, cin * 9), np.float32)) as wc:
+            img = np.zeros((1, cin, HW, HW), np.float32)
+            out = np.zeros((1, cout, HW, HW), np.float32)
+            rc = lib.inv_hip_conv2d(img.ctypes.data, wc.handle, None, out.ctypes.data, cin, cout, HW, HW, 3, 3, 1, 1,
+                                    1, 0)
+            assert rc == hip.INV_ERR_OOM and "INV_HIP_ALLOC_LIMIT_MB" in hip.last_error(), hip.last_error()
+        # a weight past the cap, and a device buffer past it
+        h = ctypes.c_void_p()
+        big = np.zeros((8192, 4096), np.uint16)  # 64 MiB
+        assert lib.inv_hip_weight_upload(big.ctypes.data, 8192, 4096, None, ctypes.byref(h)) == hip.INV_ERR_OOM
+        p = ctypes.c_void_p()
+        assert lib.inv_hip_malloc(ctypes.byref(p), 64 << 20) == hip.INV_ERR_OOM
+        # the library still works within the cap
+        with q.Weight(W, b) as w:
+            np.testing.assert_array_equal(q.linear(X, w), y)
+    finally:
+        q.shutdown()
+        monkeypatch.delenv("INV_HIP_ALLOC_LIMIT_MB")
+        q.init()
+
+
+def test_concurrent_calls_are_serialized_and_correct(hiplib):
+    """Two host threads calling inv_hip_linear on shared weight handles at once (the reference's
+    shared workspace is not safe under concurrency, src/quicknncpu.pas:117, 1842-1844): every call
+    returns the same result as a sequential call, and none fails."""
+    import threading
+    X1, W1, b1 = gen(42, 300, 1000, 520)
+    X2, W2, b2 = gen(43, 640, 2048, 1536)
+    with q.Weight(W1, b1) as w1, q.Weight(W2, b2) as w2:
+        ref1, ref2 = q.linear(X1, w1), q.linear(X2, w2, epilogue="silu")
+        errors, results = [], {}
+
+        def worker(tag, x, w, epi, ref, n):
+            try:
+                for i in range(n):
+                    y = q.linear(x, w, epilogue=epi)
+                    if not np.array_equal(y, ref):
+                        errors.append(f"{tag} call {i}: result differs")
+                results[tag] = n
+            except Exception as e:  # noqa: BLE001 - reported below
+                errors.append(f"{tag}: {e}")
+
+        threads = [threading.Thread(target=worker, args=("a", X1, w1, "none", ref1, 25)),
+                   threading.Thread(target=worker, args=("b", X2, w2, "silu", ref2, 25)),
+                   threading.Thread(target=worker, args=("c", X1, w1, "none", ref1, 25))]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join(timeout=120)
+        assert not any(t.is_alive() for t in threads), "a worker did not finish"
+        assert not errors, errors
+        assert results == {"a": 25, "b": 25, "c": 25}
