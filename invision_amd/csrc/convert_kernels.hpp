@@ -428,6 +428,22 @@ __global__ void __launch_bounds__(256) transpose64_to_bf16(const SrcT *__restric
 // is one image [C x H x W] fp32; ldc % 64 == 0 and col 16-byte aligned; grid
 // (ceil(npix / (64 * IM2COL_PG)), ldc / 64).
 constexpr int IM2COL_PG = 4;
+
+// Filter columns from the reference's order (k = ic * taps + tap, the
+// im2col order above) to tap-major (k = tap * C + ic), the order of the
+// implicit convolution's k-tiles: dst [rows x C*taps] (pitch C*taps) from src
+// [rows x lds]; total = rows * C * taps.
+__global__ void __launch_bounds__(256) conv_filter_tap_major(const uint16_t *__restrict__ src, int64_t lds,
+                                                             uint16_t *__restrict__ dst, int C, int taps,
+                                                             int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const int64_t K = (int64_t)C * taps;
+    const int64_t o = i / K;
+    const int k = (int)(i - o * K);
+    const int t = k / C, c = k - t * C;
+    dst[i] = src[o * lds + (int64_t)c * taps + t];
+}
 __global__ void __launch_bounds__(512) im2col_bf16(const float *__restrict__ src, uint16_t *__restrict__ col, int H,
                                                    int W, int kH, int kW, int stride, int pad, int outW, int oh0,
                                                    int64_t npix, int K, int64_t ldc) {
@@ -491,6 +507,144 @@ __global__ void __launch_bounds__(512) im2col_bf16(const float *__restrict__ src
         if (p0 + row < npix)
             *(uint4 *)(col + (p0 + row) * ldc + (int64_t)blockIdx.y * 64 + c * 8) =
                 *(const uint4 *)(tile + row * PITCH + c * 8);
+    }
+}
+
+// A 3x3, stride-1 convolution with few output channels (the VAE's conv_out,
+// 128 -> 3), computed directly: the im2col path would write a patch matrix
+// 9 * in_ch times larger than the image for a GEMM whose M is 3.  A 256-thread
+// workgroup makes a CT_TH x CT_TW output tile of one image (4 consecutive
+// pixels of one row per thread) for all OC (>= n_oc) output channels.  Input
+// channels go CT_CC at a time through an LDS tile of the (CT_TH + 2) x
+// (CT_TW + 2) input window, each value rounded to bf16 (RNE) as the patch
+// matrix rounds it, and multiplied in fp32 with the filter's bf16 values (the
+// weight handle's rows, [out_ch x in_ch*9] in the reference's (ic, kh, kw)
+// order, row pitch ldw), so results match the im2col path but for the fp32
+// summation order.  The chunk's filter values sit in LDS too, OC consecutive
+// per tap, so each tap's are one broadcast read.  The loads of chunk c + 1
+// (image and filter) are issued before the multiplies of chunk c and written
+// to LDS after them: the kernel streams the image at the rate of its loads in
+// flight, not of one row's latency at a time.
+// grid (ceil(outW / CT_TW), ceil(outH / CT_TH), batch).
+constexpr int CT_TH = 16, CT_TW = 64, CT_CC = 8;
+template <int OC>
+__global__ void __launch_bounds__(256) conv3x3_thin(const float *__restrict__ src, const uint16_t *__restrict__ filt,
+                                                    int64_t ldw, const float *__restrict__ bias,
+                                                    float *__restrict__ dst, int C, int H, int W, int pad, int n_oc,
+                                                    int outH, int outW) {
+    constexpr int TR = CT_TH + 2, TC = CT_TW + 2, PITCH = CT_TW + 4;  // PITCH: 16-byte aligned rows
+    constexpr int RPW = CT_CC * TR / 4;                               // window rows per wave and chunk
+    constexpr int NH = CT_CC * TR * (TC - 64);                        // halo values (columns 64..TC-1) per chunk
+    constexpr int HPT = (NH + 255) / 256;                             // of them per thread
+    constexpr int NW = CT_CC * 9 * OC;                                // filter values per chunk
+    constexpr int WPT = (NW + 255) / 256;                             // of them per thread
+    static_assert(RPW * 4 == CT_CC * TR && TC - 64 == 2, "window rows split evenly over the waves");
+    __shared__ __attribute__((aligned(16))) float tile[CT_CC][TR][PITCH];
+    __shared__ __attribute__((aligned(16))) float wts[CT_CC][9][OC];
+    // wave-uniform row bookkeeping in scalar registers; a lane adds its column
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int oh0 = blockIdx.y * CT_TH, ow0 = blockIdx.x * CT_TW;
+    const int b = blockIdx.z;
+    const float *img = src + (int64_t)b * C * H * W;
+    const int ty = tid >> 4, tx = (tid & 15) * 4;
+    const int iw = ow0 - pad + lane;
+    const bool cin = (unsigned)iw < (unsigned)W;
+    float v[RPW], v2[HPT], fw[WPT];
+    // issue chunk c0's loads into v (window columns 0..63, one row per wave
+    // and step), v2 (the two halo columns, two values per window row, spread
+    // over all threads) and fw
+    auto load = [&](int c0) {
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const int row = wave + 4 * i;
+            const int ch = row / TR, r = row - ch * TR;
+            const int ic = c0 + ch, ih = oh0 - pad + r;
+            const bool rin = ic < C && (unsigned)ih < (unsigned)H;
+            const float *rp = img + (rin ? ((int64_t)ic * H + ih) * W : 0);
+            v[i] = rin && cin ? rp[iw] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < HPT; ++i) {
+            const int e = tid + 256 * i;  // (window row, halo column)
+            const int row = e >> 1, ch = row / TR, r = row - ch * TR;
+            const int ic = c0 + ch, ih = oh0 - pad + r, iwh = ow0 - pad + 64 + (e & 1);
+            const bool in = e < NH && ic < C && (unsigned)ih < (unsigned)H && (unsigned)iwh < (unsigned)W;
+            v2[i] = in ? img[((int64_t)ic * H + ih) * W + iwh] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < WPT; ++i) {
+            const int e = tid + 256 * i;  // (ch, tap, o)
+            const int ch = e / (9 * OC), t = (e / OC) % 9, o = e % OC;
+            const int ic = c0 + ch;
+            fw[i] = (e < NW && ic < C && o < n_oc) ? __uint_as_float((uint32_t)filt[o * ldw + ic * 9 + t] << 16) : 0.f;
+        }
+    };
+    auto rounded = [](float x) { return __uint_as_float((uint32_t)bf16_rne(x) << 16); };
+    float acc[OC][4];
+#pragma unroll
+    for (int o = 0; o < OC; ++o)
+#pragma unroll
+        for (int x = 0; x < 4; ++x) acc[o][x] = 0.f;
+    load(0);
+    for (int c0 = 0; c0 < C; c0 += CT_CC) {
+        __syncthreads();  // every wave is done with the previous chunk
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const int row = wave + 4 * i;
+            const int ch = row / TR, r = row - ch * TR;
+            tile[ch][r][lane] = rounded(v[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < HPT; ++i) {
+            const int e = tid + 256 * i;
+            const int row = e >> 1, ch = row / TR, r = row - ch * TR;
+            if (e < NH) tile[ch][r][64 + (e & 1)] = rounded(v2[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < WPT; ++i)
+            if (tid + 256 * i < NW) (&wts[0][0][0])[tid + 256 * i] = fw[i];
+        __syncthreads();
+        if (c0 + CT_CC < C) load(c0 + CT_CC);  // in flight under this chunk's multiplies
+        const int nch = min(CT_CC, C - c0);
+        for (int ch = 0; ch < nch; ++ch) {
+#pragma unroll
+            for (int kh = 0; kh < 3; ++kh) {
+                const float *rp = &tile[ch][ty + kh][tx];
+                const float4 a = *(const float4 *)rp;
+                const float2 c = *(const float2 *)(rp + 4);
+                const float x[6] = {a.x, a.y, a.z, a.w, c.x, c.y};
+#pragma unroll
+                for (int kw = 0; kw < 3; ++kw) {
+                    float wv[OC];
+                    if constexpr (OC % 4 == 0) {
+#pragma unroll
+                        for (int o = 0; o < OC; o += 4) *(float4 *)&wv[o] = *(const float4 *)&wts[ch][kh * 3 + kw][o];
+                    } else {
+#pragma unroll
+                        for (int o = 0; o < OC; ++o) wv[o] = wts[ch][kh * 3 + kw][o];
+                    }
+#pragma unroll
+                    for (int o = 0; o < OC; ++o)
+#pragma unroll
+                        for (int px = 0; px < 4; ++px) acc[o][px] = fmaf(x[px + kw], wv[o], acc[o][px]);
+                }
+            }
+        }
+    }
+    const int oh = oh0 + ty, ow = ow0 + tx;
+    if (oh >= outH) return;
+#pragma unroll
+    for (int o = 0; o < OC; ++o) {
+        if (o >= n_oc) break;
+        const float bv = bias ? bias[o] : 0.f;
+        float *drow = dst + (((int64_t)b * n_oc + o) * outH + oh) * outW;
+        if (ow + 3 < outW && (((uintptr_t)(drow + ow)) & 15) == 0) {
+            *(float4 *)(drow + ow) = make_float4(acc[o][0] + bv, acc[o][1] + bv, acc[o][2] + bv, acc[o][3] + bv);
+        } else {
+#pragma unroll
+            for (int px = 0; px < 4; ++px)
+                if (ow + px < outW) drow[ow + px] = acc[o][px] + bv;
+        }
     }
 }
 

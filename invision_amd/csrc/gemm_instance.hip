@@ -11,10 +11,16 @@
 
 namespace {
 
-template <class C, int EPI, int OUT, int MODE>
+template <class C, int EPI, int OUT, int MODE, bool GATHER = false>
 void launch_one(const inv::GemmParams &p, dim3 grid, dim3 block, hipStream_t s) {
-    hipLaunchKernelGGL((inv::gemm_nt_bf16_kernel<C, EPI, OUT, MODE>), grid, block, 0, s, p);
+    hipLaunchKernelGGL((inv::gemm_nt_bf16_kernel<C, EPI, OUT, MODE, GATHER>), grid, block, 0, s, p);
 }
+
+// Tile configurations with the implicit-convolution (gather) instantiation:
+// 256x256 (one register stage: the gather offsets and tap masks take the
+// registers of the second) and 256x224 for many output channels, 256x128 for
+// 128 or fewer.
+constexpr bool kGatherCfg = INV_CFG_ID == 9 || INV_CFG_ID == 13 || INV_CFG_ID == 16;
 
 template <class C, int MODE>
 bool launch_epi(const inv::GemmParams &p, int epi, int out, dim3 grid, dim3 block, hipStream_t s) {
@@ -54,6 +60,14 @@ hipError_t launch_cfg(const inv::GemmParams &p, int epi, int out, int mode, hipS
     dim3 block(C::NTHREADS);
     const unsigned ntiles = (unsigned)(p.tiles_m * p.tiles_n);
     bool ok;
+    if (mode == inv::LAUNCH_GATHER) {
+        if constexpr (kGatherCfg && C::REG_STAGED && C::STAGED_EPI) {
+            if (epi != inv::EPI_ROWBIAS || out != inv::OUT_F32) return hipErrorInvalidConfiguration;
+            launch_one<C, inv::EPI_ROWBIAS, inv::OUT_F32, inv::GRID_TILES, true>(p, dim3(ntiles), block, s);
+            return hipGetLastError();
+        }
+        return hipErrorInvalidConfiguration;
+    }
     if (mode == inv::GRID_SPLITK)
         ok = launch_epi<C, inv::GRID_SPLITK>(p, epi, out, dim3(ntiles * p.ksplit), block, s);
     else if (mode == inv::GRID_STREAMK)

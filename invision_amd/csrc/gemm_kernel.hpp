@@ -76,6 +76,13 @@ struct GemmParams {
     float *partial;       // split/stream-K partial sums
     unsigned *counters;   // arrival counters, one per tile, zero between calls
     int ws_cached;        // 0: partial/counters are uncached memory; 1: ordinary (cached) device memory
+    // Implicit convolution (the gather instantiations): W is an NHWC bf16 image
+    // [cv_H x cv_W x cv_C] and row n of the A operand is output pixel n of the
+    // band starting at output row cv_oh0 ((cv_oh0 + n / cv_outW, n % cv_outW));
+    // k = ((kh * cv_kW + kw) * cv_C + ic), so a 64-wide k-tile is 64 channels of
+    // one filter tap (cv_C % 64 == 0; cv_taps = kH * kW <= 31).  Taps outside
+    // the image read zeros.  The image is below 2 GiB (32-bit offsets).
+    int cv_H, cv_W, cv_C, cv_outW, cv_kW, cv_taps, cv_stride, cv_pad, cv_oh0;
 };
 
 // A unit's arrival at its shared tile (thread 0, after a barrier that follows
@@ -431,6 +438,9 @@ constexpr int copy_step(int i) {
 #endif  // __HIP_DEVICE_COMPILE__
 
 enum GridMode { GRID_TILES = 0, GRID_SPLITK = 1, GRID_STREAMK = 2 };
+// Launch mode only: a tile grid whose A operand is gathered from an NHWC image
+// (implicit convolution; per-row bias epilogue, fp32 output).
+constexpr int LAUNCH_GATHER = 3;
 
 #if defined(__HIP_DEVICE_COMPILE__)
 
@@ -603,10 +613,10 @@ __device__ __forceinline__ void mainloop_ring(const GemmParams &p, lds_char_t *l
 // registers for chunk c of tile t+1+NREG.  One barrier per iteration, early in
 // the last substep: it publishes tile t+1's LDS buffer and retires every read
 // of tile t's, so the next iteration may overwrite it.
-template <class C>
+template <class C, bool GATHER = false>
 __device__ __forceinline__ void mainloop_rs(const GemmParams &p, lds_char_t *lds, __amdgpu_buffer_rsrc_t rsw,
                                             __amdgpu_buffer_rsrc_t rsx, int kt_begin, int kt_end,
-                                            typename C::acc_t (&acc)[C::FN][C::FM]) {
+                                            typename C::acc_t (&acc)[C::FN][C::FM], int n0 = 0) {
     typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
     constexpr int BK = C::BK, ROWB = C::ROWB, SLOTS = C::SLOTS;
     constexpr int AL = C::A_LOADS, L = C::LOADS;
@@ -652,17 +662,61 @@ __device__ __forceinline__ void mainloop_rs(const GemmParams &p, lds_char_t *lds
     const int wseg = p.w_seg_k / BK;
     int load_kt = kt_begin;
     int load_ktw = wseg ? kt_begin % wseg : kt_begin;
-    // Offsets of the next k-tile to load (out of range, i.e. zeros, past kt_end or K).
+    // Gather: for each A copy chunk, the byte offset of its pixel's window
+    // origin (ih0, iw0) plus the chunk's 16 bytes, and a mask of the taps that
+    // land inside the image (bit kh * cv_kW + kw; none for a pixel past N).
+    // The next k-tile is tap g_tap (byte offset g_tapoff from the origin),
+    // channel block g_cb; bit 31 is never set, so g_bit = 31 loads zeros.
+    int g_base[GATHER ? AL : 1];
+    unsigned g_mask[GATHER ? AL : 1];
+    int g_cb = 0, g_tap = 0, g_kw = 0, g_tapoff = 0, g_bit = 0;
+    if constexpr (GATHER) {
+#pragma unroll
+        for (int c = 0; c < AL; ++c) {
+            const int n = n0 + ld_row + c * RPL;
+            const int oh = p.cv_oh0 + n / p.cv_outW, ow = n % p.cv_outW;
+            const int ih0 = oh * p.cv_stride - p.cv_pad, iw0 = ow * p.cv_stride - p.cv_pad;
+            unsigned cols = 0, m = 0;
+            for (int kw = 0; kw < p.cv_kW; ++kw) cols |= ((unsigned)(iw0 + kw) < (unsigned)p.cv_W) << kw;
+            for (int kh = 0, t = 0; t < p.cv_taps; ++kh, t += p.cv_kW)
+                if ((unsigned)(ih0 + kh) < (unsigned)p.cv_H) m |= cols << t;
+            g_mask[c] = n < p.N ? m : 0u;
+            g_base[c] = n < p.N ? (ih0 * p.cv_W + iw0) * p.cv_C * 2 + ld_chunk * 16 : 0;
+        }
+    }
+    // Offsets of the next k-tile to load (out of range, i.e. zeros, past kt_end
+    // or K).  Gather (tile grids, kt_begin = 0): ka is the tap's byte offset
+    // from the window origin plus the channel block's, g_bit the tap's mask bit.
     auto next_kadd = [&](uint32_t &ka, uint32_t &kb) {
         const bool in = load_kt < kt_end;
-        ka = k_byte_offset<BK>(in && load_ktw * BK + ld_chunk * 8 < p.Kw, load_ktw);
+        if constexpr (GATHER) {
+            g_bit = in ? g_tap : 31;
+            ka = (uint32_t)(g_tapoff + g_cb * BK * 2);
+            if (++g_cb == p.cv_C / BK) {
+                g_cb = 0;
+                ++g_tap;
+                if (++g_kw == p.cv_kW) {
+                    g_kw = 0;
+                    g_tapoff += (p.cv_W - p.cv_kW + 1) * p.cv_C * 2;
+                } else {
+                    g_tapoff += p.cv_C * 2;
+                }
+            }
+        } else {
+            ka = k_byte_offset<BK>(in && load_ktw * BK + ld_chunk * 8 < p.Kw, load_ktw);
+        }
         kb = k_byte_offset<BK>(in && load_kt * BK + ld_chunk * 8 < p.K, load_kt);
         ++load_kt;
         load_ktw = (wseg && load_ktw + 1 == wseg) ? 0 : load_ktw + 1;
     };
     auto gload = [&](int cidx, uint32_t ka, uint32_t kb) -> u32x4_t {
-        if (cidx < AL)
+        if (cidx < AL) {
+            if constexpr (GATHER) {
+                const uint32_t off = ((g_mask[cidx] >> g_bit) & 1u) ? (uint32_t)g_base[cidx] + ka : 0x80000000u;
+                return __builtin_amdgcn_raw_buffer_load_b128(rsw, off, 0, 0);
+            }
             return __builtin_amdgcn_raw_buffer_load_b128(rsw, a_base + cidx * a_step + ka, 0, 0);
+        }
         return __builtin_amdgcn_raw_buffer_load_b128(rsx, b_base + (cidx - AL) * b_step + kb, 0, 0);
     };
     auto lds_chunk = [&](lds_char_t *buf, int cidx) -> u32x4_t * {
@@ -1132,7 +1186,7 @@ __device__ __forceinline__ void store_tile_swiglu(const GemmParams &p, lds_char_
 }
 
 // One work unit: output tile (tm, tn), k-tiles [kt_begin, kt_end).
-template <class C, int EPI, int OUT, int MODE>
+template <class C, int EPI, int OUT, int MODE, bool GATHER = false>
 __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int tm, int tn, int kt_begin, int kt_end,
                                           const UnitFix &fix) {
     const int tid = threadIdx.x;
@@ -1146,8 +1200,12 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
     // Buffer resources covering exactly the valid rows of this tile's panels.
     const int rows_w = min(C::TN, p.N - n0);
     const int rows_x = min(C::TM, p.M - m0);
-    const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.W + (int64_t)n0 * p.ldw), 0, (int)((int64_t)rows_w * p.ldw * 2), 0x00020000);
+    // gather: the whole NHWC image (an input pixel may belong to any output row of the tile)
+    const __amdgpu_buffer_rsrc_t rsw =
+        GATHER ? __builtin_amdgcn_make_buffer_rsrc((void *)p.W, 0, (int)((int64_t)p.cv_H * p.cv_W * p.cv_C * 2),
+                                                   0x00020000)
+               : __builtin_amdgcn_make_buffer_rsrc((void *)(p.W + (int64_t)n0 * p.ldw), 0,
+                                                   (int)((int64_t)rows_w * p.ldw * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(p.X + (int64_t)m0 * p.ldx), 0, (int)((int64_t)rows_x * p.ldx * 2), 0x00020000);
 
@@ -1163,7 +1221,7 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
             for (int r = 0; r < ACC_ELEMS; ++r) acc[i][j][r] = 0.0f;
 
     if constexpr (C::REG_STAGED)
-        mainloop_rs<C>(p, lds, rsw, rsx, kt_begin, kt_end, acc);
+        mainloop_rs<C, GATHER>(p, lds, rsw, rsx, kt_begin, kt_end, acc, n0);
     else
         mainloop_ring<C>(p, lds, rsw, rsx, kt_begin, kt_end, acc);
 
@@ -1277,8 +1335,9 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
 //                tiles (whole rounds) go one per workgroup; then workgroup g
 //                takes k-iterations [g*I/G, (g+1)*I/G) of the I = (remaining
 //                tiles) * KT, in tile order, so every workgroup ends together.
-template <class C, int EPI, int OUT, int MODE>
+template <class C, int EPI, int OUT, int MODE, bool GATHER = false>
 __global__ void __launch_bounds__(C::NTHREADS, 1) gemm_nt_bf16_kernel(const GemmParams p) {
+    static_assert(!GATHER || (C::REG_STAGED && MODE == GRID_TILES), "the gather loader is register-staged, tiles only");
 #if defined(__HIP_DEVICE_COMPILE__)
     __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
     const int ntiles = p.tiles_m * p.tiles_n;
@@ -1288,7 +1347,7 @@ __global__ void __launch_bounds__(C::NTHREADS, 1) gemm_nt_bf16_kernel(const Gemm
         grouped_tile(xcd_remap(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, p.group_m, tm, tn);
         UnitFix fix{};
         fix.nseg = 1;
-        gemm_unit<C, EPI, OUT, MODE>(p, smem, tm, tn, 0, KT, fix);
+        gemm_unit<C, EPI, OUT, MODE, GATHER>(p, smem, tm, tn, 0, KT, fix);
     } else if constexpr (MODE == GRID_SPLITK) {
         const int split = blockIdx.x % p.ksplit;
         const int tile = blockIdx.x / p.ksplit;

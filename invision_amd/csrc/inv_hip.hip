@@ -184,6 +184,7 @@ struct State {
     Buf amask;                          // attention key mask from host
     Buf hx, hvec;                       // head norm / rotary: X and the weight + tables from host
     Buf csrc, ccol, cdst;               // convolution: images from host, patch matrix, output for host
+    Buf cimg, cfilt;                    // implicit convolution: NHWC bf16 image, tap-major filter
     // Split/stream-K partial sums and arrival counters: uncached device memory
     // (coherent across XCDs without L2 maintenance).  Such memory is never
     // freed once a kernel has read it: outgrown buffers are retired, not freed.
@@ -1397,6 +1398,35 @@ int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_
 // (INV_HIP_CONV_COL_MB overrides it, in MiB).
 constexpr size_t kColCap = (size_t)1 << 30;
 
+// Tile configuration of the implicit convolution, or -1 for the patch-matrix
+// path: in_ch a multiple of 64 (a k-tile is 64 channels of one tap), at most
+// 31 taps (one mask bit each), an NHWC bf16 image below 2 GiB (32-bit buffer
+// offsets), at least 64 output channels, more than one tap and half a round
+// of tiles.  256x128
+// tiles (configuration 13) for up to 128 output channels, else 256x256 (9,
+// one register stage) or 256x224 (16), as the plain GEMM would choose between
+// its 256x256 and 256x224 tiles.  INV_HIP_CONV_GATHER=0 turns it off, =2
+// takes it whatever the tile count (where it applies at all).
+int conv_gather_cfg(int64_t in_ch, int64_t out_ch, int64_t H, int64_t W, int64_t taps, int64_t P) {
+    const int mode = env_int("INV_HIP_CONV_GATHER", 1);
+    // 1x1: the patch matrix is the image transposed, the same bytes as the
+    // NHWC copy, and the plain GEMM measured faster (0.54 against 0.58 ms at
+    // 1024x1024, 256 -> 128)
+    if (!mode || (taps == 1 && mode != 2)) return -1;
+    if (in_ch % 64 || taps > 31 || out_ch < 64 || H * W * in_ch * 2 >= ((int64_t)1 << 31)) return -1;
+    if (P > INT32_MAX / 2 || out_ch * in_ch * taps > ((int64_t)1 << 31)) return -1;
+    const int cus = g.cu_count > 0 ? g.cu_count : 256;
+    int cfg = 13;
+    if (out_ch > 128) {
+        const TileChoice tc = choose_tiles(out_ch, P, in_ch * taps);
+        cfg = tc.cfg == 16 ? 16 : 9;
+    }
+    const int ov = env_int("INV_HIP_CONV_GATHER_CFG", -1);
+    if (ov == 9 || ov == 13 || ov == 16) cfg = ov;
+    const int64_t tiles = ((out_ch + kCfg[cfg].tm - 1) / kCfg[cfg].tm) * ((P + kCfg[cfg].tn - 1) / kCfg[cfg].tn);
+    return (mode == 2 || tiles * 2 >= cus) ? cfg : -1;
+}
+
 int conv2d_impl(const float *src, inv_weight_t Wt, const float *bias, float *dst, int64_t in_ch, int64_t out_ch,
                 int64_t H, int64_t W, int64_t kH, int64_t kW, int64_t stride, int64_t padding, int64_t batch,
                 int flags) {
@@ -1447,6 +1477,98 @@ int conv2d_impl(const float *src, inv_weight_t Wt, const float *bias, float *dst
         yd = (float *)g.cdst.p;
     } else if (!aligned(src, 4) || !aligned(dst, 4)) {
         return fail(INV_ERR_ARG, "conv2d: src and dst must be 4-byte aligned");
+    }
+    // Few output channels, 3x3 at stride 1 (conv_out): the direct kernel, no patch matrix.
+    if (kH == 3 && kW == 3 && stride == 1 && out_ch <= 8 && batch <= 65535 && env_int("INV_HIP_CONV_DIRECT", 1)) {
+        const dim3 grid((unsigned)((outW + inv::CT_TW - 1) / inv::CT_TW), (unsigned)((outH + inv::CT_TH - 1) / inv::CT_TH),
+                        (unsigned)batch);
+        if (grid.y > 65535) return fail(INV_ERR_UNSUPPORTED, "conv2d: image too tall");
+        if (out_ch <= 3)  // RGB
+            hipLaunchKernelGGL(inv::conv3x3_thin<3>, grid, dim3(256), 0, g.stream, sd, Wt->w, Wt->ldw, bd, yd,
+                               (int)in_ch, (int)H, (int)W, (int)padding, (int)out_ch, (int)outH, (int)outW);
+        else if (out_ch <= 4)
+            hipLaunchKernelGGL(inv::conv3x3_thin<4>, grid, dim3(256), 0, g.stream, sd, Wt->w, Wt->ldw, bd, yd,
+                               (int)in_ch, (int)H, (int)W, (int)padding, (int)out_ch, (int)outH, (int)outW);
+        else
+            hipLaunchKernelGGL(inv::conv3x3_thin<8>, grid, dim3(256), 0, g.stream, sd, Wt->w, Wt->ldw, bd, yd,
+                               (int)in_ch, (int)H, (int)W, (int)padding, (int)out_ch, (int)outH, (int)outW);
+        HIPCHK(hipGetLastError());
+        g.calls++;
+        if (!dev) {
+            TRY(d2h_rows(dst, yd, 1, ybytes, ybytes));
+        } else if (!(flags & INV_FLAG_ASYNC)) {
+            HIPCHK(hipStreamSynchronize(g.stream));
+        }
+        return INV_OK;
+    }
+    // Many channels in and out: the implicit GEMM, whose loader gathers each
+    // k-tile (64 channels of one tap) straight from an NHWC bf16 copy of the
+    // image, so no patch matrix is written or read.
+    const int gcfg = conv_gather_cfg(in_ch, out_ch, H, W, kH * kW, P);
+    if (gcfg >= 0) {
+        const int64_t taps = kH * kW, HW = H * W;
+        TRY(ensure(g.cimg, (size_t)(HW * in_ch) * 2));
+        TRY(ensure(g.cfilt, (size_t)(out_ch * K) * 2));
+        uint16_t *nhwc = (uint16_t *)g.cimg.p, *filt = (uint16_t *)g.cfilt.p;
+        const int64_t total = out_ch * K;
+        hipLaunchKernelGGL(inv::conv_filter_tap_major, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, g.stream,
+                           Wt->w, Wt->ldw, filt, (int)in_ch, (int)taps, total);
+        HIPCHK(hipGetLastError());
+        if (!bd) {  // the per-row bias epilogue always adds one
+            TRY(ensure(g.bias, (size_t)out_ch * 4));
+            hipLaunchKernelGGL(fill_zero_u32, dim3((unsigned)((out_ch + 255) / 256)), dim3(256), 0, g.stream,
+                               (unsigned *)g.bias.p, out_ch);
+            HIPCHK(hipGetLastError());
+            bd = (const float *)g.bias.p;
+        }
+        const CfgMeta &cm = kCfg[gcfg];
+        inv::GemmParams p{};
+        p.X = filt;
+        p.ldx = K;
+        p.ldy = P;
+        p.M = (int)out_ch;
+        p.N = (int)P;
+        p.K = (int)K;
+        p.Kw = (int)K;
+        p.tiles_m = (int)((out_ch + cm.tm - 1) / cm.tm);
+        p.tiles_n = (int)((P + cm.tn - 1) / cm.tn);
+        p.group_m = std::max(1, std::min(p.tiles_m, env_int("INV_HIP_GROUP_M", 8)));
+        p.alpha = 1.0f;
+        p.row_bias = bd;
+        p.ksplit = 1;
+        p.kt_per_split = (int)(K / 64);
+        p.cv_H = (int)H;
+        p.cv_W = (int)W;
+        p.cv_C = (int)in_ch;
+        p.cv_outW = (int)outW;
+        p.cv_kW = (int)kW;
+        p.cv_taps = (int)taps;
+        p.cv_stride = (int)stride;
+        p.cv_pad = (int)padding;
+        for (int64_t b = 0; b < batch; ++b) {
+            // image b: [C x HW] fp32 -> [HW x C] bf16
+            TRY(launch_transpose<float>(sd + b * img, HW, nhwc, in_ch, in_ch, HW, in_ch));
+            p.W = nhwc;
+            p.Y = yd + b * out_ch * P;
+            p.vec_store = (P % 4 == 0) && aligned(p.Y, 16);
+            if (g.stats) HIPCHK(hipEventRecord(g.st0, g.stream));
+            HIPCHK(cm.launch(p, inv::EPI_ROWBIAS, inv::OUT_F32, inv::LAUNCH_GATHER, g.stream));
+            if (g.stats) {
+                HIPCHK(hipEventRecord(g.st1, g.stream));
+                HIPCHK(hipEventSynchronize(g.st1));
+                float ms = 0.f;
+                HIPCHK(hipEventElapsedTime(&ms, g.st0, g.st1));
+                g.gemm_ms += ms;
+                g.flops += 2.0 * (double)out_ch * (double)P * (double)K;
+            }
+        }
+        g.calls++;
+        if (!dev) {
+            TRY(d2h_rows(dst, yd, 1, ybytes, ybytes));
+        } else if (!(flags & INV_FLAG_ASYNC)) {
+            HIPCHK(hipStreamSynchronize(g.stream));
+        }
+        return INV_OK;
     }
     const int64_t row_bytes = outW * ldc * 2;
     const int64_t cap = std::max(1, env_int("INV_HIP_CONV_COL_MB", (int)(kColCap >> 20))) * ((int64_t)1 << 20);
@@ -1601,7 +1723,7 @@ int inv_hip_shutdown(void) {
     g.cache_clock = 0;
     g.cache_hits = g.cache_misses = g.cache_uploaded = 0;
     for (Buf *b : {&g.xin, &g.x16, &g.w16, &g.win, &g.yout, &g.cin, &g.bias, &g.gate, &g.aq, &g.ak, &g.avt, &g.aqin,
-                   &g.akin, &g.avin, &g.nvec, &g.amask, &g.hx, &g.hvec, &g.csrc, &g.ccol, &g.cdst})
+                   &g.akin, &g.avin, &g.nvec, &g.amask, &g.hx, &g.hvec, &g.csrc, &g.ccol, &g.cdst, &g.cimg, &g.cfilt})
         release(*b);
     // g.partial / g.counters (uncached) stay allocated until the process ends.
     release_stream_objects();

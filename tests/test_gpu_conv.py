@@ -160,3 +160,75 @@ def test_conv2d_errors(hiplib):
             hip.call("inv_hip_conv2d", x.ctypes.data, wt.handle, None, dst.ctypes.data, 4, 8, 6, 6, 3, 3, 0, 1, 1, 0)
         # batch 0 is a no-op
         hip.call("inv_hip_conv2d", None, wt.handle, None, None, 4, 8, 6, 6, 3, 3, 1, 1, 0, 0)
+
+
+# The direct kernel for 3x3 stride-1 convolutions with at most 8 output channels (conv_out):
+# ragged tiles (H, W not multiples of 16 x 64), input channels not a multiple of 8, batch 2,
+# padding 0, 1 and 2, 1 to 8 output channels (the 3-, 4- and 8-channel instantiations).
+DIRECT_SHAPES = [
+    (1, 13, 3, 37, 70, 1),
+    (2, 16, 8, 20, 129, 1),
+    (1, 24, 5, 33, 65, 0),
+    (1, 9, 1, 17, 17, 2),
+    (1, 16, 4, 23, 40, 1),
+    (1, 128, 3, 64, 128, 1),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,c,oc,H,W,p", DIRECT_SHAPES)
+def test_conv2d_direct_thin_output(hiplib, monkeypatch, b, c, oc, H, W, p):
+    x, w, bias = gen(14, b, c, oc, H, W, 3, 3)
+    with q.Weight(w) as wt:
+        y = q.conv2d(x, wt, bias, c, oc, H, W, 3, 3, 1, p, b)
+        monkeypatch.setenv("INV_HIP_CONV_DIRECT", "0")  # the im2col + GEMM path on the same inputs
+        y_gemm = q.conv2d(x, wt, bias, c, oc, H, W, 3, 3, 1, p, b)
+    check(y, x, w, bias, c, oc, H, W, 3, 3, 1, p, b)
+    # the same bf16 products summed in another order
+    assert oracle.normwise_err(y, y_gemm) <= 1e-5
+
+
+# The implicit GEMM (in_ch a multiple of 64, at least 64 output channels): each k-tile is 64
+# channels of one filter tap gathered from an NHWC bf16 copy of the image, the filter reordered
+# tap-major.  INV_HIP_CONV_GATHER=2 takes it at sizes where the patch-matrix path would otherwise
+# run (too few tiles), and =0 gives that path on the same inputs.  Shapes: 256x128 tiles (up to
+# 128 output channels), 256x256 and 256x224 tiles (more), ragged pixel counts, batch 2, stride 2
+# without padding (the VAE's downsample), 1x1 (skip connections), a 5x3 filter with padding 2.
+GATHER_SHAPES = [
+    (1, 64, 128, 24, 20, 3, 3, 1, 1, None),
+    (2, 128, 96, 19, 23, 3, 3, 1, 1, None),
+    (1, 64, 256, 17, 17, 3, 3, 2, 0, None),
+    (1, 128, 320, 16, 20, 1, 1, 1, 0, None),
+    (1, 64, 200, 9, 11, 5, 3, 1, 2, None),
+    (1, 192, 512, 12, 12, 3, 3, 1, 1, None),
+    (1, 128, 512, 13, 14, 3, 3, 1, 1, 16),
+    (1, 64, 448, 15, 9, 3, 3, 1, 1, 9),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("b,c,oc,H,W,kH,kW,s,p,cfg", GATHER_SHAPES)
+def test_conv2d_implicit_gemm(hiplib, monkeypatch, b, c, oc, H, W, kH, kW, s, p, cfg):
+    x, w, bias = gen(16, b, c, oc, H, W, kH, kW)
+    with q.Weight(w) as wt:
+        monkeypatch.setenv("INV_HIP_CONV_GATHER", "2")
+        if cfg is not None:
+            monkeypatch.setenv("INV_HIP_CONV_GATHER_CFG", str(cfg))
+        y = q.conv2d(x, wt, bias, c, oc, H, W, kH, kW, s, p, b)
+        y_nobias = q.conv2d(x, wt, None, c, oc, H, W, kH, kW, s, p, b)
+        monkeypatch.setenv("INV_HIP_CONV_GATHER", "0")
+        y_col = q.conv2d(x, wt, bias, c, oc, H, W, kH, kW, s, p, b)
+    check(y, x, w, bias, c, oc, H, W, kH, kW, s, p, b)
+    check(y_nobias, x, w, None, c, oc, H, W, kH, kW, s, p, b)
+    # the same bf16 products summed in another order (tap-major against channel-major)
+    assert oracle.normwise_err(y, y_col) <= 1e-5
+
+
+@pytest.mark.gpu
+def test_conv2d_implicit_gemm_at_size(hiplib):
+    # 128 -> 128 channels at 192x192: 144 tiles of 256x128, the default choice (no override)
+    b, c, oc, H, W, kH, kW, s, p = 1, 128, 128, 192, 192, 3, 3, 1, 1
+    x, w, bias = gen(17, b, c, oc, H, W, kH, kW)
+    with q.Weight(w) as wt:
+        y = q.conv2d(x, wt, bias, c, oc, H, W, kH, kW, s, p, b)
+    check(y, x, w, bias, c, oc, H, W, kH, kW, s, p, b)
