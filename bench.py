@@ -809,7 +809,13 @@ def summarize_profile(workload, trace_dir, fetch_dir, write_dir, busy_dir=None, 
               f"({(g_fetch + g_write) / alg:.2f}x); {(g_fetch + g_write) / avg_ns:.0f} GB/s over the timed "
               f"launches ({(g_fetch + g_write) / avg_ns / PEAK_HBM_GBS * 100:.1f}% of {PEAK_HBM_GBS:.0f} GB/s), "
               f"algorithmic {alg / avg_ns:.0f} GB/s.", ""]
-    extra = {}
+    t_mfma = flops / (PEAK_BF16_TFLOPS * 1e12) * 1e9
+    t_hbm = alg / (PEAK_HBM_GBS * 1e9) * 1e9
+    bound = "MFMA" if t_mfma >= t_hbm else "HBM"
+    lines += [f"Roofline: the MFMA bound is {t_mfma / 1e3:.2f} us (2*M*N*K at {PEAK_BF16_TFLOPS} TFLOP/s), the HBM "
+              f"bound {t_hbm / 1e3:.2f} us (the algorithmic bytes at {PEAK_HBM_GBS:.0f} GB/s); the launch at "
+              f"{avg_ns / 1e3:.2f} us is {max(t_mfma, t_hbm) / avg_ns * 100:.1f}% of the binding ({bound}) bound.", ""]
+    extra = {"roofline_bound": bound.lower(), "roofline_frac": max(t_mfma, t_hbm) / avg_ns}
     if busy_dir:
         bc = named_counters(busy_dir, kernel)
         med = lambda c: statistics.median(v for v, _ in bc[c])
