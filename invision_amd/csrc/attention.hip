@@ -9,6 +9,13 @@
 // staged in LDS (double-buffered, filled one tile ahead by direct
 // buffer_load ... lds copies) and shared by the 4 waves; two workgroups per CU,
 // so one's softmax VALU work overlaps the other's MFMAs.
+// Short sequences (KS = 2): a grid of 128-query blocks leaves CUs idle, and a
+// block walks its keys one tile after another, so the block with the most keys
+// sets the time.  There the workgroup takes 64 queries, and its 4 waves form
+// two key groups of 2 waves: group g takes key tiles g, g + 2, ..., each group
+// with its own double buffer, and group 1 hands its running max, sum and O to
+// group 0 through LDS at the end, which merges them as the online softmax
+// merges tiles.  Twice the workgroups, half the tiles in sequence.
 //
 // Per wave and key tile, with v_mfma_f32_32x32x16_bf16 (D[n][m] = sum_k A[n][k] B[m][k],
 // lane l holding A[l%32][8*(l/32) .. +7] and B[l%32][8*(l/32) .. +7], and output
@@ -77,27 +84,33 @@ __device__ __forceinline__ int xcd_order(int bid, int count) {
 
 // The body exists only in the device pass; the host pass needs the launch stub
 // (buffer-resource types do not exist for the host target).
-template <int D, bool CAUSAL, int OUT>
+template <int D, bool CAUSAL, int OUT, int KS>
 __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    constexpr int BQ = kAttnBlockQ, BK = kAttnBlockK;
-    static_assert(BQ == 128 && BK == 64, "4 waves of 32 queries, 64-key tiles");
+    constexpr int WQ = 4 / KS;             // query waves per key group
+    constexpr int BQ = 32 * WQ, BK = kAttnBlockK;
+    constexpr int NT = 64 * WQ;            // threads of one key group
+    static_assert((KS == 1 || KS == 2) && BK == 64, "one or two key groups, 64-key tiles");
     static_assert(D == 64 || D == 128, "head_dim 64 or 128");
     constexpr int KROW = D * 2;            // bytes per K-tile row
     constexpr int K_BYTES = BK * KROW;     // K tile
     constexpr int V_BYTES = D * BK * 2;    // V^T tile: D rows of 128 bytes
     constexpr int STAGE = K_BYTES + V_BYTES;
     constexpr int KCH = D / 8;             // 16-byte chunks per K row
-    constexpr int KIT = BK * KCH / 256;    // K copies per thread per tile
-    constexpr int VIT = D * 8 / 256;       // V^T copies per thread per tile
+    constexpr int KIT = BK * KCH / NT;     // K copies per thread per tile
+    constexpr int VIT = D * 8 / NT;        // V^T copies per thread per tile
     constexpr int NC = D / 16;             // 16-wide head_dim steps of S
     constexpr int ND = D / 32;             // 32-row head_dim blocks of O
-    __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
-    lds_t *lds = (lds_t *)smem;
+    constexpr int NX = ND * 16 + 2;        // KS = 2: floats per lane handed from group 1 to group 0
+    static_assert(KS == 1 || WQ * NX * 64 * 4 <= KS * 2 * STAGE, "the hand-off fits in the stage buffers");
+    __shared__ __attribute__((aligned(1024))) char smem[KS * 2 * STAGE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS copy bases stay scalar
+    const int kg = wave / WQ, wq = wave % WQ;                   // key group, query wave within it
+    const int gtid = tid % NT;                                  // thread within the key group
+    lds_t *lds = (lds_t *)smem + kg * 2 * STAGE;                // the group's double buffer
     const int lq = lane & 31, lh = lane >> 5;
     // 1-D grid of heads x query blocks; causal blocks run longest first.
     const int nqb = (p.seq_q + BQ - 1) / BQ;
@@ -106,7 +119,7 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
     const int qb = CAUSAL ? nqb - 1 - L % nqb : L % nqb;
     const int kvh = head / (p.heads / p.kv_heads);
     const int q0 = qb * BQ;
-    const int my_q = q0 + wave * 32 + lq;
+    const int my_q = q0 + wq * 32 + lq;
 
     // This wave's Q rows as the B operand of S^T = K Q^T (zero past seq_q).
     bf16x8_t qf[NC];
@@ -127,8 +140,8 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
     const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(p.Vt + (int64_t)kvh * D * p.ldv), 0, (int)((int64_t)D * p.ldv * 2), 0x00020000);
 
-    // Global -> LDS copies (buffer_load ... lds): copy i of thread tid fills the
-    // 16-byte LDS slot i*256 + tid of its tile, so each thread fetches the chunk
+    // Global -> LDS copies (buffer_load ... lds): copy i of group thread gtid fills
+    // the 16-byte LDS slot i*NT + gtid of its tile, so each thread fetches the chunk
     // that belongs there -- the swizzle and the K row order live in these
     // global offsets.  K slot s: row n = s / KCH holds key quadswap(n), physical
     // chunk s % KCH holds logical chunk (s % KCH) ^ swizzle(n).  V^T slot s: row
@@ -136,23 +149,23 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
     uint32_t k_goff[KIT], v_goff[VIT];
 #pragma unroll
     for (int i = 0; i < KIT; ++i) {
-        const int sl = i * 256 + tid, n = sl / KCH;
+        const int sl = i * NT + gtid, n = sl / KCH;
         k_goff[i] = (uint32_t)(quadswap(n) * p.ldk * 2 + k_slot<D>(n, sl % KCH) * 16);
     }
 #pragma unroll
     for (int i = 0; i < VIT; ++i) {
-        const int sl = i * 256 + tid, d = sl / 8;
+        const int sl = i * NT + gtid, d = sl / 8;
         v_goff[i] = (uint32_t)(d * p.ldv * 2 + ((sl % 8) ^ key8(d)) * 16);
     }
     const uint32_t k_tile_step = (uint32_t)(BK * p.ldk * 2), v_tile_step = BK * 2;
     auto load_tile = [&](int kt, lds_t *st) {
-        lds_t *wk = st + wave * 64 * 16;
+        lds_t *wk = st + wq * 64 * 16;
 #pragma unroll
         for (int i = 0; i < KIT; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsk, wk + i * 256 * 16, 16, k_goff[i] + kt * k_tile_step, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsk, wk + i * NT * 16, 16, k_goff[i] + kt * k_tile_step, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < VIT; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsv, wk + K_BYTES + i * 256 * 16, 16, v_goff[i] + kt * v_tile_step,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsv, wk + K_BYTES + i * NT * 16, 16, v_goff[i] + kt * v_tile_step,
                                                      0, 0, 0);
     };
 
@@ -194,21 +207,22 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
             v_frag[i][kc4] = K_BYTES + d * 128 + (((2 * kc4 + lh) ^ key8(d)) * 16);
         }
 
-    if (nkt > 0) load_tile(0, lds);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): tile 0 is in LDS
+    if (kg < nkt) load_tile(kg, lds);  // the group's first tile
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): it is in LDS
     __syncthreads();
 
     // One key tile; EDGE tiles (a partial last tile, or keys after some
     // query's diagonal) mask scores, the others carry no masking code at all.
     // PAR is the buffer holding tile kt when it is known at compile time (the
     // unmasked loop runs two tiles per trip), so LDS addresses are a register
-    // plus an immediate offset; -1: it follows kt at run time (edge tiles).
+    // plus an immediate offset; -1: it follows kt at run time (edge tiles; the
+    // group's j-th tile, kt = KS*j + kg, sits in buffer j & 1).
     auto step = [&](int kt, auto edge_c, auto par_c) {
         constexpr bool EDGE = decltype(edge_c)::value;
         constexpr int PAR = decltype(par_c)::value;
-        const int par = PAR < 0 ? (kt & 1) : PAR;
+        const int par = PAR < 0 ? ((kt / KS) & 1) : PAR;
         const lds_t *cur = lds + par * STAGE;
-        if (kt + 1 < nkt) load_tile(kt + 1, lds + (1 - par) * STAGE);
+        if (kt + KS < nkt) load_tile(kt + KS, lds + (1 - par) * STAGE);
 
         // S^T for 64 keys: two 32-key blocks whose MFMAs alternate (no back-to-back
         // accumulator chain); K fragments are read two head_dim steps ahead.
@@ -325,13 +339,55 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
     n_full = p.key_mask ? 0 : min(n_full, nkt);
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
-    int kt = 0;
-    for (; kt + 1 < n_full; kt += 2) {
-        step(kt, std::false_type{}, P0{});
-        step(kt + 1, std::false_type{}, P1{});
+    using PR = std::integral_constant<int, -1>;
+    if constexpr (KS == 1) {
+        int kt = 0;
+        for (; kt + 1 < n_full; kt += 2) {
+            step(kt, std::false_type{}, P0{});
+            step(kt + 1, std::false_type{}, P1{});
+        }
+        if (kt < n_full) step(kt++, std::false_type{}, P0{});
+        for (; kt < nkt; ++kt) step(kt, std::true_type{}, PR{});
+    } else {
+        // Both groups take the same number of turns, so every wave meets the
+        // same barriers; a group whose tiles ran out waits out the last turn.
+        const int turns = (nkt + KS - 1) / KS;
+        for (int j = 0; j < turns; ++j) {
+            const int kt = KS * j + kg;
+            if (kt < n_full) {
+                step(kt, std::false_type{}, PR{});
+            } else if (kt < nkt) {
+                step(kt, std::true_type{}, PR{});
+            } else {
+                __builtin_amdgcn_s_waitcnt(0x0F70);
+                __syncthreads();
+            }
+        }
+        // Group 1 hands its state to group 0 (same query wave, same lane); the
+        // stage buffers are free: every load has landed and every wave has
+        // passed the last turn's barrier.
+        float *xch = (float *)smem + wq * NX * 64 + lane;
+        if (kg == 1) {
+#pragma unroll
+            for (int i = 0; i < ND; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) xch[(16 * i + r) * 64] = o[i][r];
+            xch[(NX - 2) * 64] = m_run;
+            xch[(NX - 1) * 64] = l_run;
+        }
+        __syncthreads();
+        if (kg == 1) return;
+        // exp2(m_g - m) weighs each group's sums (zero for a group that saw no key)
+        const float m1 = xch[(NX - 2) * 64], l1 = xch[(NX - 1) * 64];
+        const float mn = fmaxf(m_run, m1);
+        const float a0 = (m_run == -__builtin_inff()) ? 0.f : exp2_hw(m_run - mn);
+        const float a1 = (m1 == -__builtin_inff()) ? 0.f : exp2_hw(m1 - mn);
+        l_run = l_run * a0 + l1 * a1;
+#pragma unroll
+        for (int i = 0; i < ND; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[i][r] = o[i][r] * a0 + xch[(16 * i + r) * 64] * a1;
     }
-    if (kt < n_full) step(kt++, std::false_type{}, P0{});
-    for (; kt < nkt; ++kt) step(kt, std::true_type{}, std::integral_constant<int, -1>{});
 
     // Normalise and store this lane's query row: 4 consecutive head_dim values per register group.
     const float lt = l_run + __shfl_xor(l_run, 32);
@@ -357,24 +413,31 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
-template <int D, bool CAUSAL, int OUT>
-hipError_t launch3(const AttnParams &p, hipStream_t s) {
-    const dim3 grid((unsigned)(((p.seq_q + kAttnBlockQ - 1) / kAttnBlockQ) * p.heads));
-    hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL, OUT>), grid, dim3(256), 0, s, p);
+template <int D, bool CAUSAL, int OUT, int KS>
+hipError_t launch4(const AttnParams &p, hipStream_t s) {
+    constexpr int BQ = 128 / KS;
+    const dim3 grid((unsigned)(((p.seq_q + BQ - 1) / BQ) * p.heads));
+    hipLaunchKernelGGL((attn_fwd_kernel<D, CAUSAL, OUT, KS>), grid, dim3(256), 0, s, p);
     return hipGetLastError();
 }
 
+template <int D, bool CAUSAL, int OUT>
+hipError_t launch3(const AttnParams &p, int key_groups, hipStream_t s) {
+    return key_groups == 2 ? launch4<D, CAUSAL, OUT, 2>(p, s) : launch4<D, CAUSAL, OUT, 1>(p, s);
+}
+
 template <int D>
-hipError_t launch2(const AttnParams &p, bool causal, int out, hipStream_t s) {
-    if (causal) return out ? launch3<D, true, 1>(p, s) : launch3<D, true, 0>(p, s);
-    return out ? launch3<D, false, 1>(p, s) : launch3<D, false, 0>(p, s);
+hipError_t launch2(const AttnParams &p, bool causal, int out, int key_groups, hipStream_t s) {
+    if (causal) return out ? launch3<D, true, 1>(p, key_groups, s) : launch3<D, true, 0>(p, key_groups, s);
+    return out ? launch3<D, false, 1>(p, key_groups, s) : launch3<D, false, 0>(p, key_groups, s);
 }
 
 }  // namespace
 
-hipError_t attention_launch(const AttnParams &p, int D, bool causal, int out, hipStream_t stream) {
-    if (D == 128) return launch2<128>(p, causal, out, stream);
-    if (D == 64) return launch2<64>(p, causal, out, stream);
+hipError_t attention_launch(const AttnParams &p, int D, bool causal, int out, int key_groups, hipStream_t stream) {
+    if (key_groups != 1 && key_groups != 2) return hipErrorInvalidValue;
+    if (D == 128) return launch2<128>(p, causal, out, key_groups, stream);
+    if (D == 64) return launch2<64>(p, causal, out, key_groups, stream);
     return hipErrorInvalidValue;
 }
 

@@ -24,10 +24,13 @@ struct AttnParams {
     const int32_t *key_mask;  // null, or [seq_k]: key j hidden from every query where key_mask[j] == 0
 };
 
-// D: 64 or 128; causal: mask keys after the query's diagonal; out: 0 fp32, 1 bf16.
-hipError_t attention_launch(const AttnParams &p, int D, bool causal, int out, hipStream_t stream);
+// D: 64 or 128; causal: mask keys after the query's diagonal; out: 0 fp32, 1 bf16;
+// key_groups: 1 (128 queries per workgroup, 4 waves over every key tile) or 2
+// (64 queries per workgroup, two pairs of waves over alternate key tiles: for
+// grids of 128-query blocks that do not fill the chip).
+hipError_t attention_launch(const AttnParams &p, int D, bool causal, int out, int key_groups, hipStream_t stream);
 
-constexpr int kAttnBlockQ = 128;  // queries per workgroup (4 waves x 32)
+constexpr int kAttnBlockQ = 128;  // queries per workgroup with one key group (4 waves x 32)
 constexpr int kAttnBlockK = 64;   // keys per tile; Vt rows are padded to a multiple of this
 
 }  // namespace inv

@@ -1312,7 +1312,7 @@ int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_
     if (seq_k == 0) return fail(INV_ERR_ARG, "attention: seq_k is 0 (a softmax over no keys)");
     if (!Q || !K || !V || !O) return fail(INV_ERR_ARG, "attention: Q, K, V or O is null");
     if (seq_q > INT32_MAX / 2 || seq_k > INT32_MAX / 2 ||
-        ((seq_q + inv::kAttnBlockQ - 1) / inv::kAttnBlockQ) * heads > INT32_MAX)
+        ((seq_q + 63) / 64) * heads > INT32_MAX)
         return fail(INV_ERR_UNSUPPORTED, "attention: too many heads or tokens");
     const int64_t hq = heads * head_dim, hk = kv_heads * head_dim;
     const int64_t ldv = round_up(seq_k, inv::kAttnBlockK);
@@ -1370,8 +1370,15 @@ int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_
         p.key_mask = (const int32_t *)g.amask.p;
     }
     const bool causal = (flags & INV_ATTN_CAUSAL) != 0;
+    // Two key groups (64-query workgroups) where the 128-query grid leaves CUs
+    // idle: Qwen3's 512-token prefill is 128 blocks on 256 CUs.
+    // INV_HIP_ATTN_KEY_GROUPS=1 or 2 forces the choice.
+    const int64_t blocks128 = ((seq_q + inv::kAttnBlockQ - 1) / inv::kAttnBlockQ) * heads;
+    int key_groups = blocks128 < (g.cu_count > 0 ? g.cu_count : 256) ? 2 : 1;
+    const int kg_ov = env_int("INV_HIP_ATTN_KEY_GROUPS", 0);
+    if (kg_ov == 1 || kg_ov == 2) key_groups = kg_ov;
     if (g.stats) HIPCHK(hipEventRecord(g.st0, g.stream));
-    HIPCHK(inv::attention_launch(p, (int)head_dim, causal, out_dtype == INV_DT_BF16 ? 1 : 0, g.stream));
+    HIPCHK(inv::attention_launch(p, (int)head_dim, causal, out_dtype == INV_DT_BF16 ? 1 : 0, key_groups, g.stream));
     if (g.stats) {
         HIPCHK(hipEventRecord(g.st1, g.stream));
         HIPCHK(hipEventSynchronize(g.st1));

@@ -23,6 +23,10 @@ from invision_amd import quicknn_hip as q
 from invision_amd.bf16 import as_bf16_bits, bf16_bits_to_f32, round_bf16
 
 TOL_BF16_IN = 4e-3
+# Workgroup shapes: 1 = 128 queries, 4 waves over every key tile; 2 = 64 queries, two pairs of
+# waves over alternate key tiles whose softmax states merge at the end (the default where the
+# 128-query grid has fewer blocks than the chip has CUs, i.e. for most shapes here).
+KEY_GROUPS = [1, 2]
 TOL_REF = 1.5e-2
 TOL_BF16_OUT = 2.0 ** -8
 
@@ -68,7 +72,9 @@ def check(O, Q, K, V, heads, kv_heads, d, scale, causal, out="f32", rows=None, r
     (2, 2, 5, 70, 64, True),        # causal with more keys than queries (offset 65)
 ])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_attention_matches_oracle(hiplib, heads, kv_heads, sq, sk, d, causal, dtype):
+@pytest.mark.parametrize("key_groups", KEY_GROUPS)
+def test_attention_matches_oracle(hiplib, monkeypatch, heads, kv_heads, sq, sk, d, causal, dtype, key_groups):
+    monkeypatch.setenv("INV_HIP_ATTN_KEY_GROUPS", str(key_groups))
     Q, K, V = gen(61, sq, sk, heads, kv_heads, d)
     scale = 1.0 / math.sqrt(d)
     ins = (Q, K, V) if dtype == "f32" else tuple(as_bf16_bits(a) for a in (Q, K, V))
@@ -189,10 +195,12 @@ def test_stats_count_the_evaluated_pairs(hiplib):
 @pytest.mark.gpu
 @pytest.mark.parametrize("heads,kv_heads,sq,sk,d,causal", [(2, 2, 200, 333, 128, False), (4, 2, 130, 130, 64, True),
                                                           (8, 2, 257, 257, 128, True), (2, 1, 77, 300, 64, False)])
-def test_key_mask_matches_oracle(hiplib, heads, kv_heads, sq, sk, d, causal):
+@pytest.mark.parametrize("key_groups", KEY_GROUPS)
+def test_key_mask_matches_oracle(hiplib, monkeypatch, heads, kv_heads, sq, sk, d, causal, key_groups):
     """Keys with mask 0 hidden from every query (QNNMatTriangularFill's mask,
     src/quicknncpu.pas:3017-3028): a random mask, key 0 kept so that no causal
     row is empty."""
+    monkeypatch.setenv("INV_HIP_ATTN_KEY_GROUPS", str(key_groups))
     Q, K, V = gen(70, sq, sk, heads, kv_heads, d)
     mask = (np.random.default_rng(7).random(sk) < 0.7).astype(np.int32)
     mask[0] = 1
@@ -213,9 +221,11 @@ def test_padding_mask_equals_the_unpadded_keys(hiplib):
 
 
 @pytest.mark.gpu
-def test_qwen3_encoder_shape_padded_prompt(hiplib):
+@pytest.mark.parametrize("key_groups", KEY_GROUPS)
+def test_qwen3_encoder_shape_padded_prompt(hiplib, monkeypatch, key_groups):
     """Qwen3-4B text encoder: 32 query heads over 8 kv heads of 128, 512 tokens,
     causal, a 137-token prompt padded to 512 (padding queries see the prompt)."""
+    monkeypatch.setenv("INV_HIP_ATTN_KEY_GROUPS", str(key_groups))
     heads, kvh, d, s, n = 32, 8, 128, 512, 137
     Q, K, V = gen(72, s, s, heads, kvh, d)
     mask = (np.arange(s) < n).astype(np.int32)
@@ -248,10 +258,13 @@ def test_key_mask_device_pointers_and_empty_rows(hiplib):
 
 
 @pytest.mark.gpu
-def test_rows_without_keys_are_zero(hiplib):
+@pytest.mark.parametrize("key_groups", KEY_GROUPS)
+def test_rows_without_keys_are_zero(hiplib, monkeypatch, key_groups):
     """Queries before the diagonal's start (seq_q > seq_k, causal) see no key and
     get zeros, also in waves whose other rows do see keys (their running max
-    moves while these rows' stays at -inf)."""
+    moves while these rows' stays at -inf), and with two key groups, where one
+    group may see keys for a row and the other none."""
+    monkeypatch.setenv("INV_HIP_ATTN_KEY_GROUPS", str(key_groups))
     heads, d, sq, sk = 2, 64, 300, 100
     Q, K, V = gen(75, sq, sk, heads, heads, d)
     O = q.attention(Q, K, V, heads=heads, head_dim=d, causal=True)
@@ -259,3 +272,23 @@ def test_rows_without_keys_are_zero(hiplib):
     assert np.all(np.isfinite(O))
     assert not np.any(O[:empty])
     check(O[empty:], Q[empty:], K, V, heads, heads, d, 1.0 / math.sqrt(d), True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads,kv_heads,sq,sk,d,causal", [(32, 8, 512, 512, 128, True), (3, 3, 200, 333, 64, False),
+                                                          (2, 2, 64, 1, 128, False), (2, 2, 65, 70, 128, True)])
+def test_key_groups_agree(hiplib, monkeypatch, heads, kv_heads, sq, sk, d, causal):
+    """The two workgroup shapes against each other and the oracle: one key tile
+    (sk = 1: group 1 idle), an odd number of tiles, causal blocks whose groups see
+    different numbers of tiles.  They differ by more than summation order: each
+    key group rounds its softmax weights to bf16 relative to its own running max,
+    so the bound is the bf16-input tolerance."""
+    Q, K, V = gen(76, sq, sk, heads, kv_heads, d)
+    outs = []
+    for kgrp in KEY_GROUPS:
+        monkeypatch.setenv("INV_HIP_ATTN_KEY_GROUPS", str(kgrp))
+        outs.append(q.attention(Q, K, V, heads=heads, head_dim=d, kv_heads=kv_heads, causal=causal))
+    d12 = oracle.normwise_err(outs[1], outs[0])
+    print(f"  one against two key groups: {d12:.3e}", flush=True)
+    assert d12 <= TOL_BF16_IN
+    check(outs[1], Q, K, V, heads, kv_heads, d, 1.0 / math.sqrt(d), causal)
