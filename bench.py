@@ -343,6 +343,68 @@ def mfma_ceiling(gemm_tflops):
     return out
 
 
+def vendor_gemm(workload):
+    """The same GEMM through torch on this GPU (its bf16 matmul runs hipBLASLt on ROCm), on the
+    same X, W and bias values (make_inputs), as a same-run comparator for the headline kernel.
+    torch carries its own HIP runtime, so it runs in a child process that never loads this
+    library; the inputs go to it through .npy files."""
+    import subprocess
+    import tempfile
+    desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[workload]
+    X, W, b = make_inputs(M, K, N)
+    with tempfile.TemporaryDirectory(dir="/tmp") as d:
+        np.save(os.path.join(d, "x.npy"), X)
+        np.save(os.path.join(d, "w.npy"), W)
+        np.save(os.path.join(d, "b.npy"), b)
+        r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--vendor-gemm-child", d,
+                            "--workload", workload], capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        raise RuntimeError(f"comparator exited {r.returncode}: {r.stderr[-500:]}")
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def vendor_gemm_child(d, workload, steps=50, warmup_seconds=1.0):
+    """Child side of vendor_gemm: Y = X . W^T + bias by torch.addmm on bf16 X and W, fp32 output
+    where torch offers out_dtype=float32 for bf16 operands, else bf16 output (half the bytes
+    written); prints one JSON line."""
+    import torch
+    from invision_amd.bf16 import round_bf16
+    desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[workload]
+    X, W, b = (np.load(os.path.join(d, f + ".npy")) for f in ("x", "w", "b"))
+    dev = torch.device("cuda:0")
+    xt = torch.from_numpy(round_bf16(X)).to(dev).to(torch.bfloat16)
+    wt = torch.from_numpy(W.view(np.int16)).to(dev).view(torch.bfloat16)
+    bt = torch.from_numpy(b).to(dev)
+    wtt = wt.t()
+    fn, out = (lambda: torch.addmm(bt, xt, wtt, out_dtype=torch.float32)), "f32"
+    try:
+        y = fn()
+    except Exception:
+        bb = bt.to(torch.bfloat16)
+        fn, out = (lambda: torch.addmm(bb, xt, wtt)), "bf16"
+        y = fn()
+    torch.cuda.synchronize()
+    ref = round_bf16(X[:8]).astype(np.float64) @ ((W.astype(np.uint32) << 16).view(np.float32)
+                                                   .astype(np.float64)).T + b
+    err = float(np.abs(y[:8].float().cpu().numpy() - ref).max() / np.abs(ref).max())
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < warmup_seconds:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    print(json.dumps({"what": f"torch.addmm on the same bf16 X, W and fp32 bias, {out} Y, torch {torch.__version__}"
+                              f" (hipBLASLt)", "tflops": round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1),
+                      "ms": round(ms, 5), "normwise_err_first_rows": err}), flush=True)
+    return 0
+
+
 def run_attention(name, steps, warmup_seconds=0.5, check=True):
     """inv_hip_attention on resident bf16 Q, K, V; FLOP = 4 * seq_q * seq_k * head_dim * heads
     (halved for causal: the keys after the diagonal are skipped)."""
@@ -879,6 +941,8 @@ def main():
                     help="GEMM shape for the bench line; attention shapes only with --profile-run")
     ap.add_argument("--all", action="store_true", help="also time every workload shape (stderr)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-vendor-gemm", action="store_true", help="skip the torch/hipBLASLt comparator")
+    ap.add_argument("--vendor-gemm-child", metavar="DIR", help=argparse.SUPPRESS)
     ap.add_argument("--no-mfma-ceiling", action="store_true",
                     help="skip the register-only MFMA ceiling measured on the same GPU (~5 s)")
     ap.add_argument("--profile-run", action="store_true",
@@ -893,6 +957,8 @@ def main():
                     help="run every rocprofv3 pass for --workload (child processes; raw output under OUT_DIR) and "
                          "write its profiles/ summary")
     args = ap.parse_args()
+    if args.vendor_gemm_child:
+        return vendor_gemm_child(args.vendor_gemm_child, args.workload)
     if args.profile_all:
         return profile_all(args.workload, os.path.abspath(args.profile_all), cold=args.cold)
     if args.summarize_profile:
@@ -940,6 +1006,13 @@ def main():
         ceiling["gemm_constant_operands_tflops"] = const["tflops"]
         ceiling["gemm_constant_operands_exact"] = const["exact"]
         log(f"[bench] GEMM with constant operands: {const}")
+    vendor = None
+    if not args.no_vendor_gemm and WORKLOADS[args.workload][5] == "none" and WORKLOADS[args.workload][6] == "bf16":
+        try:
+            vendor = vendor_gemm(args.workload)
+            log(f"[bench] vendor GEMM: {vendor}")
+        except Exception as e:  # a comparator only: its failure does not void the line
+            log(f"[bench] vendor GEMM comparator failed: {e!r}")
     desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[args.workload]
     achieved = res["tflops_kernel"]
     traffic = None
@@ -978,6 +1051,7 @@ def main():
         "host_fp32_io_tflops": round(res["host_fp32_io_tflops"], 2) if "host_fp32_io_tflops" in res else None,
         "device": info["name"],
         "mfma_ceiling": ceiling,
+        "vendor_gemm": vendor,
     }
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")
