@@ -987,9 +987,10 @@ def main():
             if name != args.workload:
                 extra.append(run_workload(name, max(5, args.steps // 2), 3,
                                           warmup_seconds=min(args.warmup_seconds, 0.5)))
+                log(f"[bench] {json.dumps(extra[-1])}")
                 if name == "c5_adaln":
                     extra.append(run_workload(name, max(5, args.steps // 2), 3, warmup_seconds=0.5, cold=True))
-                log(f"[bench] {json.dumps(extra[-1])}")
+                    log(f"[bench] {json.dumps(extra[-1])}")
         for name in ATTN_WORKLOADS:
             extra.append(run_attention(name, max(5, args.steps // 4), warmup_seconds=min(args.warmup_seconds, 0.5)))
             log(f"[bench] {json.dumps(extra[-1])}")
