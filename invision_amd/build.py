@@ -18,6 +18,9 @@ ROOT = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libinvision_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+# The versioned name a library probe list may also try (the reference probes "libopenblas.so"
+# then "libopenblas.so.0", src/quicknncpu.pas:3967-3978): a symlink beside the library.
+SONAME = LIB_NAME + ".0"
 PROBE_NAME = "libinv_probe.so"  # the MFMA-ceiling measurement aid (not the linear-layer ABI)
 PROBE_PATH = os.path.join(PKG_DIR, PROBE_NAME)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -89,17 +92,26 @@ def build_lib(verbose: bool = True, jobs: int = 0) -> str:
         if rc != 0:
             raise RuntimeError(f"hipcc failed ({rc}):\n{' '.join(cmd)}\n{err}")
     tmp = LIB_PATH + ".tmp"
-    link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + [o for _, o in todo]
+    link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,-soname,{SONAME}", "-o", tmp] + [o for _, o in todo]
     rc, err, cmd = _run(link)
     if rc != 0:
         raise RuntimeError(f"link failed ({rc}):\n{' '.join(cmd)}\n{err}")
     os.replace(tmp, LIB_PATH)
+    link_soname()
     if verbose:
         print(f"[build] {LIB_NAME} ({len(todo)} translation units) in {time.time() - t0:.1f}s", flush=True)
         warn = "\n".join(e for rc, e, _ in results if e.strip())
         if warn.strip():
             print(warn, flush=True)
     return LIB_PATH
+
+
+def link_soname() -> None:
+    """libinvision_hip.so.0 -> libinvision_hip.so, in the package directory."""
+    path = os.path.join(PKG_DIR, SONAME)
+    if os.path.islink(path) or os.path.exists(path):
+        os.remove(path)
+    os.symlink(LIB_NAME, path)
 
 
 def build_oracle(verbose: bool = True) -> None:

@@ -31,6 +31,16 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def test_versioned_name_loads_the_same_library():
+    # A probe list may try libinvision_hip.so.0 (as the reference probes libopenblas.so.0):
+    # the build links that name to the library, whose soname it is.
+    so0 = hip.lib_path() + ".0"
+    assert os.path.realpath(so0) == os.path.realpath(hip.lib_path())
+    assert "libinvision_hip.so.0" in os.popen(f"readelf -d {hip.lib_path()}").read()
+    lib = ctypes.CDLL(so0)
+    assert all(hasattr(lib, s) for s in declared_symbols())
+
+
 def test_only_c_symbols_are_exported_by_the_abi():
     # extern "C": the declared names are exported unmangled.
     out = os.popen(f"nm -D --defined-only {hip.lib_path()}").read()
