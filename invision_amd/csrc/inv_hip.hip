@@ -439,12 +439,14 @@ int cfg_occupancy(const CfgMeta &m) { return std::max(1, std::min(2, (160 * 1024
 //  - else half a round of 256x128 tiles (configuration 13: 256 W rows, 128 X
 //    rows), else half a round of 128x128 tiles (configuration 15, two
 //    workgroups per CU);
-//  - else (fewer than 128 tiles even at 128x128): 128x128 tiles, or for
-//    M <= 256 the 128x64 ring tile (configuration 4), with the K range split
-//    so that the units fill at most one workgroup per CU (2 to 4 splits of at
-//    least 8 k-tiles, when K has at least 32).  Sustained: 512x9728x2560 three
-//    ways 623 -> 669 TFLOP/s against two; 256x3072x3072 at 128x64 split two
-//    ways 234 against 204 (128x128, two ways) and 220 (four ways).  More
+//  - else (fewer than 128 tiles even at 128x128): the 128x128 ring tile
+//    (configuration 3), or for M <= 256 the 128x64 ring tile (configuration
+//    4), with the K range split so that the units fill at most one workgroup
+//    per CU (2 to 4 splits of at least 8 k-tiles, when K has at least 32).
+//    Sustained: 512x9728x2560 three ways 36.4 us against 38.7 for the
+//    register-staged 128x128 tile (configuration 15) and 40.8 two ways;
+//    256x3072x3072 at 128x64 split two ways 15.6 us against 17.2-18.5 for
+//    128x128 split two to four ways, and 16.3 with a 6-stage ring.  More
 //    splits lose to the partial-sum traffic, stream-K to its bookkeeping;
 //  - M <= 64: the W-streaming ring tiles with a short X tile.
 TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
@@ -471,7 +473,7 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
     } else if (tiles_of(13) * 2 >= cus) {
         c.cfg = 13;
     } else {
-        c.cfg = (M <= 256) ? 4 : 15;
+        c.cfg = (M <= 256) ? 4 : 3;
         const int64_t KT = (K + kCfg[c.cfg].bk - 1) / kCfg[c.cfg].bk;
         const int64_t ks = std::min<int64_t>({4, cus / tiles_of(c.cfg), KT / 8});
         if (KT >= 32 && ks >= 2) {
