@@ -1349,9 +1349,13 @@ __global__ void __launch_bounds__(C::NTHREADS, 1) gemm_nt_bf16_kernel(const Gemm
         fix.nseg = 1;
         gemm_unit<C, EPI, OUT, MODE, GATHER>(p, smem, tm, tn, 0, KT, fix);
     } else if constexpr (MODE == GRID_SPLITK) {
-        const int split = blockIdx.x % p.ksplit;
-        const int tile = blockIdx.x / p.ksplit;
-        grouped_tile(xcd_remap(tile, ntiles), p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+        // Logical units in split-major order, remapped so that consecutive ones
+        // share an XCD: the m-tiles of one n-tile and one K range then run on one
+        // XCD and its L2 fetches their W panel slice once.
+        const int L = xcd_remap(blockIdx.x, ntiles * p.ksplit);
+        const int split = L / ntiles;
+        const int tile = L - split * ntiles;
+        grouped_tile(tile, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
         UnitFix fix{};
         fix.tile = tile;
         fix.nseg = p.ksplit;
