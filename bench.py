@@ -886,9 +886,9 @@ def summarize_profile(workload, trace_dir, fetch_dir, write_dir, busy_dir=None, 
         mfma_cyc = med("SQ_VALU_MFMA_BUSY_CYCLES") / (cus * 4)  # per SIMD
         mops = med("SQ_INSTS_VALU_MFMA_MOPS_BF16") * 512.0
         waves = med("SQ_WAVE_CYCLES")
-        extra = {"mfma_busy_cycles_per_simd": mfma_cyc, "mfma_flops_counted": mops, "flops_expected": flops,
-                 "lds_wait_frac_of_wave_cycles": med("SQ_WAIT_INST_LDS") / waves,
-                 "lds_bank_conflicts": med("SQ_LDS_BANK_CONFLICT"), "counter_pass_duration_ns": dur}
+        extra.update({"mfma_busy_cycles_per_simd": mfma_cyc, "mfma_flops_counted": mops, "flops_expected": flops,
+                      "lds_wait_frac_of_wave_cycles": med("SQ_WAIT_INST_LDS") / waves,
+                      "lds_bank_conflicts": med("SQ_LDS_BANK_CONFLICT"), "counter_pass_duration_ns": dur})
         lines += ["Activity counters (one pass, their own run):", "", "```", cmds["busy"], "```", "",
                   "| Counter | Median per dispatch |", "|---|---|"]
         lines += [f"| {c} | {med(c):.4g} |" for c in sorted(bc)]
