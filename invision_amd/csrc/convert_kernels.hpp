@@ -517,14 +517,15 @@ __global__ void __launch_bounds__(512) im2col_bf16(const float *__restrict__ src
 // pixels of one row per thread) for all OC (>= n_oc) output channels.  Input
 // channels go CT_CC at a time through an LDS tile of the (CT_TH + 2) x
 // (CT_TW + 2) input window, each value rounded to bf16 (RNE) as the patch
-// matrix rounds it, and multiplied in fp32 with the filter's bf16 values (the
-// weight handle's rows, [out_ch x in_ch*9] in the reference's (ic, kh, kw)
-// order, row pitch ldw), so results match the im2col path but for the fp32
-// summation order.  The chunk's filter values sit in LDS too, OC consecutive
-// per tap, so each tap's are one broadcast read.  The loads of chunk c + 1
-// (image and filter) are issued before the multiplies of chunk c and written
-// to LDS after them: the kernel streams the image at the rate of its loads in
-// flight, not of one row's latency at a time.
+// matrix rounds it and stored as bf16 pairs of channels (2p, 2p + 1); the
+// filter's bf16 values (the weight handle's rows, [out_ch x in_ch*9] in the
+// reference's (ic, kh, kw) order, row pitch ldw) are paired the same way, OC
+// consecutive per tap so each tap's are one broadcast read.  v_dot2_f32_bf16
+// then multiplies a pair and adds both products to the fp32 sum: results
+// match the im2col path but for the summation order.  The loads of chunk
+// c + 1 (image and filter) are issued before the multiplies of chunk c and
+// written to LDS after them: the kernel streams the image at the rate of its
+// loads in flight, not of one row's latency at a time.
 // grid (ceil(outW / CT_TW), ceil(outH / CT_TH), batch).
 constexpr int CT_TH = 16, CT_TW = 64, CT_CC = 8;
 template <int OC>
@@ -532,54 +533,68 @@ __global__ void __launch_bounds__(256) conv3x3_thin(const float *__restrict__ sr
                                                     int64_t ldw, const float *__restrict__ bias,
                                                     float *__restrict__ dst, int C, int H, int W, int pad, int n_oc,
                                                     int outH, int outW) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    constexpr int CP = CT_CC / 2;                                     // channel pairs per chunk
     constexpr int TR = CT_TH + 2, TC = CT_TW + 2, PITCH = CT_TW + 4;  // PITCH: 16-byte aligned rows
-    constexpr int RPW = CT_CC * TR / 4;                               // window rows per wave and chunk
-    constexpr int NH = CT_CC * TR * (TC - 64);                        // halo values (columns 64..TC-1) per chunk
+    constexpr int RPW = CP * TR / 4;                                  // window row pairs per wave and chunk
+    constexpr int NH = CP * TR * (TC - 64);                           // halo pairs (columns 64..TC-1) per chunk
     constexpr int HPT = (NH + 255) / 256;                             // of them per thread
-    constexpr int NW = CT_CC * 9 * OC;                                // filter values per chunk
+    constexpr int NW = CP * 9 * OC;                                   // filter pairs per chunk
     constexpr int WPT = (NW + 255) / 256;                             // of them per thread
-    static_assert(RPW * 4 == CT_CC * TR && TC - 64 == 2, "window rows split evenly over the waves");
-    __shared__ __attribute__((aligned(16))) float tile[CT_CC][TR][PITCH];
-    __shared__ __attribute__((aligned(16))) float wts[CT_CC][9][OC];
+    static_assert(RPW * 4 == CP * TR && TC - 64 == 2 && CT_CC % 2 == 0, "window rows split evenly over the waves");
+    __shared__ __attribute__((aligned(16))) uint32_t tile[CP][TR][PITCH];
+    __shared__ __attribute__((aligned(16))) uint32_t wts[CP][9][OC];
     // wave-uniform row bookkeeping in scalar registers; a lane adds its column
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int oh0 = blockIdx.y * CT_TH, ow0 = blockIdx.x * CT_TW;
     const int b = blockIdx.z;
     const float *img = src + (int64_t)b * C * H * W;
+    const int64_t plane = (int64_t)H * W;
     const int ty = tid >> 4, tx = (tid & 15) * 4;
     const int iw = ow0 - pad + lane;
     const bool cin = (unsigned)iw < (unsigned)W;
-    float v[RPW], v2[HPT], fw[WPT];
-    // issue chunk c0's loads into v (window columns 0..63, one row per wave
-    // and step), v2 (the two halo columns, two values per window row, spread
+    float v[RPW][2], v2[HPT][2];
+    uint32_t fw[WPT];
+    // the two channels' values at one window position (zero outside the image or past C)
+    auto pair_at = [&](int ic, int ih, int iwp, bool ok, float (&out)[2]) {
+        const bool rin = ok && ic < C && (unsigned)ih < (unsigned)H;
+        const float *rp = img + (rin ? ((int64_t)ic * H + ih) * W + iwp : 0);
+        out[0] = rin ? rp[0] : 0.f;
+        out[1] = rin && ic + 1 < C ? rp[plane] : 0.f;
+    };
+    // issue chunk c0's loads into v (window columns 0..63 of channels 2p and
+    // 2p + 1, one row pair per wave and step), v2 (the two halo columns, spread
     // over all threads) and fw
     auto load = [&](int c0) {
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
             const int row = wave + 4 * i;
-            const int ch = row / TR, r = row - ch * TR;
-            const int ic = c0 + ch, ih = oh0 - pad + r;
-            const bool rin = ic < C && (unsigned)ih < (unsigned)H;
-            const float *rp = img + (rin ? ((int64_t)ic * H + ih) * W : 0);
-            v[i] = rin && cin ? rp[iw] : 0.f;
+            const int cp = row / TR, r = row - cp * TR;
+            pair_at(c0 + 2 * cp, oh0 - pad + r, iw, cin, v[i]);
         }
 #pragma unroll
         for (int i = 0; i < HPT; ++i) {
-            const int e = tid + 256 * i;  // (window row, halo column)
-            const int row = e >> 1, ch = row / TR, r = row - ch * TR;
-            const int ic = c0 + ch, ih = oh0 - pad + r, iwh = ow0 - pad + 64 + (e & 1);
-            const bool in = e < NH && ic < C && (unsigned)ih < (unsigned)H && (unsigned)iwh < (unsigned)W;
-            v2[i] = in ? img[((int64_t)ic * H + ih) * W + iwh] : 0.f;
+            const int e = tid + 256 * i;  // (window row pair, halo column)
+            const int row = e >> 1, cp = row / TR, r = row - cp * TR;
+            const int iwh = ow0 - pad + 64 + (e & 1);
+            pair_at(c0 + 2 * cp, oh0 - pad + r, iwh, e < NH && (unsigned)iwh < (unsigned)W, v2[i]);
         }
 #pragma unroll
         for (int i = 0; i < WPT; ++i) {
-            const int e = tid + 256 * i;  // (ch, tap, o)
-            const int ch = e / (9 * OC), t = (e / OC) % 9, o = e % OC;
-            const int ic = c0 + ch;
-            fw[i] = (e < NW && ic < C && o < n_oc) ? __uint_as_float((uint32_t)filt[o * ldw + ic * 9 + t] << 16) : 0.f;
+            const int e = tid + 256 * i;  // (pair, tap, o)
+            const int cp = e / (9 * OC), t = (e / OC) % 9, o = e % OC;
+            const int ic = c0 + 2 * cp;
+            const bool ok = e < NW && o < n_oc;
+            const uint32_t lo = (ok && ic < C) ? filt[o * ldw + ic * 9 + t] : 0u;
+            const uint32_t hi = (ok && ic + 1 < C) ? filt[o * ldw + (ic + 1) * 9 + t] : 0u;
+            fw[i] = lo | (hi << 16);
         }
     };
-    auto rounded = [](float x) { return __uint_as_float((uint32_t)bf16_rne(x) << 16); };
+    // two fp32 values -> their bf16 pair (RNE), the first in the low half
+    auto packed = [](const float (&x)[2]) {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{x[0], x[1]}, bf16x2_t));
+    };
     float acc[OC][4];
 #pragma unroll
     for (int o = 0; o < OC; ++o)
@@ -591,42 +606,45 @@ __global__ void __launch_bounds__(256) conv3x3_thin(const float *__restrict__ sr
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
             const int row = wave + 4 * i;
-            const int ch = row / TR, r = row - ch * TR;
-            tile[ch][r][lane] = rounded(v[i]);
+            const int cp = row / TR, r = row - cp * TR;
+            tile[cp][r][lane] = packed(v[i]);
         }
 #pragma unroll
         for (int i = 0; i < HPT; ++i) {
             const int e = tid + 256 * i;
-            const int row = e >> 1, ch = row / TR, r = row - ch * TR;
-            if (e < NH) tile[ch][r][64 + (e & 1)] = rounded(v2[i]);
+            const int row = e >> 1, cp = row / TR, r = row - cp * TR;
+            if (e < NH) tile[cp][r][64 + (e & 1)] = packed(v2[i]);
         }
 #pragma unroll
         for (int i = 0; i < WPT; ++i)
             if (tid + 256 * i < NW) (&wts[0][0][0])[tid + 256 * i] = fw[i];
         __syncthreads();
         if (c0 + CT_CC < C) load(c0 + CT_CC);  // in flight under this chunk's multiplies
-        const int nch = min(CT_CC, C - c0);
-        for (int ch = 0; ch < nch; ++ch) {
+#pragma unroll
+        for (int cp = 0; cp < CP; ++cp) {  // pairs past C hold zeros
 #pragma unroll
             for (int kh = 0; kh < 3; ++kh) {
-                const float *rp = &tile[ch][ty + kh][tx];
-                const float4 a = *(const float4 *)rp;
-                const float2 c = *(const float2 *)(rp + 4);
-                const float x[6] = {a.x, a.y, a.z, a.w, c.x, c.y};
+                const uint32_t *rp = &tile[cp][ty + kh][tx];
+                const uint4 a = *(const uint4 *)rp;
+                const uint2 c = *(const uint2 *)(rp + 4);
+                const uint32_t x[6] = {a.x, a.y, a.z, a.w, c.x, c.y};
 #pragma unroll
                 for (int kw = 0; kw < 3; ++kw) {
-                    float wv[OC];
+                    uint32_t wv[OC];
                     if constexpr (OC % 4 == 0) {
 #pragma unroll
-                        for (int o = 0; o < OC; o += 4) *(float4 *)&wv[o] = *(const float4 *)&wts[ch][kh * 3 + kw][o];
+                        for (int o = 0; o < OC; o += 4) *(uint4 *)&wv[o] = *(const uint4 *)&wts[cp][kh * 3 + kw][o];
                     } else {
 #pragma unroll
-                        for (int o = 0; o < OC; ++o) wv[o] = wts[ch][kh * 3 + kw][o];
+                        for (int o = 0; o < OC; ++o) wv[o] = wts[cp][kh * 3 + kw][o];
                     }
 #pragma unroll
                     for (int o = 0; o < OC; ++o)
 #pragma unroll
-                        for (int px = 0; px < 4; ++px) acc[o][px] = fmaf(x[px + kw], wv[o], acc[o][px]);
+                        for (int px = 0; px < 4; ++px)
+                            acc[o][px] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x[px + kw]),
+                                                                          __builtin_bit_cast(bf16x2_t, wv[o]),
+                                                                          acc[o][px], false);
                 }
             }
         }
