@@ -203,6 +203,10 @@ GATHER_SHAPES = [
     (1, 192, 512, 12, 12, 3, 3, 1, 1, None),
     (1, 128, 512, 13, 14, 3, 3, 1, 1, 16),
     (1, 64, 448, 15, 9, 3, 3, 1, 1, 9),
+    (3, 64, 64, 7, 5, 3, 3, 1, 1, None),     # the smallest channel counts, batch 3
+    (1, 64, 128, 2, 3, 3, 3, 1, 1, None),    # an image smaller than the window: most taps outside
+    (1, 128, 256, 21, 18, 3, 3, 2, 1, None), # stride 2 with padding
+    (1, 64, 96, 11, 13, 1, 1, 2, 0, None),   # 1x1 at stride 2 (forced: 1x1 takes the patch path by default)
 ]
 
 
