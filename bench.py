@@ -1056,7 +1056,15 @@ def main():
     }
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")
-        line["cpu_baseline"] = cpu_baseline(args.workload)
+        cb = cpu_baseline(args.workload)
+        # the GPU's kernel rate over each CPU leg's all-threads rate on the same GEMM
+        if headline_ok and cb:
+            cb["gpu_speedup"] = {"vs_port": round(achieved / cb["value"], 1),
+                                 "vs_openblas": round(achieved / cb["openblas_cblas_sgemm"]["all_threads"]["tflops"], 1)}
+            if "reference_sgemm2" in cb:
+                cb["gpu_speedup"]["vs_reference_sgemm2"] = round(
+                    achieved / cb["reference_sgemm2"]["all_threads"]["tflops"], 1)
+        line["cpu_baseline"] = cb
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)
