@@ -84,8 +84,10 @@ __device__ __forceinline__ int xcd_order(int bid, int count) {
 
 // The body exists only in the device pass; the host pass needs the launch stub
 // (buffer-resource types do not exist for the host target).
+// Two workgroups per CU with one key group; with two, each workgroup's stage
+// buffers fill most of the LDS and it runs alone.
 template <int D, bool CAUSAL, int OUT, int KS>
-__global__ void __launch_bounds__(256, 2) attn_fwd_kernel(const AttnParams p) {
+__global__ void __launch_bounds__(256, KS == 1 ? 2 : 1) attn_fwd_kernel(const AttnParams p) {
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int WQ = 4 / KS;             // query waves per key group
     constexpr int BQ = 32 * WQ, BK = kAttnBlockK;
