@@ -242,12 +242,26 @@ def run_workload(name, steps, warmup, check=True, host_path=False, warmup_second
         host_call = lambda: hip.call("inv_hip_linear", Xh.ctypes.data, hip.INV_DT_F32, w.handle, None, Yh.ctypes.data,
                                      hip.INV_DT_F32, M, K, R, hip.INV_EPI_NONE if epi == "none" else
                                      (hip.INV_EPI_SILU if epi == "silu" else hip.INV_EPI_GELU_ERF), 0)
-        host_call()
-        reps, th = 0, time.perf_counter()
-        while reps < 3 or time.perf_counter() - th < 1.0:
+        def time_host():
             host_call()
-            reps += 1
-        host_ms = (time.perf_counter() - th) * 1e3 / reps
+            reps, th = 0, time.perf_counter()
+            while reps < 3 or time.perf_counter() - th < 1.0:
+                host_call()
+                reps += 1
+            return (time.perf_counter() - th) * 1e3 / reps
+
+        # Row bands overlap upload, GEMM and download (the library's default);
+        # the one serial pass (INV_HIP_HOST_PIPELINE=0) is timed beside it.
+        host_ms = time_host()
+        prev = os.environ.get("INV_HIP_HOST_PIPELINE")
+        os.environ["INV_HIP_HOST_PIPELINE"] = "0"
+        try:
+            res["host_fp32_io_serial_ms"] = time_host()
+        finally:
+            if prev is None:
+                del os.environ["INV_HIP_HOST_PIPELINE"]
+            else:
+                os.environ["INV_HIP_HOST_PIPELINE"] = prev
         res["host_fp32_io_ms"] = host_ms
         res["host_fp32_io_tflops"] = flops / (host_ms * 1e-3) / 1e12
     if check:
@@ -1050,6 +1064,8 @@ def main():
         "parity_tol": res.get("parity_tol"),
         "launch_ms_p10_p50_p90": res["launch_ms_p10_p50_p90"],
         "host_fp32_io_tflops": round(res["host_fp32_io_tflops"], 2) if "host_fp32_io_tflops" in res else None,
+        "host_fp32_io_ms": round(res["host_fp32_io_ms"], 3) if "host_fp32_io_ms" in res else None,
+        "host_fp32_io_serial_ms": round(res["host_fp32_io_serial_ms"], 3) if "host_fp32_io_serial_ms" in res else None,
         "device": info["name"],
         "mfma_ceiling": ceiling,
         "vendor_gemm": vendor,

@@ -176,6 +176,16 @@ struct State {
     hipEvent_t tim0 = nullptr, tim1 = nullptr, st0 = nullptr, st1 = nullptr;
     hipEvent_t pin_ev[2] = {nullptr, nullptr};
     void *pin[2] = {nullptr, nullptr};
+    // Row-band pipeline of a host-pointer projection, made on its first use:
+    // an upload and a download stream (default priority), their events, and two
+    // pinned bounce buffers for the output (the input uses pin[]).
+    struct {
+        bool tried = false, ready = false;
+        hipStream_t up = nullptr, down = nullptr;
+        hipEvent_t start = nullptr, in_ev[2] = {nullptr, nullptr}, gemm_ev[2] = {nullptr, nullptr},
+                   out_ev[2] = {nullptr, nullptr};
+        void *pin_out[2] = {nullptr, nullptr};
+    } pipe;
     int cu_count = 0, clock_khz = 0;
     char name[256] = {0};
     Buf xin, x16, w16, win, yout, cin, bias, gate;
@@ -449,7 +459,7 @@ int cfg_occupancy(const CfgMeta &m) { return std::max(1, std::min(2, (160 * 1024
 //    128x128 split two to four ways, and 16.3 with a 6-stage ring.  More
 //    splits lose to the partial-sum traffic, stream-K to its bookkeeping;
 //  - M <= 64: the W-streaming ring tiles with a short X tile.
-TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
+TileChoice choose_tiles(int64_t M, int64_t N, int64_t K, int epi = INV_EPI_NONE) {
     TileChoice c{8, inv::GRID_TILES, 1};
     const int cus = g.cu_count > 0 ? g.cu_count : 256;
     auto tiles_of = [&](int cfg) { return ((M + kCfg[cfg].tm - 1) / kCfg[cfg].tm) * ((N + kCfg[cfg].tn - 1) / kCfg[cfg].tn); };
@@ -495,6 +505,11 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K) {
         c.mode = inv::GRID_STREAMK;
         c.count = std::max(1, env_int("INV_HIP_SK_GRID", (int)slots));
     }
+    if (epi == INV_EPI_SWIGLU) {
+        // gate | up wave columns over 256-row tiles, one workgroup per tile
+        if (!kCfg[c.cfg].swiglu_ok) c.cfg = (M > 128) ? 8 : 2;
+        c.mode = inv::GRID_TILES;
+    }
     return c;
 }
 
@@ -513,20 +528,17 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
              const float *bias, const float *Cin, int64_t ldc, float alpha, float beta, int64_t M, int64_t N,
              int64_t K, int epi, int64_t w_seg_k = 0, int64_t Kw = -1, int64_t nout = -1,
              const float *colscale = nullptr, const float *row_bias = nullptr,
-             const FixedWorkspace *fixed_ws = nullptr) {
+             const FixedWorkspace *fixed_ws = nullptr, const TileChoice *tiles = nullptr) {
     if (M == 0 || N == 0) return INV_OK;
     if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2) return fail(INV_ERR_ARG, "dimension too large");
     if (K % 8 || ldw % 8 || ldx % 8 || !aligned(W, 16) || !aligned(X, 16))
         return fail(INV_ERR_ARG, "internal: GEMM operands not 16-byte granular");
     if ((int64_t)256 * ldw * 2 >= ((int64_t)1 << 31) || (int64_t)256 * ldx * 2 >= ((int64_t)1 << 31))
         return fail(INV_ERR_UNSUPPORTED, "leading dimension too large for 32-bit buffer offsets");
-    TileChoice tc = choose_tiles(M, N, K);
-    if (epi == INV_EPI_SWIGLU) {
-        // gate | up wave columns over 256-row tiles, one workgroup per tile
-        if (!kCfg[tc.cfg].swiglu_ok) tc.cfg = (M > 128) ? 8 : 2;
-        tc.mode = inv::GRID_TILES;
-        if (beta != 0.0f) return fail(INV_ERR_UNSUPPORTED, "SwiGLU epilogue with beta != 0");
-    }
+    // tiles: a choice made by the caller (a row band of a larger product runs
+    // the whole product's tiles); else the choice for this M.
+    const TileChoice tc = tiles ? *tiles : choose_tiles(M, N, K, epi);
+    if (epi == INV_EPI_SWIGLU && beta != 0.0f) return fail(INV_ERR_UNSUPPORTED, "SwiGLU epilogue with beta != 0");
     if (row_bias && (epi != INV_EPI_NONE || !kCfg[tc.cfg].staged_epi))
         return fail(INV_ERR_UNSUPPORTED, "internal: a per-row bias needs the staged epilogue and no activation");
     inv::GemmParams p{};
@@ -1082,6 +1094,137 @@ int linear_noalloc_impl(const void *X, int x_dtype, inv_weight_t W, const float 
     return INV_OK;
 }
 
+// The band pipeline's streams, events and output bounce buffers, made on first
+// use.  False (and the serial path is taken) when they cannot be made.
+bool pipe_ready() {
+    auto &P = g.pipe;
+    if (P.tried) return P.ready;
+    P.tried = true;
+    bool ok = hipStreamCreateWithFlags(&P.up, hipStreamNonBlocking) == hipSuccess &&
+              hipStreamCreateWithFlags(&P.down, hipStreamNonBlocking) == hipSuccess &&
+              hipEventCreateWithFlags(&P.start, hipEventDisableTiming) == hipSuccess;
+    for (int k = 0; k < 2 && ok; ++k) {
+        for (hipEvent_t *e : {&P.in_ev[k], &P.gemm_ev[k], &P.out_ev[k]})
+            ok = ok && hipEventCreateWithFlags(e, hipEventDisableTiming) == hipSuccess &&
+                 hipEventRecord(*e, P.up) == hipSuccess;  // complete before first use
+        ok = ok && hipHostMalloc(&P.pin_out[k], kPinChunk, hipHostMallocDefault) == hipSuccess;
+    }
+    if (!ok) (void)hipGetLastError();
+    P.ready = ok;
+    return ok;
+}
+
+void release_pipe() {
+    auto &P = g.pipe;
+    for (hipStream_t s : {P.up, P.down})
+        if (s) (void)hipStreamSynchronize(s);
+    for (int k = 0; k < 2; ++k) {
+        if (P.pin_out[k]) (void)hipHostFree(P.pin_out[k]);
+        for (hipEvent_t e : {P.in_ev[k], P.gemm_ev[k], P.out_ev[k]})
+            if (e) (void)hipEventDestroy(e);
+    }
+    if (P.start) (void)hipEventDestroy(P.start);
+    for (hipStream_t s : {P.up, P.down})
+        if (s) (void)hipStreamDestroy(s);
+    P = {};
+}
+
+// Rows per band for a host-pointer projection, or 0 for one serial pass:
+// about M / INV_HIP_HOST_BANDS (default 8) rows in whole tile rows, but at
+// least ~16 MB of PCIe traffic per band, and fewer rows when a band's input or
+// output would not fit one bounce buffer (INV_HIP_HOST_BAND_MB caps the larger
+// side below that).  Larger bands leave more of the first upload and the last
+// download exposed; smaller ones pay ~80 us of host synchronisation, copy
+// dispatch and launches per band, and a part-filled GEMM.  Measured with fp32
+// X and Y (ms; one serial pass in brackets): 4608x3072 -> 9216 3.75 (5.01),
+// 4608x3072 -> 3072 1.83 (2.54), 4608x12288 -> 3072 4.86 (5.86), 2048x3840 ->
+// 15360 2.81 (3.46), 1024x3072 -> 3072 0.62 (0.73).  Only the one-launch tile
+// grid is banded: its elements do not depend on M, so each band gives the bits
+// one launch over all rows gives.
+int64_t host_band_rows(const TileChoice &tc, int64_t M, size_t in_row, size_t out_row) {
+    if (tc.mode != inv::GRID_TILES) return 0;
+    const size_t cap = std::min(kPinChunk, (size_t)std::max(1, env_int("INV_HIP_HOST_BAND_MB", 32)) << 20);
+    const int64_t tm = kCfg[tc.cfg].tm;
+    const int64_t bands = std::max(2, env_int("INV_HIP_HOST_BANDS", 8));
+    const int64_t fit = (int64_t)(cap / std::max(in_row, out_row)) / tm * tm;
+    const int64_t min_rows = round_up((int64_t)((16u << 20) / (in_row + out_row)) + 1, tm);
+    const int64_t mb = std::min(fit, std::max(min_rows, M / bands / tm * tm));
+    return (mb > 0 && M > mb) ? mb : 0;
+}
+
+// Y = X W^T (+ bias, activation) with X and Y in host memory, in row bands of
+// mb rows: band b+2's upload (host rows -> pinned -> device, `up` stream), band
+// b's conversion and GEMM (library stream) and band b's download (device ->
+// pinned, `down` stream, then pinned -> host rows) overlap, so the two PCIe
+// directions run at once and the GEMM hides under them.  Every band runs the
+// tile choice tc of the whole product.  Returns when Y is written.
+int linear_host_banded(const void *X, int x_dtype, inv_weight_t W, const float *bd, void *Y, int y_dtype, int64_t M,
+                       int64_t K, int64_t N, int epilogue, const TileChoice &tc, int64_t mb) {
+    auto &P = g.pipe;
+    const size_t xsz = (x_dtype == INV_DT_F32) ? 4 : 2, ysz = (y_dtype == INV_DT_F32) ? 4 : 2;
+    const int out = (y_dtype == INV_DT_F32) ? inv::OUT_F32 : inv::OUT_BF16;
+    const int64_t ldw = W->ldw;
+    const size_t in_row = (size_t)K * xsz, out_row = (size_t)N * ysz;
+    // bf16 rows already 16-byte granular land in the GEMM operand as they are
+    const bool direct = x_dtype == INV_DT_BF16 && K == ldw;
+    TRY(ensure(g.x16, (size_t)(M * ldw) * 2));
+    if (!direct) TRY(ensure(g.xin, (size_t)M * in_row));
+    TRY(ensure(g.yout, (size_t)M * out_row));
+    // The copy streams start after the library stream's earlier work (which
+    // may still read these buffers), and the bounce buffers after their uploads.
+    HIPCHK(hipEventRecord(P.start, g.stream));
+    HIPCHK(hipStreamWaitEvent(P.up, P.start, 0));
+    HIPCHK(hipStreamWaitEvent(P.down, P.start, 0));
+    for (int k = 0; k < 2; ++k) HIPCHK(hipEventSynchronize(g.pin_ev[k]));
+    const int64_t nb = (M + mb - 1) / mb;
+    auto rows_of = [&](int64_t b) { return std::min(mb, M - b * mb); };
+    auto upload_and_multiply = [&](int64_t b) -> int {
+        const int k = (int)(b & 1);
+        const int64_t r0 = b * mb, nr = rows_of(b);
+        HIPCHK(hipEventSynchronize(P.in_ev[k]));  // band b-2's upload has left pin[k]
+        par_copy_rows((char *)g.pin[k], in_row, (const char *)X + r0 * in_row, in_row, nr, in_row);
+        char *dst = direct ? (char *)g.x16.p + (size_t)r0 * ldw * 2 : (char *)g.xin.p + (size_t)r0 * in_row;
+        HIPCHK(hipMemcpyAsync(dst, g.pin[k], (size_t)nr * in_row, hipMemcpyHostToDevice, P.up));
+        HIPCHK(hipEventRecord(P.in_ev[k], P.up));
+        HIPCHK(hipStreamWaitEvent(g.stream, P.in_ev[k], 0));
+        uint16_t *xb = (uint16_t *)g.x16.p + r0 * ldw;
+        if (!direct) {
+            if (x_dtype == INV_DT_F32)
+                TRY(launch_cvt_rows_f32((const float *)g.xin.p + r0 * K, K, xb, ldw, nr, K, ldw));
+            else
+                TRY(launch_copy_rows_bf16((const uint16_t *)g.xin.p + r0 * K, K, xb, ldw, nr, K, ldw));
+        }
+        TRY(run_gemm(W->w, ldw, xb, ldw, (char *)g.yout.p + (size_t)r0 * out_row, N, out, bd, nullptr, N, 1.0f, 0.0f,
+                     nr, W->rows, ldw, epilogue, 0, -1, N, nullptr, nullptr, nullptr, &tc));
+        HIPCHK(hipEventRecord(P.gemm_ev[k], g.stream));
+        return INV_OK;
+    };
+    auto download = [&](int64_t b) -> int {  // pin_out[b & 1] is free (band b-2 drained)
+        const int k = (int)(b & 1);
+        HIPCHK(hipStreamWaitEvent(P.down, P.gemm_ev[k], 0));
+        HIPCHK(hipMemcpyAsync(P.pin_out[k], (const char *)g.yout.p + (size_t)(b * mb) * out_row,
+                              (size_t)rows_of(b) * out_row, hipMemcpyDeviceToHost, P.down));
+        HIPCHK(hipEventRecord(P.out_ev[k], P.down));
+        return INV_OK;
+    };
+    auto drain = [&](int64_t b) -> int {
+        const int k = (int)(b & 1);
+        HIPCHK(hipEventSynchronize(P.out_ev[k]));
+        par_copy_rows((char *)Y + (size_t)(b * mb) * out_row, out_row, (const char *)P.pin_out[k], out_row,
+                      rows_of(b), out_row);
+        return INV_OK;
+    };
+    for (int64_t b = 0; b < std::min<int64_t>(2, nb); ++b) TRY(upload_and_multiply(b));
+    for (int64_t b = 0; b < std::min<int64_t>(2, nb); ++b) TRY(download(b));
+    for (int64_t b = 0; b < nb; ++b) {
+        if (b + 2 < nb) TRY(upload_and_multiply(b + 2));
+        TRY(drain(b));
+        if (b + 2 < nb) TRY(download(b + 2));
+    }
+    g.calls++;
+    return INV_OK;
+}
+
 int linear_impl(const char *who, const void *X, int x_dtype, inv_weight_t W, const float *bias, void *Y, int y_dtype,
                 int64_t M, int64_t K, int64_t N, int epilogue, int flags, bool accumulate, const float *gate,
                 const NormArgs *nm = nullptr) {
@@ -1092,21 +1235,8 @@ int linear_impl(const char *who, const void *X, int x_dtype, inv_weight_t W, con
     const bool dev = (flags & INV_FLAG_DEVICE_PTRS) != 0;
     const int out = (y_dtype == INV_DT_F32) ? inv::OUT_F32 : inv::OUT_BF16;
     const size_t ysz = (y_dtype == INV_DT_F32) ? 4 : 2;
-
-    // Activations -> bf16 [M x ldw] (ldw = K rounded up to 8, zero padded), or
-    // with INV_FLAG_PRECISE and fp32 X: [Xh | Xl], each half K rounded up to 64,
-    // multiplied against the resident W read twice (the W k-tiles wrap).
     const bool precise = (flags & INV_FLAG_PRECISE) && x_dtype == INV_DT_F32;
-    const uint16_t *Xd = nullptr;
-    int64_t ldx = 0;
-    const int64_t kseg = precise ? round_up(K, 64) : W->ldw;
-    if (nm) {
-        if (precise) return fail(INV_ERR_UNSUPPORTED, "%s: INV_FLAG_PRECISE with a normalisation", who);
-        TRY(stage_normalized(who, (const float *)X, *nm, dev, M, K, &Xd, &ldx));
-    } else {
-        TRY(stage_operand(X, x_dtype, dev, false, M, K, K, precise ? 2 : 1, precise ? 0x2 : 0, precise ? 64 : 8,
-                          g.x16, g.xin, &Xd, &ldx));
-    }
+    if (nm && precise) return fail(INV_ERR_UNSUPPORTED, "%s: INV_FLAG_PRECISE with a normalisation", who);
 
     // Bias: explicit argument first, else the handle's.
     const float *bd = W->bias;
@@ -1137,6 +1267,33 @@ int linear_impl(const char *who, const void *X, int x_dtype, inv_weight_t W, con
                 TRY(h2d_rows(g.gate.p, gate, 1, (size_t)N * 4, (size_t)N * 4));
             gd = (const float *)g.gate.p;
         }
+    }
+
+    // Host X and Y of a plain projection: the row-band pipeline
+    // (INV_HIP_HOST_PIPELINE: 0 never, 2 required: a host call it cannot take fails).
+    if (!dev) {
+        const int pipe_mode = env_int("INV_HIP_HOST_PIPELINE", 1);
+        if (pipe_mode && !nm && !precise && !accumulate) {
+            const TileChoice tc = choose_tiles(M, W->rows, W->ldw, epilogue);
+            const int64_t mb = host_band_rows(tc, M, (size_t)K * (x_dtype == INV_DT_F32 ? 4 : 2), (size_t)N * ysz);
+            if (mb > 0 && pipe_ready())
+                return linear_host_banded(X, x_dtype, W, bd, Y, y_dtype, M, K, N, epilogue, tc, mb);
+        }
+        if (pipe_mode == 2)
+            return fail(INV_ERR_UNSUPPORTED, "%s: INV_HIP_HOST_PIPELINE=2 but this call is not banded", who);
+    }
+
+    // Activations -> bf16 [M x ldw] (ldw = K rounded up to 8, zero padded), or
+    // with INV_FLAG_PRECISE and fp32 X: [Xh | Xl], each half K rounded up to 64,
+    // multiplied against the resident W read twice (the W k-tiles wrap).
+    const uint16_t *Xd = nullptr;
+    int64_t ldx = 0;
+    const int64_t kseg = precise ? round_up(K, 64) : W->ldw;
+    if (nm) {
+        TRY(stage_normalized(who, (const float *)X, *nm, dev, M, K, &Xd, &ldx));
+    } else {
+        TRY(stage_operand(X, x_dtype, dev, false, M, K, K, precise ? 2 : 1, precise ? 0x2 : 0, precise ? 64 : 8,
+                          g.x16, g.xin, &Xd, &ldx));
     }
 
     void *Yd = Y;
@@ -1184,6 +1341,7 @@ int init_stream_objects() {
 
 void release_stream_objects() {
     if (g.stream) (void)hipStreamSynchronize(g.stream);
+    release_pipe();
     for (int k = 0; k < 2; ++k) {
         if (g.pin[k]) (void)hipHostFree(g.pin[k]);
         if (g.pin_ev[k]) (void)hipEventDestroy(g.pin_ev[k]);

@@ -1,0 +1,128 @@
+"""Row-band pipeline of inv_hip_linear with host pointers (marked gpu).
+
+With X and Y in host memory a product of at least two bands is uploaded,
+multiplied and downloaded band by band on overlapping streams.  Every band runs
+the tile choice of the whole product, so the banded call must give the same
+bits as the serial pass (INV_HIP_HOST_PIPELINE=0) and as the device-pointer
+call: bit-exact, for every epilogue, fp32 and bf16 X (16-byte granular rows
+and not) and Y, with a ragged last band.  INV_HIP_HOST_BAND_MB=1 makes bands of
+small products; the full-size product (4608 x 3072 x 9216) runs with the
+default bands and is also checked against the oracle on sampled rows.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from invision_amd import hip
+from invision_amd import quicknn_hip as q
+from invision_amd.bf16 import as_bf16_bits, bf16_bits_to_f32, round_bf16
+
+pytestmark = pytest.mark.gpu
+
+TOL_TIGHT = 2e-5
+
+
+def gen(seed, M, K, N):
+    oracle.rng_seed(seed)
+    X = oracle.randn_scaled((M, K), 1.0, False)
+    W = oracle.f32_to_bf16_rne(oracle.randn_scaled((N, K), 0.02, False))
+    b = oracle.randn_scaled((N,), 0.01, False)
+    return X, W, b
+
+
+def device_call(Xin, xdt, w, M, ydt, epi):
+    xd = q.DeviceArray.from_host(Xin, xdt)
+    yd = q.DeviceArray((M, w.N), ydt)
+    try:
+        q.linear_device(xd, w, yd, M, epilogue=epi)
+        return yd.to_host()
+    finally:
+        xd.free()
+        yd.free()
+
+
+# (M, K, N, epilogue, bias, X dtype, Y dtype): 1 MiB bands
+CASES = [
+    (1100, 1000, 1000, "none", True, "f32", "f32"),
+    (1100, 1000, 1000, "silu", False, "f32", "bf16"),
+    (777, 1001, 1500, "gelu", True, "bf16", "f32"),    # bf16 rows of 2002 bytes: staged, then copied
+    (1536, 512, 2048, "none", True, "bf16", "bf16"),   # bf16 rows land in the operand as they are
+    (1025, 1900, 300, "silu", True, "f32", "f32"),     # the input side sets the band; last band 1 row
+]
+
+
+@pytest.mark.parametrize("M,K,N,epi,bias,xdt,ydt", CASES)
+def test_banded_equals_serial_and_device(hiplib, monkeypatch, M, K, N, epi, bias, xdt, ydt):
+    X, W, b = gen(M + K + N, M, K, N)
+    Xin = X.astype(np.float32) if xdt == "f32" else as_bf16_bits(X)
+    monkeypatch.setenv("INV_HIP_HOST_BAND_MB", "1")
+    monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "2")  # fails unless the call is banded
+    with q.Weight(W, b if bias else None) as w:
+        y_band = q.linear(Xin, w, epilogue=epi, out_dtype=ydt)
+        monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "0")
+        y_serial = q.linear(Xin, w, epilogue=epi, out_dtype=ydt)
+        y_dev = device_call(Xin, xdt, w, M, ydt, epi)
+    print(f"  {M}x{K}x{N} {epi} bias={bias} X {xdt} Y {ydt}: banded == serial == device", flush=True)
+    np.testing.assert_array_equal(y_band, y_serial)
+    np.testing.assert_array_equal(y_band, y_dev)
+    yf = bf16_bits_to_f32(y_band) if ydt == "bf16" else y_band
+    ref = oracle.linear_bf16w(round_bf16(X), W, b if bias else None,
+                              {"none": oracle.EPI_NONE, "silu": oracle.EPI_SILU, "gelu": oracle.EPI_GELU}[epi])
+    assert oracle.normwise_err(yf, ref) <= (2.0 ** -8 + TOL_TIGHT if ydt == "bf16" else TOL_TIGHT)
+
+
+def test_banded_swiglu_equals_serial(hiplib, monkeypatch):
+    M, K, F = 900, 512, 640
+    oracle.rng_seed(41)
+    X = oracle.randn_scaled((M, K), 1.0, False)
+    Wg = oracle.f32_to_bf16_rne(oracle.randn_scaled((F, K), 0.02, False))
+    Wu = oracle.f32_to_bf16_rne(oracle.randn_scaled((F, K), 0.02, False))
+    monkeypatch.setenv("INV_HIP_HOST_BAND_MB", "1")
+    monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "2")
+    with q.Weight.gate_up(Wg, Wu) as w:
+        y_band = q.linear(as_bf16_bits(X), w, epilogue="swiglu")
+        monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "0")
+        y_serial = q.linear(as_bf16_bits(X), w, epilogue="swiglu")
+    np.testing.assert_array_equal(y_band, y_serial)
+
+
+def test_consecutive_banded_calls_and_interleaved_device_calls(hiplib, monkeypatch):
+    """Bounce buffers and events are reused across calls: alternate banded host
+    calls of different sizes with asynchronous device calls on the library stream."""
+    monkeypatch.setenv("INV_HIP_HOST_BAND_MB", "1")
+    X, W, b = gen(5, 1300, 768, 1024)
+    with q.Weight(W, b) as w:
+        want = {m: device_call(X[:m].astype(np.float32), "f32", w, m, "f32", "none") for m in (1300, 600)}
+        xd = q.DeviceArray.from_host(X.astype(np.float32), "f32")
+        yd = q.DeviceArray((1300, 1024), "f32")
+        try:
+            for m in (1300, 600, 1300):
+                q.linear_device(xd, w, yd, 1300, asynchronous=True)
+                monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "2")
+                y = q.linear(X[:m].astype(np.float32), w)
+                monkeypatch.delenv("INV_HIP_HOST_PIPELINE")
+                np.testing.assert_array_equal(y, want[m])
+            hip.call("inv_hip_synchronize")
+            np.testing.assert_array_equal(yd.to_host(), want[1300])
+        finally:
+            xd.free()
+            yd.free()
+
+
+def test_full_size_projection_banded(hiplib, monkeypatch):
+    """4608 x 3072 x 9216 with fp32 host X and Y (eleven bands of 448 rows,
+    two 224-row tiles each): the same bits as the device-pointer call, and
+    the oracle on sampled rows, band edges among them."""
+    M, K, N = 4608, 3072, 9216
+    X, W, b = gen(2, M, K, N)
+    X32 = X.astype(np.float32)
+    with q.Weight(W, b) as w:
+        monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "2")
+        y = q.linear(X32, w)
+        monkeypatch.delenv("INV_HIP_HOST_PIPELINE")
+        y_dev = device_call(X32, "f32", w, M, "f32", "none")
+    np.testing.assert_array_equal(y, y_dev)
+    rows = np.unique(np.concatenate([[0, 447, 448, 4479, 4480, M - 1], np.random.default_rng(0).choice(M, 24, replace=False)]))
+    e = oracle.normwise_err(y[rows], oracle.linear_bf16w(round_bf16(X[rows]), W, b, oracle.EPI_NONE))
+    print(f"  sampled rows normwise err {e:.3e}", flush=True)
+    assert e <= TOL_TIGHT
