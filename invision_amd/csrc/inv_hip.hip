@@ -937,35 +937,34 @@ struct NormArgs {
     float eps;
 };
 
-// Stage X = norm(X_f32) as bf16 [M x round_up(K, 8)] in g.x16 (X, scale and
-// shift host or device per `dev`).
-int stage_normalized(const char *who, const float *X, const NormArgs &nm, bool dev, int64_t M, int64_t K,
-                     const uint16_t **out, int64_t *out_ld) {
-    const int64_t ldw = round_up(K, 8);
-    const float *xd = X, *ad = nm.scale, *bd = nm.shift;
+// The normalisation's per-column vectors as the row kernels read them: host
+// vectors uploaded, device vectors not 16-byte aligned copied (the register
+// kernel reads them 16 bytes at a time); null stays null.
+int stage_norm_vectors(const NormArgs &nm, bool dev, int64_t K, const float **ad, const float **bd) {
+    *ad = nm.scale;
+    *bd = nm.shift;
+    const size_t vb = (size_t)K * 4;
     if (!dev) {
-        TRY(ensure(g.xin, (size_t)(M * K) * 4));
-        TRY(h2d_rows(g.xin.p, X, M, (size_t)K * 4, (size_t)K * 4));
-        xd = (const float *)g.xin.p;
-        const size_t vb = (size_t)K * 4;
         TRY(ensure(g.nvec, 2 * vb));
         if (nm.scale) TRY(h2d_rows(g.nvec.p, nm.scale, 1, vb, vb));
         if (nm.shift) TRY(h2d_rows((char *)g.nvec.p + vb, nm.shift, 1, vb, vb));
-        ad = nm.scale ? (const float *)g.nvec.p : nullptr;
-        bd = nm.shift ? (const float *)((char *)g.nvec.p + vb) : nullptr;
-    } else if (!aligned(X, 4)) {
-        return fail(INV_ERR_ARG, "%s: X not 4-byte aligned", who);
-    } else if ((ad && !aligned(ad, 16)) || (bd && !aligned(bd, 16))) {
-        // the register kernel reads the per-column vectors 16 bytes at a time
-        const size_t vb = (size_t)K * 4;
+    } else if ((*ad && !aligned(*ad, 16)) || (*bd && !aligned(*bd, 16))) {
         TRY(ensure(g.nvec, 2 * vb));
-        if (ad) HIPCHK(hipMemcpyAsync(g.nvec.p, ad, vb, hipMemcpyDeviceToDevice, g.stream));
-        if (bd) HIPCHK(hipMemcpyAsync((char *)g.nvec.p + vb, bd, vb, hipMemcpyDeviceToDevice, g.stream));
-        ad = ad ? (const float *)g.nvec.p : nullptr;
-        bd = bd ? (const float *)((char *)g.nvec.p + vb) : nullptr;
+        if (*ad) HIPCHK(hipMemcpyAsync(g.nvec.p, *ad, vb, hipMemcpyDeviceToDevice, g.stream));
+        if (*bd) HIPCHK(hipMemcpyAsync((char *)g.nvec.p + vb, *bd, vb, hipMemcpyDeviceToDevice, g.stream));
+    } else {
+        return INV_OK;
     }
-    TRY(ensure(g.x16, (size_t)(M * ldw) * 2));
-    uint16_t *d = (uint16_t *)g.x16.p;
+    *ad = nm.scale ? (const float *)g.nvec.p : nullptr;
+    *bd = nm.shift ? (const float *)((char *)g.nvec.p + vb) : nullptr;
+    return INV_OK;
+}
+
+// d[M x ldw] bf16 = norm(xd[M x K] fp32) on the library stream, one workgroup
+// per row (ad, bd from stage_norm_vectors).
+int launch_norm_rows(const float *xd, const NormArgs &nm, const float *ad, const float *bd, int64_t M, int64_t K,
+                     uint16_t *d, int64_t ldw) {
+    if (M == 0) return INV_OK;
     const bool in_regs = K % 4 == 0 && K <= 4 * 256 * inv::NORM_ROW_GROUPS && aligned(xd, 16);
     if (in_regs) {
         const int64_t groups = (K / 4 + 255) / 256;  // register groups of 4 columns per thread
@@ -992,6 +991,27 @@ int stage_normalized(const char *who, const float *X, const NormArgs &nm, bool d
         hipLaunchKernelGGL(inv::norm_rows_f32_bf16<inv::NORM_RMS>, dim3((unsigned)M), dim3(256), 0, g.stream, xd, K,
                            ad, bd, nm.eps, d, ldw, K, ldw);
     HIPCHK(hipGetLastError());
+    return INV_OK;
+}
+
+// Stage X = norm(X_f32) as bf16 [M x round_up(K, 8)] in g.x16 (X, scale and
+// shift host or device per `dev`).
+int stage_normalized(const char *who, const float *X, const NormArgs &nm, bool dev, int64_t M, int64_t K,
+                     const uint16_t **out, int64_t *out_ld) {
+    const int64_t ldw = round_up(K, 8);
+    const float *xd = X;
+    if (!dev) {
+        TRY(ensure(g.xin, (size_t)(M * K) * 4));
+        TRY(h2d_rows(g.xin.p, X, M, (size_t)K * 4, (size_t)K * 4));
+        xd = (const float *)g.xin.p;
+    } else if (!aligned(X, 4)) {
+        return fail(INV_ERR_ARG, "%s: X not 4-byte aligned", who);
+    }
+    const float *ad = nullptr, *bd = nullptr;
+    TRY(stage_norm_vectors(nm, dev, K, &ad, &bd));
+    TRY(ensure(g.x16, (size_t)(M * ldw) * 2));
+    uint16_t *d = (uint16_t *)g.x16.p;
+    TRY(launch_norm_rows(xd, nm, ad, bd, M, K, d, ldw));
     *out = d;
     *out_ld = ldw;
     return INV_OK;
@@ -1131,9 +1151,10 @@ void release_pipe() {
 
 // Rows per band for a host-pointer projection, or 0 for one serial pass:
 // about M / INV_HIP_HOST_BANDS (default 8) rows in whole tile rows, but at
-// least ~16 MB of PCIe traffic per band, and fewer rows when a band's input or
-// output would not fit one bounce buffer (INV_HIP_HOST_BAND_MB caps the larger
-// side below that).  Larger bands leave more of the first upload and the last
+// least ~16 MB of PCIe traffic per band, and fewer rows when a band's upload
+// (up_row bytes per row: its X rows, and its Y rows when Y is accumulated) or
+// download would not fit one bounce buffer (INV_HIP_HOST_BAND_MB caps the
+// larger side below that).  Larger bands leave more of the first upload and the last
 // download exposed; smaller ones pay ~80 us of host synchronisation, copy
 // dispatch and launches per band, and a part-filled GEMM.  Measured with fp32
 // X and Y (ms; one serial pass in brackets): 4608x3072 -> 9216 3.75 (5.01),
@@ -1141,32 +1162,44 @@ void release_pipe() {
 // 15360 2.81 (3.46), 1024x3072 -> 3072 0.62 (0.73).  Only the one-launch tile
 // grid is banded: its elements do not depend on M, so each band gives the bits
 // one launch over all rows gives.
-int64_t host_band_rows(const TileChoice &tc, int64_t M, size_t in_row, size_t out_row) {
+int64_t host_band_rows(const TileChoice &tc, int64_t M, size_t up_row, size_t out_row) {
     if (tc.mode != inv::GRID_TILES) return 0;
     const size_t cap = std::min(kPinChunk, (size_t)std::max(1, env_int("INV_HIP_HOST_BAND_MB", 32)) << 20);
     const int64_t tm = kCfg[tc.cfg].tm;
     const int64_t bands = std::max(2, env_int("INV_HIP_HOST_BANDS", 8));
-    const int64_t fit = (int64_t)(cap / std::max(in_row, out_row)) / tm * tm;
-    const int64_t min_rows = round_up((int64_t)((16u << 20) / (in_row + out_row)) + 1, tm);
+    const int64_t fit = (int64_t)(cap / std::max(up_row, out_row)) / tm * tm;
+    const int64_t min_rows = round_up((int64_t)((16u << 20) / (up_row + out_row)) + 1, tm);
     const int64_t mb = std::min(fit, std::max(min_rows, M / bands / tm * tm));
     return (mb > 0 && M > mb) ? mb : 0;
 }
 
+// The row-band pipeline's optional stages: X normalised (fp32 X; the
+// vectors already on the device), and Y accumulated (Y += gate * (...), Y
+// uploaded band by band as well).
+struct BandExtras {
+    const NormArgs *nm = nullptr;
+    const float *nscale = nullptr, *nshift = nullptr;
+    bool accumulate = false;
+    const float *gate = nullptr;  // device, or null
+};
+
 // Y = X W^T (+ bias, activation) with X and Y in host memory, in row bands of
 // mb rows: band b+2's upload (host rows -> pinned -> device, `up` stream), band
-// b's conversion and GEMM (library stream) and band b's download (device ->
-// pinned, `down` stream, then pinned -> host rows) overlap, so the two PCIe
-// directions run at once and the GEMM hides under them.  Every band runs the
-// tile choice tc of the whole product.  Returns when Y is written.
+// b's conversion (or normalisation) and GEMM (library stream) and band b's
+// download (device -> pinned, `down` stream, then pinned -> host rows) overlap,
+// so the two PCIe directions run at once and the GEMM hides under them.  When
+// Y is accumulated, a band's Y rows travel up behind its X rows in the same
+// bounce buffer.  Every band runs the tile choice tc of the whole product.
+// Returns when Y is written.
 int linear_host_banded(const void *X, int x_dtype, inv_weight_t W, const float *bd, void *Y, int y_dtype, int64_t M,
-                       int64_t K, int64_t N, int epilogue, const TileChoice &tc, int64_t mb) {
+                       int64_t K, int64_t N, int epilogue, const TileChoice &tc, int64_t mb, const BandExtras &ex) {
     auto &P = g.pipe;
     const size_t xsz = (x_dtype == INV_DT_F32) ? 4 : 2, ysz = (y_dtype == INV_DT_F32) ? 4 : 2;
     const int out = (y_dtype == INV_DT_F32) ? inv::OUT_F32 : inv::OUT_BF16;
     const int64_t ldw = W->ldw;
     const size_t in_row = (size_t)K * xsz, out_row = (size_t)N * ysz;
     // bf16 rows already 16-byte granular land in the GEMM operand as they are
-    const bool direct = x_dtype == INV_DT_BF16 && K == ldw;
+    const bool direct = !ex.nm && x_dtype == INV_DT_BF16 && K == ldw;
     TRY(ensure(g.x16, (size_t)(M * ldw) * 2));
     if (!direct) TRY(ensure(g.xin, (size_t)M * in_row));
     TRY(ensure(g.yout, (size_t)M * out_row));
@@ -1182,20 +1215,29 @@ int linear_host_banded(const void *X, int x_dtype, inv_weight_t W, const float *
         const int k = (int)(b & 1);
         const int64_t r0 = b * mb, nr = rows_of(b);
         HIPCHK(hipEventSynchronize(P.in_ev[k]));  // band b-2's upload has left pin[k]
-        par_copy_rows((char *)g.pin[k], in_row, (const char *)X + r0 * in_row, in_row, nr, in_row);
+        char *pin = (char *)g.pin[k];
+        char *yb = (char *)g.yout.p + (size_t)r0 * out_row;
+        par_copy_rows(pin, in_row, (const char *)X + r0 * in_row, in_row, nr, in_row);
+        if (ex.accumulate) par_copy_rows(pin + nr * in_row, out_row, (const char *)Y + r0 * out_row, out_row, nr, out_row);
         char *dst = direct ? (char *)g.x16.p + (size_t)r0 * ldw * 2 : (char *)g.xin.p + (size_t)r0 * in_row;
-        HIPCHK(hipMemcpyAsync(dst, g.pin[k], (size_t)nr * in_row, hipMemcpyHostToDevice, P.up));
+        HIPCHK(hipMemcpyAsync(dst, pin, (size_t)nr * in_row, hipMemcpyHostToDevice, P.up));
+        if (ex.accumulate)
+            HIPCHK(hipMemcpyAsync(yb, pin + nr * in_row, (size_t)nr * out_row, hipMemcpyHostToDevice, P.up));
         HIPCHK(hipEventRecord(P.in_ev[k], P.up));
         HIPCHK(hipStreamWaitEvent(g.stream, P.in_ev[k], 0));
         uint16_t *xb = (uint16_t *)g.x16.p + r0 * ldw;
-        if (!direct) {
+        if (ex.nm) {
+            TRY(launch_norm_rows((const float *)g.xin.p + r0 * K, *ex.nm, ex.nscale, ex.nshift, nr, K, xb, ldw));
+        } else if (!direct) {
             if (x_dtype == INV_DT_F32)
                 TRY(launch_cvt_rows_f32((const float *)g.xin.p + r0 * K, K, xb, ldw, nr, K, ldw));
             else
                 TRY(launch_copy_rows_bf16((const uint16_t *)g.xin.p + r0 * K, K, xb, ldw, nr, K, ldw));
         }
-        TRY(run_gemm(W->w, ldw, xb, ldw, (char *)g.yout.p + (size_t)r0 * out_row, N, out, bd, nullptr, N, 1.0f, 0.0f,
-                     nr, W->rows, ldw, epilogue, 0, -1, N, nullptr, nullptr, nullptr, &tc));
+        // accumulating reads the band's Y as C (beta = 1) in place, as the one-pass call does
+        TRY(run_gemm(W->w, ldw, xb, ldw, yb, N, out, bd, ex.accumulate ? (const float *)yb : nullptr, N, 1.0f,
+                     ex.accumulate ? 1.0f : 0.0f, nr, W->rows, ldw, epilogue, 0, -1, N, ex.gate, nullptr, nullptr,
+                     &tc));
         HIPCHK(hipEventRecord(P.gemm_ev[k], g.stream));
         return INV_OK;
     };
@@ -1269,15 +1311,24 @@ int linear_impl(const char *who, const void *X, int x_dtype, inv_weight_t W, con
         }
     }
 
-    // Host X and Y of a plain projection: the row-band pipeline
-    // (INV_HIP_HOST_PIPELINE: 0 never, 2 required: a host call it cannot take fails).
+    // Host X and Y: the row-band pipeline (INV_HIP_HOST_PIPELINE: 0 never, 2
+    // required: a host call it cannot take fails).
     if (!dev) {
         const int pipe_mode = env_int("INV_HIP_HOST_PIPELINE", 1);
-        if (pipe_mode && !nm && !precise && !accumulate) {
+        if (pipe_mode && !precise) {
             const TileChoice tc = choose_tiles(M, W->rows, W->ldw, epilogue);
-            const int64_t mb = host_band_rows(tc, M, (size_t)K * (x_dtype == INV_DT_F32 ? 4 : 2), (size_t)N * ysz);
-            if (mb > 0 && pipe_ready())
-                return linear_host_banded(X, x_dtype, W, bd, Y, y_dtype, M, K, N, epilogue, tc, mb);
+            const size_t up_row = (size_t)K * (x_dtype == INV_DT_F32 ? 4 : 2) + (accumulate ? (size_t)N * ysz : 0);
+            const int64_t mb = host_band_rows(tc, M, up_row, (size_t)N * ysz);
+            if (mb > 0 && pipe_ready()) {
+                BandExtras ex;
+                ex.accumulate = accumulate;
+                ex.gate = gd;
+                if (nm) {
+                    ex.nm = nm;
+                    TRY(stage_norm_vectors(*nm, false, K, &ex.nscale, &ex.nshift));
+                }
+                return linear_host_banded(X, x_dtype, W, bd, Y, y_dtype, M, K, N, epilogue, tc, mb, ex);
+            }
         }
         if (pipe_mode == 2)
             return fail(INV_ERR_UNSUPPORTED, "%s: INV_HIP_HOST_PIPELINE=2 but this call is not banded", who);

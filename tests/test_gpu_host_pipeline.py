@@ -7,7 +7,9 @@ bits as the serial pass (INV_HIP_HOST_PIPELINE=0) and as the device-pointer
 call: bit-exact, for every epilogue, fp32 and bf16 X (16-byte granular rows
 and not) and Y, with a ragged last band.  INV_HIP_HOST_BAND_MB=1 makes bands of
 small products; the full-size product (4608 x 3072 x 9216) runs with the
-default bands and is also checked against the oracle on sampled rows.
+default bands and is also checked against the oracle on sampled rows.  The
+normalised (inv_hip_linear_norm) and accumulating (inv_hip_linear_gated_add)
+entry points band the same way.
 """
 import numpy as np
 import pytest
@@ -126,3 +128,57 @@ def test_full_size_projection_banded(hiplib, monkeypatch):
     e = oracle.normwise_err(y[rows], oracle.linear_bf16w(round_bf16(X[rows]), W, b, oracle.EPI_NONE))
     print(f"  sampled rows normwise err {e:.3e}", flush=True)
     assert e <= TOL_TIGHT
+
+
+@pytest.mark.parametrize("norm,K", [("adaln", 1024), ("rms", 1024), ("adaln", 1001)])
+def test_banded_linear_norm_equals_serial(hiplib, monkeypatch, norm, K):
+    """inv_hip_linear_norm with host X and Y: each band normalises its own rows
+    (K = 1001 takes the row kernel without register groups)."""
+    M, N = 1100, 1000
+    X, W, b = gen(K + 7, M, K, N)
+    rng = np.random.default_rng(K)
+    scale = (rng.standard_normal(K) * 0.3).astype(np.float32)
+    shift = (rng.standard_normal(K) * 0.3).astype(np.float32) if norm == "adaln" else None
+    X32 = X.astype(np.float32)
+    monkeypatch.setenv("INV_HIP_HOST_BAND_MB", "1")
+    monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "2")
+    with q.Weight(W, b) as w:
+        y_band = q.linear_norm(X32, norm, w, scale, shift, epilogue="silu")
+        monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "0")
+        y_serial = q.linear_norm(X32, norm, w, scale, shift, epilogue="silu")
+    print(f"  {norm} {M}x{K}x{N}: banded == serial", flush=True)
+    np.testing.assert_array_equal(y_band, y_serial)
+    assert np.all(np.isfinite(y_band))
+
+
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_banded_gated_add_equals_serial_and_device(hiplib, monkeypatch, xdt):
+    """inv_hip_linear_gated_add with host X and Y: a band's Y rows go up behind
+    its X rows and are updated in place (Y += gate * (X W^T + b))."""
+    M, K, N = 1300, 768, 1024
+    X, W, b = gen(9, M, K, N)
+    rng = np.random.default_rng(9)
+    Y0 = rng.standard_normal((M, N)).astype(np.float32)
+    gate = (rng.standard_normal(N) * 0.5).astype(np.float32)
+    Xin = X.astype(np.float32) if xdt == "f32" else as_bf16_bits(X)
+    monkeypatch.setenv("INV_HIP_HOST_BAND_MB", "1")
+    with q.Weight(W, b) as w:
+        monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "2")
+        y_band = Y0.copy()
+        q.linear_gated_add(y_band, Xin, w, gate)
+        monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "0")
+        y_serial = Y0.copy()
+        q.linear_gated_add(y_serial, Xin, w, gate)
+        xd = q.DeviceArray.from_host(Xin, xdt)
+        yd = q.DeviceArray.from_host(Y0, "f32")
+        gd = q.DeviceArray.from_host(gate, "f32")
+        try:
+            q.linear_gated_add_device(xd, w, yd, M, gate=gd)
+            y_dev = yd.to_host()
+        finally:
+            for d in (xd, yd, gd):
+                d.free()
+    np.testing.assert_array_equal(y_band, y_serial)
+    np.testing.assert_array_equal(y_band, y_dev)
+    ref = Y0.astype(np.float64) + gate * oracle.linear_bf16w(round_bf16(X), W, b, oracle.EPI_NONE)
+    assert oracle.normwise_err(y_band - Y0, ref - Y0) <= TOL_TIGHT
