@@ -1256,12 +1256,24 @@ int linear_host_banded(const void *X, int x_dtype, inv_weight_t W, const float *
                       rows_of(b), out_row);
         return INV_OK;
     };
-    for (int64_t b = 0; b < std::min<int64_t>(2, nb); ++b) TRY(upload_and_multiply(b));
-    for (int64_t b = 0; b < std::min<int64_t>(2, nb); ++b) TRY(download(b));
-    for (int64_t b = 0; b < nb; ++b) {
-        if (b + 2 < nb) TRY(upload_and_multiply(b + 2));
-        TRY(drain(b));
-        if (b + 2 < nb) TRY(download(b + 2));
+    auto run = [&]() -> int {
+        for (int64_t b = 0; b < std::min<int64_t>(2, nb); ++b) TRY(upload_and_multiply(b));
+        for (int64_t b = 0; b < std::min<int64_t>(2, nb); ++b) TRY(download(b));
+        for (int64_t b = 0; b < nb; ++b) {
+            if (b + 2 < nb) TRY(upload_and_multiply(b + 2));
+            TRY(drain(b));
+            if (b + 2 < nb) TRY(download(b + 2));
+        }
+        return INV_OK;
+    };
+    const int rc = run();
+    if (rc != INV_OK) {
+        // copies still in flight must not outlive the call: the bounce buffers
+        // are reused by the next one
+        (void)hipStreamSynchronize(P.up);
+        (void)hipStreamSynchronize(g.stream);
+        (void)hipStreamSynchronize(P.down);
+        return rc;
     }
     g.calls++;
     return INV_OK;
