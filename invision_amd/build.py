@@ -27,7 +27,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
-NUM_GEMM_CONFIGS = 17  # INV_GEMM_NUM_CONFIGS in csrc/gemm_configs.hpp
+NUM_GEMM_CONFIGS = 18  # INV_GEMM_NUM_CONFIGS in csrc/gemm_configs.hpp
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",

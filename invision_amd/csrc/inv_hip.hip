@@ -438,12 +438,15 @@ int cfg_occupancy(const CfgMeta &m) { return std::max(1, std::min(2, (160 * 1024
 
 // Pick a tile shape and how the grid covers it (rules from measurements on
 // MI355X, 256 CUs):
-//  - at least 3/4 of a round of 256x256 tiles: the 256x256 register-staged tile
-//    on 32x32 MFMAs (configuration 8) or the 256x224 one on 16x16 MFMAs
-//    (configuration 16), by last-round fill and edge padding: sustained, c2
-//    1131 -> 1190 TFLOP/s (756 tiles = 2.95 rounds against 648 = 2.53),
-//    4608x9216x3072 1217 -> 1315, 9216x15360x3840 1040 -> 1126, and
-//    9216x3840x11520 1170 against 1150 (both fill their last round alike);
+//  - at least 3/4 of a round of 256x256 tiles: the 256x256 tile of 8 waves on
+//    16x16 MFMAs, two waves per SIMD (configuration 17), or the 256x224 one of 4
+//    waves (configuration 16), by last-round fill and edge padding, 17 doing
+//    ~10% more per tile.  Sustained, in one run (TFLOP/s, 16 / 17, and the
+//    32x32-MFMA 256x256 tile, configuration 8, that 17 replaced):
+//    9216x3840x15360 1157 / 1208 (8: 1158), 9216x3840x11520 1150 / 1217 (1168),
+//    2048x3840x15360 1021 / 1241 (1192), 9216x15360x3840 1122 / 1088 (1047),
+//    9216x3840x3840 1125 / 1054 (993), c2 1188 / 1180 (1124: 756 tiles = 2.95
+//    rounds against 648 = 2.53);
 //  - M <= 128 and half a round of 256x128 tiles: configuration 13, whose 128 X
 //    rows cover M (a 256x256 tile would spend half its MFMAs on zero rows);
 //  - else half a round of 256x128 tiles (configuration 13: 256 W rows, 128 X
@@ -460,7 +463,7 @@ int cfg_occupancy(const CfgMeta &m) { return std::max(1, std::min(2, (160 * 1024
 //    splits lose to the partial-sum traffic, stream-K to its bookkeeping;
 //  - M <= 64: the W-streaming ring tiles with a short X tile.
 TileChoice choose_tiles(int64_t M, int64_t N, int64_t K, int epi = INV_EPI_NONE) {
-    TileChoice c{8, inv::GRID_TILES, 1};
+    TileChoice c{17, inv::GRID_TILES, 1};
     const int cus = g.cu_count > 0 ? g.cu_count : 256;
     auto tiles_of = [&](int cfg) { return ((M + kCfg[cfg].tm - 1) / kCfg[cfg].tm) * ((N + kCfg[cfg].tn - 1) / kCfg[cfg].tn); };
     if (M <= 32) {
@@ -469,17 +472,17 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K, int epi = INV_EPI_NONE)
         c.cfg = 4;
     } else if (M <= 128 && tiles_of(13) * 2 >= cus) {
         c.cfg = 13;  // 128 X rows cover M: a 256-row tile would multiply zeros for half its MFMAs
-    } else if (tiles_of(8) * 4 >= (int64_t)cus * 3) {
-        // 256x256 tiles on 32x32 MFMAs (8) or 256x224 on 16x16 (16), whichever leaves fewer
-        // CUs idle in the last round and fewer MFMAs on zero padding at the edges; 16 runs a
-        // full round about 2% slower (measured at equal fill).
+    } else if (tiles_of(17) * 4 >= (int64_t)cus * 3) {
+        // 256x256 tiles of 8 waves (17) or 256x224 of 4 waves (16), whichever leaves fewer
+        // CUs idle in the last round and fewer MFMAs on zero padding at the edges; 17 runs a
+        // full round about 10% faster (fitted over ten shapes: 0.93 to 1.16).
         auto score = [&](int cfg) {
             const int64_t tm = (M + kCfg[cfg].tm - 1) / kCfg[cfg].tm, tn = (N + kCfg[cfg].tn - 1) / kCfg[cfg].tn;
             const int64_t t = tm * tn, rounds = (t + cus - 1) / cus;
             return (double)t / (double)(rounds * cus) * (double)M / (double)(tm * kCfg[cfg].tm) * (double)N /
                    (double)(tn * kCfg[cfg].tn);
         };
-        c.cfg = (0.98 * score(16) > score(8)) ? 16 : 8;
+        c.cfg = (score(16) > 1.10 * score(17)) ? 16 : 17;
     } else if (tiles_of(13) * 2 >= cus) {
         c.cfg = 13;
     } else {

@@ -165,8 +165,8 @@ GRID_MODES = {  # INV_HIP_MODE / INV_HIP_KSPLIT / INV_HIP_SK_GRID
 }
 
 
-ALL_CFGS = list(range(17))  # INV_GEMM_NUM_CONFIGS in invision_amd/csrc/gemm_configs.hpp
-REG_STAGED_CFGS = [8, 9, 10, 11, 12, 13, 14, 15, 16]  # 11-14, 16: unequal W and X copy-chunk counts
+ALL_CFGS = list(range(18))  # INV_GEMM_NUM_CONFIGS in invision_amd/csrc/gemm_configs.hpp
+REG_STAGED_CFGS = [8, 9, 10, 11, 12, 13, 14, 15, 16, 17]  # 11-14, 16: unequal W and X copy-chunk counts
 
 
 @pytest.mark.parametrize("cfg", ALL_CFGS)
@@ -184,7 +184,7 @@ def test_every_tile_shape_and_grid_mode(hiplib, monkeypatch, cfg, grid):
     np.testing.assert_array_equal(y, y2)  # deterministic, counters reset
 
 
-@pytest.mark.parametrize("cfg", [8, 13, 15, 16])
+@pytest.mark.parametrize("cfg", [8, 13, 15, 16, 17])
 @pytest.mark.parametrize("grid", ["splitk3", "streamk37"])
 def test_shared_tiles_bf16_out_and_gelu(hiplib, monkeypatch, cfg, grid):
     """Split- and stream-K tiles with the bf16 output and GELU epilogue."""
