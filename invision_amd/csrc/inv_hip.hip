@@ -1651,8 +1651,12 @@ int conv_gather_cfg(int64_t in_ch, int64_t out_ch, int64_t H, int64_t W, int64_t
     const int cus = g.cu_count > 0 ? g.cu_count : 256;
     int cfg = 13;
     if (out_ch > 128) {
+        // the GEMM's own choice where it has a gather loader (16, 13), else the
+        // 4-wave 256x256 tile (the 8-wave one gathers slower: 450 against 314 us
+        // at 512 channels x 256^2); 13 keeps 512 channels x 128^2 at one full
+        // round of 256 tiles (95 us, against 120 for 128 tiles of 256x256)
         const TileChoice tc = choose_tiles(out_ch, P, in_ch * taps);
-        cfg = tc.cfg == 16 ? 16 : 9;
+        cfg = (tc.cfg == 16 || tc.cfg == 13) ? tc.cfg : 9;
     }
     const int ov = env_int("INV_HIP_CONV_GATHER_CFG", -1);
     if (ov == 9 || ov == 13 || ov == 16) cfg = ov;

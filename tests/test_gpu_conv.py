@@ -207,6 +207,7 @@ GATHER_SHAPES = [
     (1, 64, 128, 2, 3, 3, 3, 1, 1, None),    # an image smaller than the window: most taps outside
     (1, 128, 256, 21, 18, 3, 3, 2, 1, None), # stride 2 with padding
     (1, 64, 96, 11, 13, 1, 1, 2, 0, None),   # 1x1 at stride 2 (forced: 1x1 takes the patch path by default)
+    (2, 128, 320, 21, 18, 3, 3, 2, 1, 13),   # 256x128 tiles over ragged out_ch, stride 2, batch 2
 ]
 
 
