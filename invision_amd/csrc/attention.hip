@@ -25,13 +25,16 @@
 //                scores of ONE query (m = l%32) for 16 keys per 32-key block, so
 //                the row max and row sum are lane-local plus one exchange with
 //                lane l^32.
-//  O^T += V^T P^T: A = V^T tile rows (head_dim), B = P (bf16) straight from the
+//  O^T += V^T P^T: A = V^T (head_dim rows), B = P (bf16) straight from the
 //                score registers, k = keys.  For that, the B fragment's 8 k-slots
 //                of lane l must be the keys the lane holds; the K tile is stored
 //                with rows 4-7 and 8-11 of every 16-row group swapped (`quadswap`),
 //                which makes a lane's 8 consecutive score registers exactly keys
-//                16c + 8*(l/32) + 0..7 -- the contiguous 16 bytes its V^T fragment
-//                reads.  No cross-lane shuffle of P is needed.
+//                16c + 8*(l/32) + 0..7, the keys its V^T fragment covers.  No
+//                cross-lane shuffle of P is needed.  V stays in the reference's
+//                layout (key rows, as K) in HBM and LDS; its V^T fragments come
+//                from two ds_read_b64_tr_b16 (4 keys each), so no transposed copy
+//                of V is made.
 // Softmax runs in the exp2 domain: exp(scale*s - m) = exp2(s*scale*log2e - m'),
 // on the hardware exp2; P is rounded to bf16 (nearest-even) for the second MFMA,
 // and the row sum is taken over those same bf16 weights (v_dot2_f32_bf16).
@@ -71,6 +74,18 @@ __device__ __forceinline__ int quadswap(int r) { return (((r >> 2) ^ (r >> 3)) &
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// V tile rows (keys) hold D/8 chunks of 16 bytes; chunk c of key row r sits in
+// slot c ^ v_swz(r).  The P.V fragments are read with ds_read_b64_tr_b16 from
+// 4 key rows at a time (keys 4j..4j+3): the key bits the XOR uses spread each
+// read's 8 rows x 4 chunks over every bank in the minimum two passes.
+template <int D>
+__device__ __forceinline__ int v_swz(int r) {
+    if constexpr (D == 128)
+        return 4 * (r & 3);
+    else
+        return 4 * ((r >> 1) & 1);
+}
+
 // Hardware dispatches workgroup b to XCD b % 8: the logical index whose
 // consecutive values share an XCD, so the query blocks of one head meet its K
 // and V in one L2.
@@ -96,11 +111,11 @@ __global__ void __launch_bounds__(256, KS == 1 ? 2 : 1) attn_fwd_kernel(const At
     static_assert(D == 64 || D == 128, "head_dim 64 or 128");
     constexpr int KROW = D * 2;            // bytes per K-tile row
     constexpr int K_BYTES = BK * KROW;     // K tile
-    constexpr int V_BYTES = D * BK * 2;    // V^T tile: D rows of 128 bytes
+    constexpr int V_BYTES = BK * KROW;     // V tile: key rows, as K
     constexpr int STAGE = K_BYTES + V_BYTES;
     constexpr int KCH = D / 8;             // 16-byte chunks per K row
     constexpr int KIT = BK * KCH / NT;     // K copies per thread per tile
-    constexpr int VIT = D * 8 / NT;        // V^T copies per thread per tile
+    constexpr int VIT = BK * KCH / NT;     // V copies per thread per tile
     constexpr int NC = D / 16;             // 16-wide head_dim steps of S
     constexpr int ND = D / 32;             // 32-row head_dim blocks of O
     constexpr int NX = ND * 16 + 2;        // KS = 2: floats per lane handed from group 1 to group 0
@@ -135,19 +150,19 @@ __global__ void __launch_bounds__(256, KS == 1 ? 2 : 1) attn_fwd_kernel(const At
         }
     }
 
-    // K rows of kv head kvh: the buffer range ends with key seq_k - 1, so the
-    // rows of a partial last tile read as zeros.  V^T rows are padded to ldv.
+    // K and V rows of kv head kvh: the buffer ranges end with key seq_k - 1, so
+    // the rows of a partial last tile read as zeros.
     const __amdgpu_buffer_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(p.K + kvh * D), 0, (int)(((int64_t)(p.seq_k - 1) * p.ldk + D) * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.Vt + (int64_t)kvh * D * p.ldv), 0, (int)((int64_t)D * p.ldv * 2), 0x00020000);
+        (void *)(p.V + kvh * D), 0, (int)(((int64_t)(p.seq_k - 1) * p.ldv + D) * 2), 0x00020000);
 
     // Global -> LDS copies (buffer_load ... lds): copy i of group thread gtid fills
     // the 16-byte LDS slot i*NT + gtid of its tile, so each thread fetches the chunk
     // that belongs there -- the swizzle and the K row order live in these
     // global offsets.  K slot s: row n = s / KCH holds key quadswap(n), physical
-    // chunk s % KCH holds logical chunk (s % KCH) ^ swizzle(n).  V^T slot s: row
-    // d = s / 8, logical chunk (s % 8) ^ key8(d).
+    // chunk s % KCH holds logical chunk (s % KCH) ^ swizzle(n).  V slot s: row
+    // n = s / KCH holds key n, physical chunk s % KCH logical chunk (s % KCH) ^ v_swz(n).
     uint32_t k_goff[KIT], v_goff[VIT];
 #pragma unroll
     for (int i = 0; i < KIT; ++i) {
@@ -156,10 +171,10 @@ __global__ void __launch_bounds__(256, KS == 1 ? 2 : 1) attn_fwd_kernel(const At
     }
 #pragma unroll
     for (int i = 0; i < VIT; ++i) {
-        const int sl = i * NT + gtid, d = sl / 8;
-        v_goff[i] = (uint32_t)(d * p.ldv * 2 + ((sl % 8) ^ key8(d)) * 16);
+        const int sl = i * NT + gtid, n = sl / KCH;
+        v_goff[i] = (uint32_t)(n * p.ldv * 2 + ((sl % KCH) ^ v_swz<D>(n)) * 16);
     }
-    const uint32_t k_tile_step = (uint32_t)(BK * p.ldk * 2), v_tile_step = BK * 2;
+    const uint32_t k_tile_step = (uint32_t)(BK * p.ldk * 2), v_tile_step = (uint32_t)(BK * p.ldv * 2);
     auto load_tile = [&](int kt, lds_t *st) {
         lds_t *wk = st + wq * 64 * 16;
 #pragma unroll
@@ -200,14 +215,23 @@ __global__ void __launch_bounds__(256, KS == 1 ? 2 : 1) attn_fwd_kernel(const At
             const int n = 32 * b + lq;
             k_frag[b][c] = n * KROW + k_slot<D>(n, 2 * c + lh) * 16;
         }
-    int v_frag[ND][4];
+    // P.V's A operand (V^T: row d = lq of head_dim block i, keys 16*kc4 + 8*lh
+    // + 0..7) through two ds_read_b64_tr_b16.  In each 16-lane group (lanes
+    // 16*gq .. +15) output lane j receives element j % 4 of source lanes j/4,
+    // j/4 + 4, j/4 + 8, j/4 + 12; so source lane sq points at key row
+    // 8*(gq/2) + sq/4 (+4 for the second read), head_dim 32*i + 16*(gq%2) +
+    // 4*(sq%4) .. +3, and lane j gets 4 consecutive keys of head_dim 32*i +
+    // 16*(gq%2) + j.  The row's swizzle depends on key bits the per-lane part
+    // fixes, so v_addr[i] plus the key block's row offset is the whole address.
+    int v_addr[ND];
+    {
+        const int gq = lane >> 4, sq = lane & 15;
+        const int row = 8 * (gq >> 1) + (sq >> 2);
+        const int cc = 2 * (gq & 1) + ((sq & 3) >> 1);  // chunk within the 32-wide block
+        const int swz = v_swz<D>(row) >> 2;              // v_swz is 4 * swz for these rows
 #pragma unroll
-    for (int i = 0; i < ND; ++i)
-#pragma unroll
-        for (int kc4 = 0; kc4 < 4; ++kc4) {  // 16-key chunk kc4 = 2*b + c'
-            const int d = 32 * i + lq;
-            v_frag[i][kc4] = K_BYTES + d * 128 + (((2 * kc4 + lh) ^ key8(d)) * 16);
-        }
+        for (int i = 0; i < ND; ++i) v_addr[i] = K_BYTES + row * KROW + 8 * (sq & 1) + 16 * (4 * (i ^ swz) + cc);
+    }
 
     if (kg < nkt) load_tile(kg, lds);  // the group's first tile
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): it is in LDS
@@ -254,8 +278,15 @@ __global__ void __launch_bounds__(256, KS == 1 ? 2 : 1) attn_fwd_kernel(const At
 
         // The first V^T fragments: their LDS latency hides under the softmax.
         auto read_v = [&](int kc4, bf16x8_t (&f)[ND]) {
+            typedef short s16x4_t __attribute__((ext_vector_type(4)));
 #pragma unroll
-            for (int i = 0; i < ND; ++i) f[i] = *(const __attribute__((address_space(3))) bf16x8_t *)(cur + v_frag[i][kc4]);
+            for (int i = 0; i < ND; ++i) {
+                const lds_t *a = cur + v_addr[i] + 16 * kc4 * KROW;
+                const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t *)a);
+                const s16x4_t hi =
+                    __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4_t *)(a + 4 * KROW));
+                f[i] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            }
         };
         bf16x8_t vf[2][ND];
         read_v(0, vf[0]);

@@ -15,7 +15,7 @@ namespace inv {
 struct AttnParams {
     const uint16_t *Q;   // [seq_q x ldq], head h at columns h*D .. h*D+D-1
     const uint16_t *K;   // [seq_k x ldk], kv head g at columns g*D ..
-    const uint16_t *Vt;  // V transposed: [kv_heads*D x ldv], zero for keys >= seq_k up to ldv
+    const uint16_t *V;   // [seq_k x ldv], kv head g at columns g*D .. (as K)
     void *O;             // [seq_q x ldo], fp32 or bf16
     int64_t ldq, ldk, ldv, ldo;
     int seq_q, seq_k, heads, kv_heads;
@@ -31,6 +31,6 @@ struct AttnParams {
 hipError_t attention_launch(const AttnParams &p, int D, bool causal, int out, int key_groups, hipStream_t stream);
 
 constexpr int kAttnBlockQ = 128;  // queries per workgroup with one key group (4 waves x 32)
-constexpr int kAttnBlockK = 64;   // keys per tile; Vt rows are padded to a multiple of this
+constexpr int kAttnBlockK = 64;   // keys per tile
 
 }  // namespace inv

@@ -1541,18 +1541,18 @@ int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_
         ((seq_q + 63) / 64) * heads > INT32_MAX)
         return fail(INV_ERR_UNSUPPORTED, "attention: too many heads or tokens");
     const int64_t hq = heads * head_dim, hk = kv_heads * head_dim;
-    const int64_t ldv = round_up(seq_k, inv::kAttnBlockK);
-    if (seq_k * hk * 2 >= ((int64_t)1 << 31) || head_dim * ldv * 2 >= ((int64_t)1 << 31))
+    // K and V are staged with leading dimension round_up(hk, 8) (or used in place at hk)
+    if (seq_k * round_up(hk, 8) * 2 >= ((int64_t)1 << 31))
         return fail(INV_ERR_UNSUPPORTED, "attention: K or V above 2 GiB (32-bit buffer offsets)");
     const bool dev = (flags & INV_FLAG_DEVICE_PTRS) != 0;
     const size_t osz = out_dtype == INV_DT_F32 ? 4 : 2;
     if (dev && !aligned(O, 16)) return fail(INV_ERR_ARG, "attention: device O must be 16-byte aligned");
     if (dev && key_mask && !aligned(key_mask, 4)) return fail(INV_ERR_ARG, "attention: device key_mask not 4-byte aligned");
 
-    // bf16 operands: Q and K row-major as given (in place when already bf16 on
-    // the device), V transposed to [kv_heads*head_dim x ldv] with zero keys up to ldv.
-    const uint16_t *Qd = nullptr, *Kd = nullptr, *Vt = nullptr;
-    int64_t ldq = 0, ldk = 0, ldvt = 0;
+    // bf16 operands: Q, K and V row-major as given (in place when already bf16
+    // on the device); the kernel reads V^T fragments with transposing LDS reads.
+    const uint16_t *Qd = nullptr, *Kd = nullptr, *Vd = nullptr;
+    int64_t ldq = 0, ldk = 0, ldv = 0;
     if (prep) {
         if (in_dtype != INV_DT_F32) return fail(INV_ERR_ARG, "attention: the Q/K norm and rotary need fp32 Q and K");
         if (prep->rope != INV_ROPE_NONE && prep->rope != INV_ROPE_INTERLEAVED && prep->rope != INV_ROPE_HALF)
@@ -1567,8 +1567,7 @@ int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_
         TRY(stage_operand(Q, in_dtype, dev, false, seq_q, hq, hq, 1, 0, 8, g.aq, g.aqin, &Qd, &ldq));
         TRY(stage_operand(K, in_dtype, dev, false, seq_k, hk, hk, 1, 0, 8, g.ak, g.akin, &Kd, &ldk));
     }
-    TRY(stage_operand(V, in_dtype, dev, true, hk, seq_k, prep ? prep->ldv : hk, 1, 0, inv::kAttnBlockK, g.avt, g.avin,
-                      &Vt, &ldvt));
+    TRY(stage_operand(V, in_dtype, dev, false, seq_k, hk, prep ? prep->ldv : hk, 1, 0, 8, g.avt, g.avin, &Vd, &ldv));
     void *Od = O;
     if (!dev) {
         TRY(ensure(g.yout, (size_t)(seq_q * hq) * osz));
@@ -1577,11 +1576,11 @@ int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_
     inv::AttnParams p{};
     p.Q = Qd;
     p.K = Kd;
-    p.Vt = Vt;
+    p.V = Vd;
     p.O = Od;
     p.ldq = ldq;
     p.ldk = ldk;
-    p.ldv = ldvt;
+    p.ldv = ldv;
     p.ldo = hq;
     p.seq_q = (int)seq_q;
     p.seq_k = (int)seq_k;
