@@ -1165,15 +1165,16 @@ void release_pipe() {
 // 15360 2.81 (3.46), 1024x3072 -> 3072 0.62 (0.73).  Only the one-launch tile
 // grid is banded: its elements do not depend on M, so each band gives the bits
 // one launch over all rows gives.
-int64_t host_band_rows(const TileChoice &tc, int64_t M, size_t up_row, size_t out_row) {
-    if (tc.mode != inv::GRID_TILES) return 0;
+int64_t host_band_rows(int64_t tm, int64_t M, size_t up_row, size_t out_row) {
     const size_t cap = std::min(kPinChunk, (size_t)std::max(1, env_int("INV_HIP_HOST_BAND_MB", 32)) << 20);
-    const int64_t tm = kCfg[tc.cfg].tm;
     const int64_t bands = std::max(2, env_int("INV_HIP_HOST_BANDS", 8));
     const int64_t fit = (int64_t)(cap / std::max(up_row, out_row)) / tm * tm;
     const int64_t min_rows = round_up((int64_t)((16u << 20) / (up_row + out_row)) + 1, tm);
     const int64_t mb = std::min(fit, std::max(min_rows, M / bands / tm * tm));
     return (mb > 0 && M > mb) ? mb : 0;
+}
+int64_t host_band_rows(const TileChoice &tc, int64_t M, size_t up_row, size_t out_row) {
+    return tc.mode == inv::GRID_TILES ? host_band_rows(kCfg[tc.cfg].tm, M, up_row, out_row) : 0;
 }
 
 // The row-band pipeline's optional stages: X normalised (fp32 X; the
@@ -1186,84 +1187,57 @@ struct BandExtras {
     const float *gate = nullptr;  // device, or null
 };
 
-// Y = X W^T (+ bias, activation) with X and Y in host memory, in row bands of
-// mb rows: band b+2's upload (host rows -> pinned -> device, `up` stream), band
-// b's conversion (or normalisation) and GEMM (library stream) and band b's
-// download (device -> pinned, `down` stream, then pinned -> host rows) overlap,
-// so the two PCIe directions run at once and the GEMM hides under them.  When
-// Y is accumulated, a band's Y rows travel up behind its X rows in the same
-// bounce buffer.  Every band runs the tile choice tc of the whole product.
-// Returns when Y is written.
-int linear_host_banded(const void *X, int x_dtype, inv_weight_t W, const float *bd, void *Y, int y_dtype, int64_t M,
-                       int64_t K, int64_t N, int epilogue, const TileChoice &tc, int64_t mb, const BandExtras &ex) {
+// The row-band pipeline's schedule, shared by the host-pointer entry points:
+// rows [0, M) in bands of mb.  stage(r0, nr, pin) copies band rows from the
+// host into the pinned buffer pin (band b uses pin[b & 1]) and queues their
+// uploads on the `up` stream; compute(r0, nr) queues the band's kernels on the
+// library stream, after those uploads; then the band's output, nr rows of
+// out_row bytes at dev_out + r0 * out_row, goes down through pin_out[b & 1] to
+// Y + r0 * out_row.  Band b+2 is staged and computed while band b drains, so
+// upload, kernels and download of neighbouring bands overlap.  Returns when Y
+// is written.
+int run_band_pipeline(int64_t M, int64_t mb, char *Y, size_t out_row, const char *dev_out,
+                      const std::function<int(int64_t, int64_t, char *)> &stage,
+                      const std::function<int(int64_t, int64_t)> &compute) {
     auto &P = g.pipe;
-    const size_t xsz = (x_dtype == INV_DT_F32) ? 4 : 2, ysz = (y_dtype == INV_DT_F32) ? 4 : 2;
-    const int out = (y_dtype == INV_DT_F32) ? inv::OUT_F32 : inv::OUT_BF16;
-    const int64_t ldw = W->ldw;
-    const size_t in_row = (size_t)K * xsz, out_row = (size_t)N * ysz;
-    // bf16 rows already 16-byte granular land in the GEMM operand as they are
-    const bool direct = !ex.nm && x_dtype == INV_DT_BF16 && K == ldw;
-    TRY(ensure(g.x16, (size_t)(M * ldw) * 2));
-    if (!direct) TRY(ensure(g.xin, (size_t)M * in_row));
-    TRY(ensure(g.yout, (size_t)M * out_row));
     // The copy streams start after the library stream's earlier work (which
-    // may still read these buffers), and the bounce buffers after their uploads.
+    // may still read the device buffers), and the bounce buffers after their uploads.
     HIPCHK(hipEventRecord(P.start, g.stream));
     HIPCHK(hipStreamWaitEvent(P.up, P.start, 0));
     HIPCHK(hipStreamWaitEvent(P.down, P.start, 0));
     for (int k = 0; k < 2; ++k) HIPCHK(hipEventSynchronize(g.pin_ev[k]));
     const int64_t nb = (M + mb - 1) / mb;
     auto rows_of = [&](int64_t b) { return std::min(mb, M - b * mb); };
-    auto upload_and_multiply = [&](int64_t b) -> int {
+    auto upload_and_compute = [&](int64_t b) -> int {
         const int k = (int)(b & 1);
-        const int64_t r0 = b * mb, nr = rows_of(b);
         HIPCHK(hipEventSynchronize(P.in_ev[k]));  // band b-2's upload has left pin[k]
-        char *pin = (char *)g.pin[k];
-        char *yb = (char *)g.yout.p + (size_t)r0 * out_row;
-        par_copy_rows(pin, in_row, (const char *)X + r0 * in_row, in_row, nr, in_row);
-        if (ex.accumulate) par_copy_rows(pin + nr * in_row, out_row, (const char *)Y + r0 * out_row, out_row, nr, out_row);
-        char *dst = direct ? (char *)g.x16.p + (size_t)r0 * ldw * 2 : (char *)g.xin.p + (size_t)r0 * in_row;
-        HIPCHK(hipMemcpyAsync(dst, pin, (size_t)nr * in_row, hipMemcpyHostToDevice, P.up));
-        if (ex.accumulate)
-            HIPCHK(hipMemcpyAsync(yb, pin + nr * in_row, (size_t)nr * out_row, hipMemcpyHostToDevice, P.up));
+        TRY(stage(b * mb, rows_of(b), (char *)g.pin[k]));
         HIPCHK(hipEventRecord(P.in_ev[k], P.up));
         HIPCHK(hipStreamWaitEvent(g.stream, P.in_ev[k], 0));
-        uint16_t *xb = (uint16_t *)g.x16.p + r0 * ldw;
-        if (ex.nm) {
-            TRY(launch_norm_rows((const float *)g.xin.p + r0 * K, *ex.nm, ex.nscale, ex.nshift, nr, K, xb, ldw));
-        } else if (!direct) {
-            if (x_dtype == INV_DT_F32)
-                TRY(launch_cvt_rows_f32((const float *)g.xin.p + r0 * K, K, xb, ldw, nr, K, ldw));
-            else
-                TRY(launch_copy_rows_bf16((const uint16_t *)g.xin.p + r0 * K, K, xb, ldw, nr, K, ldw));
-        }
-        // accumulating reads the band's Y as C (beta = 1) in place, as the one-pass call does
-        TRY(run_gemm(W->w, ldw, xb, ldw, yb, N, out, bd, ex.accumulate ? (const float *)yb : nullptr, N, 1.0f,
-                     ex.accumulate ? 1.0f : 0.0f, nr, W->rows, ldw, epilogue, 0, -1, N, ex.gate, nullptr, nullptr,
-                     &tc));
+        TRY(compute(b * mb, rows_of(b)));
         HIPCHK(hipEventRecord(P.gemm_ev[k], g.stream));
         return INV_OK;
     };
     auto download = [&](int64_t b) -> int {  // pin_out[b & 1] is free (band b-2 drained)
         const int k = (int)(b & 1);
         HIPCHK(hipStreamWaitEvent(P.down, P.gemm_ev[k], 0));
-        HIPCHK(hipMemcpyAsync(P.pin_out[k], (const char *)g.yout.p + (size_t)(b * mb) * out_row,
-                              (size_t)rows_of(b) * out_row, hipMemcpyDeviceToHost, P.down));
+        HIPCHK(hipMemcpyAsync(P.pin_out[k], dev_out + (size_t)(b * mb) * out_row, (size_t)rows_of(b) * out_row,
+                              hipMemcpyDeviceToHost, P.down));
         HIPCHK(hipEventRecord(P.out_ev[k], P.down));
         return INV_OK;
     };
     auto drain = [&](int64_t b) -> int {
         const int k = (int)(b & 1);
         HIPCHK(hipEventSynchronize(P.out_ev[k]));
-        par_copy_rows((char *)Y + (size_t)(b * mb) * out_row, out_row, (const char *)P.pin_out[k], out_row,
-                      rows_of(b), out_row);
+        par_copy_rows(Y + (size_t)(b * mb) * out_row, out_row, (const char *)P.pin_out[k], out_row, rows_of(b),
+                      out_row);
         return INV_OK;
     };
     auto run = [&]() -> int {
-        for (int64_t b = 0; b < std::min<int64_t>(2, nb); ++b) TRY(upload_and_multiply(b));
+        for (int64_t b = 0; b < std::min<int64_t>(2, nb); ++b) TRY(upload_and_compute(b));
         for (int64_t b = 0; b < std::min<int64_t>(2, nb); ++b) TRY(download(b));
         for (int64_t b = 0; b < nb; ++b) {
-            if (b + 2 < nb) TRY(upload_and_multiply(b + 2));
+            if (b + 2 < nb) TRY(upload_and_compute(b + 2));
             TRY(drain(b));
             if (b + 2 < nb) TRY(download(b + 2));
         }
@@ -1276,8 +1250,53 @@ int linear_host_banded(const void *X, int x_dtype, inv_weight_t W, const float *
         (void)hipStreamSynchronize(P.up);
         (void)hipStreamSynchronize(g.stream);
         (void)hipStreamSynchronize(P.down);
-        return rc;
     }
+    return rc;
+}
+
+// Y = X W^T (+ bias, activation) with X and Y in host memory, in row bands of
+// mb rows through run_band_pipeline: a band's conversion (or normalisation)
+// and GEMM run while its neighbours upload and download.  When Y is
+// accumulated, a band's Y rows travel up behind its X rows in the same bounce
+// buffer.  Every band runs the tile choice tc of the whole product.
+int linear_host_banded(const void *X, int x_dtype, inv_weight_t W, const float *bd, void *Y, int y_dtype, int64_t M,
+                       int64_t K, int64_t N, int epilogue, const TileChoice &tc, int64_t mb, const BandExtras &ex) {
+    const size_t xsz = (x_dtype == INV_DT_F32) ? 4 : 2, ysz = (y_dtype == INV_DT_F32) ? 4 : 2;
+    const int out = (y_dtype == INV_DT_F32) ? inv::OUT_F32 : inv::OUT_BF16;
+    const int64_t ldw = W->ldw;
+    const size_t in_row = (size_t)K * xsz, out_row = (size_t)N * ysz;
+    // bf16 rows already 16-byte granular land in the GEMM operand as they are
+    const bool direct = !ex.nm && x_dtype == INV_DT_BF16 && K == ldw;
+    TRY(ensure(g.x16, (size_t)(M * ldw) * 2));
+    if (!direct) TRY(ensure(g.xin, (size_t)M * in_row));
+    TRY(ensure(g.yout, (size_t)M * out_row));
+    auto stage = [&](int64_t r0, int64_t nr, char *pin) -> int {
+        char *yb = (char *)g.yout.p + (size_t)r0 * out_row;
+        par_copy_rows(pin, in_row, (const char *)X + r0 * in_row, in_row, nr, in_row);
+        if (ex.accumulate) par_copy_rows(pin + nr * in_row, out_row, (const char *)Y + r0 * out_row, out_row, nr, out_row);
+        char *dst = direct ? (char *)g.x16.p + (size_t)r0 * ldw * 2 : (char *)g.xin.p + (size_t)r0 * in_row;
+        HIPCHK(hipMemcpyAsync(dst, pin, (size_t)nr * in_row, hipMemcpyHostToDevice, g.pipe.up));
+        if (ex.accumulate)
+            HIPCHK(hipMemcpyAsync(yb, pin + nr * in_row, (size_t)nr * out_row, hipMemcpyHostToDevice, g.pipe.up));
+        return INV_OK;
+    };
+    auto compute = [&](int64_t r0, int64_t nr) -> int {
+        char *yb = (char *)g.yout.p + (size_t)r0 * out_row;
+        uint16_t *xb = (uint16_t *)g.x16.p + r0 * ldw;
+        if (ex.nm) {
+            TRY(launch_norm_rows((const float *)g.xin.p + r0 * K, *ex.nm, ex.nscale, ex.nshift, nr, K, xb, ldw));
+        } else if (!direct) {
+            if (x_dtype == INV_DT_F32)
+                TRY(launch_cvt_rows_f32((const float *)g.xin.p + r0 * K, K, xb, ldw, nr, K, ldw));
+            else
+                TRY(launch_copy_rows_bf16((const uint16_t *)g.xin.p + r0 * K, K, xb, ldw, nr, K, ldw));
+        }
+        // accumulating reads the band's Y as C (beta = 1) in place, as the one-pass call does
+        return run_gemm(W->w, ldw, xb, ldw, yb, N, out, bd, ex.accumulate ? (const float *)yb : nullptr, N, 1.0f,
+                        ex.accumulate ? 1.0f : 0.0f, nr, W->rows, ldw, epilogue, 0, -1, N, ex.gate, nullptr, nullptr,
+                        &tc);
+    };
+    TRY(run_band_pipeline(M, mb, (char *)Y, out_row, (const char *)g.yout.p, stage, compute));
     g.calls++;
     return INV_OK;
 }
@@ -1549,6 +1568,25 @@ int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_
     if (dev && !aligned(O, 16)) return fail(INV_ERR_ARG, "attention: device O must be 16-byte aligned");
     if (dev && key_mask && !aligned(key_mask, 4)) return fail(INV_ERR_ARG, "attention: device key_mask not 4-byte aligned");
 
+    const bool causal = (flags & INV_ATTN_CAUSAL) != 0;
+    // Two key groups (64-query workgroups) where the 128-query grid leaves CUs
+    // idle: Qwen3's 512-token prefill is 128 blocks on 256 CUs.
+    // INV_HIP_ATTN_KEY_GROUPS=1 or 2 forces the choice.
+    const int64_t blocks128 = ((seq_q + inv::kAttnBlockQ - 1) / inv::kAttnBlockQ) * heads;
+    int key_groups = blocks128 < (g.cu_count > 0 ? g.cu_count : 256) ? 2 : 1;
+    const int kg_ov = env_int("INV_HIP_ATTN_KEY_GROUPS", 0);
+    if (kg_ov == 1 || kg_ov == 2) key_groups = kg_ov;
+    // Host Q and O: query-row bands through the band pipeline (K and V first,
+    // whole); bands are whole query blocks of the whole problem's workgroup
+    // shape, so each query's result is the one-launch result.
+    const size_t xsz = in_dtype == INV_DT_F32 ? 4 : 2;
+    const int64_t band_q =
+        (!dev && !prep && !g.stats && env_int("INV_HIP_HOST_PIPELINE", 1))
+            ? host_band_rows(inv::kAttnBlockQ / key_groups, seq_q, (size_t)hq * xsz, (size_t)hq * osz) : 0;
+    const bool banded = band_q > 0 && pipe_ready();
+    if (!dev && !banded && env_int("INV_HIP_HOST_PIPELINE", 1) == 2)
+        return fail(INV_ERR_UNSUPPORTED, "attention: INV_HIP_HOST_PIPELINE=2 but this call is not banded");
+
     // bf16 operands: Q, K and V row-major as given (in place when already bf16
     // on the device); the kernel reads V^T fragments with transposing LDS reads.
     const uint16_t *Qd = nullptr, *Kd = nullptr, *Vd = nullptr;
@@ -1564,7 +1602,7 @@ int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_
         TRY(stage_prepped((const float *)K, prep->ldk, dev, seq_k, kv_heads, head_dim, prep->k_w, prep->rope,
                           prep->k_cos, prep->k_sin, g.ak, g.akin, g.hx, &Kd, &ldk));
     } else {
-        TRY(stage_operand(Q, in_dtype, dev, false, seq_q, hq, hq, 1, 0, 8, g.aq, g.aqin, &Qd, &ldq));
+        if (!banded) TRY(stage_operand(Q, in_dtype, dev, false, seq_q, hq, hq, 1, 0, 8, g.aq, g.aqin, &Qd, &ldq));
         TRY(stage_operand(K, in_dtype, dev, false, seq_k, hk, hk, 1, 0, 8, g.ak, g.akin, &Kd, &ldk));
     }
     TRY(stage_operand(V, in_dtype, dev, false, seq_k, hk, prep ? prep->ldv : hk, 1, 0, 8, g.avt, g.avin, &Vd, &ldv));
@@ -1594,14 +1632,37 @@ int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_
         TRY(h2d_rows(g.amask.p, key_mask, 1, (size_t)seq_k * 4, (size_t)seq_k * 4));
         p.key_mask = (const int32_t *)g.amask.p;
     }
-    const bool causal = (flags & INV_ATTN_CAUSAL) != 0;
-    // Two key groups (64-query workgroups) where the 128-query grid leaves CUs
-    // idle: Qwen3's 512-token prefill is 128 blocks on 256 CUs.
-    // INV_HIP_ATTN_KEY_GROUPS=1 or 2 forces the choice.
-    const int64_t blocks128 = ((seq_q + inv::kAttnBlockQ - 1) / inv::kAttnBlockQ) * heads;
-    int key_groups = blocks128 < (g.cu_count > 0 ? g.cu_count : 256) ? 2 : 1;
-    const int kg_ov = env_int("INV_HIP_ATTN_KEY_GROUPS", 0);
-    if (kg_ov == 1 || kg_ov == 2) key_groups = kg_ov;
+    if (banded) {
+        // a band's host Q rows go up raw (fp32 to the staging rows, bf16 straight
+        // into the operand), are rounded on the device, and its queries run as a
+        // smaller problem whose causal offset counts from the band's first row
+        const size_t in_row = (size_t)hq * xsz, out_row = (size_t)hq * osz;
+        TRY(ensure(g.aq, (size_t)(seq_q * hq) * 2));
+        if (in_dtype == INV_DT_F32) TRY(ensure(g.aqin, (size_t)seq_q * in_row));
+        char *qraw = in_dtype == INV_DT_F32 ? (char *)g.aqin.p : (char *)g.aq.p;
+        auto stage = [&](int64_t r0, int64_t nr, char *pin) -> int {
+            par_copy_rows(pin, in_row, (const char *)Q + r0 * in_row, in_row, nr, in_row);
+            HIPCHK(hipMemcpyAsync(qraw + (size_t)r0 * in_row, pin, (size_t)nr * in_row, hipMemcpyHostToDevice,
+                                  g.pipe.up));
+            return INV_OK;
+        };
+        auto compute = [&](int64_t r0, int64_t nr) -> int {
+            uint16_t *qb = (uint16_t *)g.aq.p + r0 * hq;
+            if (in_dtype == INV_DT_F32) TRY(launch_cvt_rows_f32((const float *)g.aqin.p + r0 * hq, hq, qb, hq, nr, hq, hq));
+            inv::AttnParams pb = p;
+            pb.Q = qb;
+            pb.ldq = hq;
+            pb.seq_q = (int)nr;
+            pb.O = (char *)g.yout.p + (size_t)r0 * out_row;
+            pb.causal_offset = p.causal_offset + (int)r0;
+            HIPCHK(inv::attention_launch(pb, (int)head_dim, causal, out_dtype == INV_DT_BF16 ? 1 : 0, key_groups,
+                                         g.stream));
+            return INV_OK;
+        };
+        TRY(run_band_pipeline(seq_q, band_q, (char *)O, out_row, (const char *)g.yout.p, stage, compute));
+        g.calls++;
+        return INV_OK;
+    }
     if (g.stats) HIPCHK(hipEventRecord(g.st0, g.stream));
     HIPCHK(inv::attention_launch(p, (int)head_dim, causal, out_dtype == INV_DT_BF16 ? 1 : 0, key_groups, g.stream));
     if (g.stats) {

@@ -9,7 +9,8 @@ and not) and Y, with a ragged last band.  INV_HIP_HOST_BAND_MB=1 makes bands of
 small products; the full-size product (4608 x 3072 x 9216) runs with the
 default bands and is also checked against the oracle on sampled rows.  The
 normalised (inv_hip_linear_norm) and accumulating (inv_hip_linear_gated_add)
-entry points band the same way.
+entry points band the same way, and so does host-pointer attention over query
+rows (bands of whole workgroup blocks: bit-exact against one launch).
 """
 import numpy as np
 import pytest
@@ -182,3 +183,74 @@ def test_banded_gated_add_equals_serial_and_device(hiplib, monkeypatch, xdt):
     np.testing.assert_array_equal(y_band, y_dev)
     ref = Y0.astype(np.float64) + gate * oracle.linear_bf16w(round_bf16(X), W, b, oracle.EPI_NONE)
     assert oracle.normwise_err(y_band - Y0, ref - Y0) <= TOL_TIGHT
+
+
+def attn_gen(seed, sq, sk, heads, kv_heads, d):
+    oracle.rng_seed(seed)
+    Q = oracle.randn_scaled((sq, heads * d), 1.0, False)
+    K = oracle.randn_scaled((sk, kv_heads * d), 1.0, False)
+    V = oracle.randn_scaled((sk, kv_heads * d), 1.0, False)
+    return Q, K, V
+
+
+# (seq_q, seq_k, heads, kv_heads, head_dim, causal, key mask, Q/K/V dtype, O dtype, key groups):
+# 1 MiB bands of 256 or 512 query rows, ragged last bands; causal with more keys
+# than queries (the diagonal offset counts from each band's first row)
+ATTN_CASES = [
+    (1100, 1100, 8, 8, 128, False, False, "f32", "f32", 2),
+    (1000, 1300, 8, 2, 128, True, False, "f32", "bf16", 2),
+    (777, 777, 16, 16, 64, True, True, "bf16", "f32", 2),
+    (1536, 600, 8, 4, 128, False, True, "bf16", "bf16", 1),
+    (1300, 1400, 8, 4, 128, True, True, "f32", "f32", 1),
+]
+
+
+@pytest.mark.parametrize("sq,sk,heads,kvh,d,causal,masked,idt,odt,kg", ATTN_CASES)
+def test_banded_attention_equals_serial_and_device(hiplib, monkeypatch, sq, sk, heads, kvh, d, causal, masked, idt,
+                                                   odt, kg):
+    """inv_hip_attention(_masked) with host Q and O: K and V go up whole, then
+    query bands of whole workgroup blocks upload, run and download overlapped."""
+    Q, K, V = attn_gen(sq + sk + d, sq, sk, heads, kvh, d)
+    mask = None
+    if masked:
+        mask = (np.random.default_rng(sq).random(sk) < 0.7).astype(np.int32)
+        mask[0] = 1
+    cvt = (lambda a: a.astype(np.float32)) if idt == "f32" else as_bf16_bits
+    Qh, Kh, Vh = cvt(Q), cvt(K), cvt(V)
+    monkeypatch.setenv("INV_HIP_ATTN_KEY_GROUPS", str(kg))
+    monkeypatch.setenv("INV_HIP_HOST_BAND_MB", "1")
+    monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "2")  # fails unless the call is banded
+    kw = dict(heads=heads, head_dim=d, kv_heads=kvh, causal=causal, out_dtype=odt, key_mask=mask)
+    o_band = q.attention(Qh, Kh, Vh, **kw)
+    monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "0")
+    o_serial = q.attention(Qh, Kh, Vh, **kw)
+    devs = [q.DeviceArray.from_host(a, idt) for a in (Qh, Kh, Vh)]
+    od = q.DeviceArray((sq, heads * d), odt)
+    md = q.DeviceArray.from_host(mask, "i32") if masked else None
+    try:
+        q.attention_device(*devs, od, heads=heads, head_dim=d, kv_heads=kvh, causal=causal, key_mask=md)
+        o_dev = od.to_host()
+    finally:
+        for a in devs + [od] + ([md] if md is not None else []):
+            a.free()
+    print(f"  {sq}x{sk} {heads}/{kvh} heads of {d} causal={causal} mask={masked} {idt}->{odt} key groups {kg}: "
+          "banded == serial == device", flush=True)
+    np.testing.assert_array_equal(o_band, o_serial)
+    np.testing.assert_array_equal(o_band, o_dev)
+    of = bf16_bits_to_f32(o_band) if odt == "bf16" else o_band
+    ref = oracle.attention_f64(round_bf16(Q), round_bf16(K), round_bf16(V), heads, kvh, d, 1.0 / np.sqrt(d), causal,
+                               key_mask=mask)
+    assert oracle.normwise_err(of, ref) <= 4e-3 + (2.0 ** -8 if odt == "bf16" else 0.0)
+
+
+def test_attention_not_banded_below_two_bands(hiplib, monkeypatch):
+    """A query count that fits one band runs the one-pass path (PIPELINE=2 then
+    reports the call as not banded)."""
+    Q, K, V = attn_gen(5, 200, 200, 8, 8, 128)
+    monkeypatch.setenv("INV_HIP_HOST_BAND_MB", "1")
+    monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "2")
+    with pytest.raises(hip.HipError):
+        q.attention(Q, K, V, heads=8, head_dim=128)
+    monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "1")
+    O = q.attention(Q, K, V, heads=8, head_dim=128)
+    assert np.all(np.isfinite(O))
