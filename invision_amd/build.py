@@ -24,6 +24,8 @@ SONAME = LIB_NAME + ".0"
 PROBE_NAME = "libinv_probe.so"  # the MFMA-ceiling measurement aid (not the linear-layer ABI)
 PROBE_PATH = os.path.join(PKG_DIR, PROBE_NAME)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+# host-only sources: ROCm's clang as a plain C++ compiler (hipcc would compile them as HIP)
+HOST_CXX = os.environ.get("INV_HOST_CXX", "/opt/rocm/llvm/bin/clang++")
 ARCH = "gfx950"
 
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
@@ -49,9 +51,9 @@ def compile_jobs() -> list[tuple[list[str], str]]:
     jobs.append(([HIPCC] + COMMON_FLAGS + inc + ["-c", os.path.join(CSRC, "inv_hip.hip"), "-o", obj], obj))
     obj = os.path.join(BUILD_DIR, "attention.o")
     jobs.append(([HIPCC] + COMMON_FLAGS + inc + ["-c", os.path.join(CSRC, "attention.hip"), "-o", obj], obj))
-    for host_src in ("safetensors.cpp", "sample.cpp"):  # host code only
+    for host_src in ("safetensors.cpp", "sample.cpp", "host_convert.cpp"):  # host code only
         obj = os.path.join(BUILD_DIR, host_src.replace(".cpp", ".o"))
-        jobs.append(([HIPCC, "-O2", "-std=c++17", "-fPIC", "-Wall"] + inc + ["-c", os.path.join(CSRC, host_src),
+        jobs.append(([HOST_CXX, "-O2", "-std=c++17", "-fPIC", "-Wall"] + inc + ["-c", os.path.join(CSRC, host_src),
                                                                              "-o", obj], obj))
     for cfg in range(NUM_GEMM_CONFIGS):
         obj = os.path.join(BUILD_DIR, f"gemm_cfg{cfg}.o")

@@ -31,6 +31,7 @@
 
 #include "attention.hpp"
 #include "convert_kernels.hpp"
+#include "host_convert.hpp"
 #include "gemm_configs.hpp"
 #include "gemm_kernel.hpp"
 
@@ -160,6 +161,31 @@ void par_copy_rows(char *dst, size_t dpitch, const char *src, size_t spitch, int
         g_copy.parallel_for(parts, [&](int i) {
             for (int64_t r = (int64_t)i * per; r < std::min<int64_t>(rows, (int64_t)(i + 1) * per); ++r)
                 memcpy(dst + r * dpitch, src + r * spitch, width);
+        });
+    }
+}
+
+// Host fp32 rows rounded to bf16 rows (nearest even, the device's rounding)
+// on the pool: dst [rows x ldd], columns cols..cols_pad-1 zero.  Rounding while
+// copying into the bounce buffers halves the bytes that cross PCIe.
+void par_cvt_rows(uint16_t *dst, int64_t ldd, const float *src, int64_t lds, int64_t rows, int64_t cols,
+                  int64_t cols_pad) {
+    const size_t total = (size_t)rows * (size_t)cols * 4;
+    const int parts = (int)std::min<size_t>((size_t)g_copy.threads() * 2, std::max<size_t>(1, total >> 20));
+    if (rows >= parts) {
+        const int64_t per = (rows + parts - 1) / parts;
+        g_copy.parallel_for(parts, [&](int i) {
+            const int64_t r0 = (int64_t)i * per, nr = std::min<int64_t>(per, rows - r0);
+            if (nr > 0) inv::host_f32_to_bf16_rows(dst + r0 * ldd, ldd, src + r0 * lds, lds, nr, cols, cols_pad);
+        });
+    } else {  // few wide rows: column slices of every row (multiples of 16 columns)
+        const int64_t per = ((cols_pad + parts - 1) / parts + 15) / 16 * 16;
+        g_copy.parallel_for(parts, [&](int i) {
+            const int64_t c0 = (int64_t)i * per;
+            if (c0 >= cols_pad) return;
+            const int64_t cp = std::min<int64_t>(per, cols_pad - c0);
+            const int64_t cc = std::max<int64_t>(0, std::min<int64_t>(cp, cols - c0));
+            inv::host_f32_to_bf16_rows(dst + c0, ldd, src + std::min(c0, cols), lds, rows, cc, cp);
         });
     }
 }
@@ -354,6 +380,25 @@ int h2d_rows(void *dev, const void *host, int64_t rows, size_t width, size_t pit
         char *pb = (char *)g.pin[k];
         par_copy_rows(pb, width, src + r0 * pitch, pitch, nr, width);
         HIPCHK(hipMemcpyAsync(dst + r0 * width, pb, (size_t)nr * width, hipMemcpyHostToDevice, g.stream));
+        HIPCHK(hipEventRecord(g.pin_ev[k], g.stream));
+        k ^= 1;
+    }
+    return INV_OK;
+}
+
+// Host fp32 rows (ld floats apart) -> contiguous device bf16 rows of cols_pad
+// (zero padded), rounded by the host while they are copied into the bounce
+// buffers.  Rows of up to one bounce buffer (cols_pad * 2 <= kPinChunk).
+int h2d_rows_bf16(uint16_t *dev, const float *host, int64_t rows, int64_t cols, int64_t ld, int64_t cols_pad) {
+    const size_t width = (size_t)cols_pad * 2;
+    if (width > kPinChunk) return fail(INV_ERR_ARG, "internal: bf16 row of %zu bytes above a bounce buffer", width);
+    const int64_t rows_per = (int64_t)(kPinChunk / width);
+    int k = 0;
+    for (int64_t r0 = 0; r0 < rows; r0 += rows_per) {
+        const int64_t nr = std::min(rows_per, rows - r0);
+        HIPCHK(hipEventSynchronize(g.pin_ev[k]));
+        par_cvt_rows((uint16_t *)g.pin[k], cols_pad, host + r0 * ld, ld, nr, cols, cols_pad);
+        HIPCHK(hipMemcpyAsync(dev + r0 * cols_pad, g.pin[k], (size_t)nr * width, hipMemcpyHostToDevice, g.stream));
         HIPCHK(hipEventRecord(g.pin_ev[k], g.stream));
         k ^= 1;
     }
@@ -719,7 +764,9 @@ int weight_upload_impl(const void *w, bool is_f32, int64_t N, int64_t K, const f
     uint16_t *dw = nullptr;
     TRY(dev_alloc((void **)&dw, (size_t)(N * ldw) * 2, "weight"));
     int rc = INV_OK;
-    if (is_f32) {
+    if (is_f32 && (size_t)ldw * 2 <= kPinChunk) {  // rounded by the host on its way up
+        rc = h2d_rows_bf16(dw, (const float *)w, N, K, K, ldw);
+    } else if (is_f32) {
         rc = ensure(g.win, (size_t)(N * K) * 4);
         if (!rc) rc = h2d_rows(g.win.p, w, N, (size_t)K * 4, (size_t)K * 4);
         if (!rc) rc = launch_cvt_rows_f32((const float *)g.win.p, K, dw, ldw, N, K, ldw);
@@ -824,6 +871,14 @@ int stage_operand(const void *src, int dtype, bool on_device, bool trans, int64_
     const void *dsrc = src;
     int64_t dld = ld;
     if (!on_device) {
+        // fp32 rounded plainly: by the host, on its way into the bounce buffers
+        if (!trans && dtype == INV_DT_F32 && nseg == 1 && lo_mask == 0 && (size_t)cols_pad * 2 <= kPinChunk) {
+            TRY(ensure(dst, (size_t)(rows * cols_pad) * 2));
+            TRY(h2d_rows_bf16((uint16_t *)dst.p, (const float *)src, rows, cols, ld, cols_pad));
+            *out = (const uint16_t *)dst.p;
+            *out_ld = cols_pad;
+            return INV_OK;
+        }
         // Upload the exact extent into a contiguous device buffer.
         if (!trans && dtype == INV_DT_BF16 && cols == cols_pad) {
             TRY(ensure(dst, (size_t)(rows * cols_pad) * 2));
@@ -1264,20 +1319,26 @@ int linear_host_banded(const void *X, int x_dtype, inv_weight_t W, const float *
     const size_t xsz = (x_dtype == INV_DT_F32) ? 4 : 2, ysz = (y_dtype == INV_DT_F32) ? 4 : 2;
     const int out = (y_dtype == INV_DT_F32) ? inv::OUT_F32 : inv::OUT_BF16;
     const int64_t ldw = W->ldw;
-    const size_t in_row = (size_t)K * xsz, out_row = (size_t)N * ysz;
-    // bf16 rows already 16-byte granular land in the GEMM operand as they are
-    const bool direct = !ex.nm && x_dtype == INV_DT_BF16 && K == ldw;
+    const size_t out_row = (size_t)N * ysz;
+    // fp32 rows (not normalised) are rounded by the host into bf16 operand
+    // rows; bf16 rows already 16-byte granular land in the operand as they are
+    const bool host_round = !ex.nm && x_dtype == INV_DT_F32;
+    const bool direct = host_round || (!ex.nm && x_dtype == INV_DT_BF16 && K == ldw);
+    const size_t in_row = (size_t)K * xsz, up_row = host_round ? (size_t)ldw * 2 : in_row;
     TRY(ensure(g.x16, (size_t)(M * ldw) * 2));
     if (!direct) TRY(ensure(g.xin, (size_t)M * in_row));
     TRY(ensure(g.yout, (size_t)M * out_row));
     auto stage = [&](int64_t r0, int64_t nr, char *pin) -> int {
         char *yb = (char *)g.yout.p + (size_t)r0 * out_row;
-        par_copy_rows(pin, in_row, (const char *)X + r0 * in_row, in_row, nr, in_row);
-        if (ex.accumulate) par_copy_rows(pin + nr * in_row, out_row, (const char *)Y + r0 * out_row, out_row, nr, out_row);
+        if (host_round)
+            par_cvt_rows((uint16_t *)pin, ldw, (const float *)X + r0 * K, K, nr, K, ldw);
+        else
+            par_copy_rows(pin, in_row, (const char *)X + r0 * in_row, in_row, nr, in_row);
+        if (ex.accumulate) par_copy_rows(pin + nr * up_row, out_row, (const char *)Y + r0 * out_row, out_row, nr, out_row);
         char *dst = direct ? (char *)g.x16.p + (size_t)r0 * ldw * 2 : (char *)g.xin.p + (size_t)r0 * in_row;
-        HIPCHK(hipMemcpyAsync(dst, pin, (size_t)nr * in_row, hipMemcpyHostToDevice, g.pipe.up));
+        HIPCHK(hipMemcpyAsync(dst, pin, (size_t)nr * up_row, hipMemcpyHostToDevice, g.pipe.up));
         if (ex.accumulate)
-            HIPCHK(hipMemcpyAsync(yb, pin + nr * in_row, (size_t)nr * out_row, hipMemcpyHostToDevice, g.pipe.up));
+            HIPCHK(hipMemcpyAsync(yb, pin + nr * up_row, (size_t)nr * out_row, hipMemcpyHostToDevice, g.pipe.up));
         return INV_OK;
     };
     auto compute = [&](int64_t r0, int64_t nr) -> int {
@@ -1285,11 +1346,8 @@ int linear_host_banded(const void *X, int x_dtype, inv_weight_t W, const float *
         uint16_t *xb = (uint16_t *)g.x16.p + r0 * ldw;
         if (ex.nm) {
             TRY(launch_norm_rows((const float *)g.xin.p + r0 * K, *ex.nm, ex.nscale, ex.nshift, nr, K, xb, ldw));
-        } else if (!direct) {
-            if (x_dtype == INV_DT_F32)
-                TRY(launch_cvt_rows_f32((const float *)g.xin.p + r0 * K, K, xb, ldw, nr, K, ldw));
-            else
-                TRY(launch_copy_rows_bf16((const uint16_t *)g.xin.p + r0 * K, K, xb, ldw, nr, K, ldw));
+        } else if (!direct) {  // bf16 rows re-pitched to ldw
+            TRY(launch_copy_rows_bf16((const uint16_t *)g.xin.p + r0 * K, K, xb, ldw, nr, K, ldw));
         }
         // accumulating reads the band's Y as C (beta = 1) in place, as the one-pass call does
         return run_gemm(W->w, ldw, xb, ldw, yb, N, out, bd, ex.accumulate ? (const float *)yb : nullptr, N, 1.0f,
@@ -1351,7 +1409,10 @@ int linear_impl(const char *who, const void *X, int x_dtype, inv_weight_t W, con
         const int pipe_mode = env_int("INV_HIP_HOST_PIPELINE", 1);
         if (pipe_mode && !precise) {
             const TileChoice tc = choose_tiles(M, W->rows, W->ldw, epilogue);
-            const size_t up_row = (size_t)K * (x_dtype == INV_DT_F32 ? 4 : 2) + (accumulate ? (size_t)N * ysz : 0);
+            // bytes a row sends up: fp32 X not normalised goes as bf16 operand rows
+            const size_t x_up = (x_dtype == INV_DT_F32 && !nm) ? (size_t)W->ldw * 2
+                                                               : (size_t)K * (x_dtype == INV_DT_F32 ? 4 : 2);
+            const size_t up_row = x_up + (accumulate ? (size_t)N * ysz : 0);
             const int64_t mb = host_band_rows(tc, M, up_row, (size_t)N * ysz);
             if (mb > 0 && pipe_ready()) {
                 BandExtras ex;
@@ -1579,10 +1640,9 @@ int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_
     // Host Q and O: query-row bands through the band pipeline (K and V first,
     // whole); bands are whole query blocks of the whole problem's workgroup
     // shape, so each query's result is the one-launch result.
-    const size_t xsz = in_dtype == INV_DT_F32 ? 4 : 2;
     const int64_t band_q =
         (!dev && !prep && !g.stats && env_int("INV_HIP_HOST_PIPELINE", 1))
-            ? host_band_rows(inv::kAttnBlockQ / key_groups, seq_q, (size_t)hq * xsz, (size_t)hq * osz) : 0;
+            ? host_band_rows(inv::kAttnBlockQ / key_groups, seq_q, (size_t)hq * 2, (size_t)hq * osz) : 0;
     const bool banded = band_q > 0 && pipe_ready();
     if (!dev && !banded && env_int("INV_HIP_HOST_PIPELINE", 1) == 2)
         return fail(INV_ERR_UNSUPPORTED, "attention: INV_HIP_HOST_PIPELINE=2 but this call is not banded");
@@ -1633,22 +1693,22 @@ int attention_impl(const void *Q, const void *K, const void *V, void *O, int in_
         p.key_mask = (const int32_t *)g.amask.p;
     }
     if (banded) {
-        // a band's host Q rows go up raw (fp32 to the staging rows, bf16 straight
-        // into the operand), are rounded on the device, and its queries run as a
+        // a band's host Q rows go up as bf16 operand rows (fp32 rounded by the
+        // host on the way into the bounce buffer), and its queries run as a
         // smaller problem whose causal offset counts from the band's first row
-        const size_t in_row = (size_t)hq * xsz, out_row = (size_t)hq * osz;
-        TRY(ensure(g.aq, (size_t)(seq_q * hq) * 2));
-        if (in_dtype == INV_DT_F32) TRY(ensure(g.aqin, (size_t)seq_q * in_row));
-        char *qraw = in_dtype == INV_DT_F32 ? (char *)g.aqin.p : (char *)g.aq.p;
+        const size_t row16 = (size_t)hq * 2, out_row = (size_t)hq * osz;
+        TRY(ensure(g.aq, (size_t)seq_q * row16));
         auto stage = [&](int64_t r0, int64_t nr, char *pin) -> int {
-            par_copy_rows(pin, in_row, (const char *)Q + r0 * in_row, in_row, nr, in_row);
-            HIPCHK(hipMemcpyAsync(qraw + (size_t)r0 * in_row, pin, (size_t)nr * in_row, hipMemcpyHostToDevice,
+            if (in_dtype == INV_DT_F32)
+                par_cvt_rows((uint16_t *)pin, hq, (const float *)Q + r0 * hq, hq, nr, hq, hq);
+            else
+                par_copy_rows(pin, row16, (const char *)Q + r0 * row16, row16, nr, row16);
+            HIPCHK(hipMemcpyAsync((char *)g.aq.p + (size_t)r0 * row16, pin, (size_t)nr * row16, hipMemcpyHostToDevice,
                                   g.pipe.up));
             return INV_OK;
         };
         auto compute = [&](int64_t r0, int64_t nr) -> int {
             uint16_t *qb = (uint16_t *)g.aq.p + r0 * hq;
-            if (in_dtype == INV_DT_F32) TRY(launch_cvt_rows_f32((const float *)g.aqin.p + r0 * hq, hq, qb, hq, nr, hq, hq));
             inv::AttnParams pb = p;
             pb.Q = qb;
             pb.ldq = hq;

@@ -50,7 +50,7 @@ CASES = [
     (1100, 1000, 1000, "silu", False, "f32", "bf16"),
     (777, 1001, 1500, "gelu", True, "bf16", "f32"),    # bf16 rows of 2002 bytes: staged, then copied
     (1536, 512, 2048, "none", True, "bf16", "bf16"),   # bf16 rows land in the operand as they are
-    (1025, 1900, 300, "silu", True, "f32", "f32"),     # the input side sets the band; last band 1 row
+    (1025, 1900, 300, "silu", True, "f32", "f32"),     # the input side sets the band
 ]
 
 
@@ -254,3 +254,45 @@ def test_attention_not_banded_below_two_bands(hiplib, monkeypatch):
     monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "1")
     O = q.attention(Q, K, V, heads=8, head_dim=128)
     assert np.all(np.isfinite(O))
+
+
+def tie_values(rng, shape):
+    """fp32 values whose low half-words sit at and around the bf16 rounding ties
+    (normal exponents from ~1e-9 to ~2e9, both signs)."""
+    hi = rng.integers(0x3000, 0x4F00, size=shape, dtype=np.uint32)
+    sign = rng.integers(0, 2, size=shape, dtype=np.uint32) << np.uint32(31)
+    low = rng.choice(np.array([0x0000, 0x0001, 0x7FFF, 0x8000, 0x8001, 0xFFFF], np.uint32), size=shape)
+    return ((hi << np.uint32(16)) | low | sign).view(np.float32)
+
+
+@pytest.mark.parametrize("path", ["serial", "banded"])
+def test_host_rounding_is_the_device_rounding(hiplib, monkeypatch, path):
+    """Host fp32 X is rounded to bf16 by the host on its way into the bounce
+    buffers.  Through an identity weight Y is the rounded X itself: nearest
+    even at every tie, as the oracle rounds and as the device-pointer call
+    (rounded on the device) gives; a NaN makes its whole row NaN on both."""
+    M, K = 2600, 512
+    X = tie_values(np.random.default_rng(77), (M, K))
+    X[0, 5] = np.nan
+    W = oracle.f32_to_bf16_rne(np.eye(K, dtype=np.float32))
+    monkeypatch.setenv("INV_HIP_HOST_BAND_MB", "1")
+    monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "2" if path == "banded" else "0")
+    with q.Weight(W) as w:
+        y = q.linear(X, w)
+        y_dev = device_call(X, "f32", w, M, "f32", "none")
+    np.testing.assert_array_equal(y, y_dev)
+    assert np.all(np.isnan(y[0]))
+    np.testing.assert_array_equal(y[1:], bf16_bits_to_f32(oracle.f32_to_bf16_rne(X[1:])))
+
+
+def test_fp32_weight_rounded_on_upload_is_the_oracle_rounding(hiplib):
+    """inv_hip_weight_upload_f32 rounds on the host (rows padded 1001 -> 1008):
+    the same products as the weight rounded by the oracle and uploaded as bf16."""
+    N, K, M = 300, 1001, 64
+    rng = np.random.default_rng(78)
+    W = tie_values(rng, (N, K))
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    with q.Weight(W) as w32, q.Weight(oracle.f32_to_bf16_rne(W)) as w16:
+        y32 = device_call(X, "f32", w32, M, "f32", "none")
+        y16 = device_call(X, "f32", w16, M, "f32", "none")
+    np.testing.assert_array_equal(y32, y16)

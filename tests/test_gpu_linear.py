@@ -438,8 +438,8 @@ def test_allocation_cap_returns_oom_from_every_entry_point(hiplib, monkeypatch):
         with q.Weight(W, b) as w:  # small: under the cap
             y = q.linear(X, w)
             check(y, X, W, b)
-        # fp32 X of 4096 x 4096 needs a 64 MiB staging buffer: refused
-        M = K = 4096
+        # fp32 X of 8192 x 4096 needs a 64 MiB bf16 operand (rounded on the host): refused
+        M, K = 8192, 4096
         Xb = np.zeros((M, K), np.float32)
         Wb = np.zeros((16, K), np.uint16)
         with q.Weight(Wb) as w:
