@@ -547,8 +547,17 @@ __global__ void __launch_bounds__(256) conv3x3_thin(const float *__restrict__ sr
     __shared__ __attribute__((aligned(16))) uint32_t wts[CP][9][OC];
     // wave-uniform row bookkeeping in scalar registers; a lane adds its column
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int oh0 = blockIdx.y * CT_TH, ow0 = blockIdx.x * CT_TW;
-    const int b = blockIdx.z;
+    // Workgroup w of the dispatch runs on XCD w % 8.  The tiles are handed out
+    // so that consecutive tiles (x fastest), which share their halo columns and
+    // rows, run on one XCD and meet in its L2: the image's lines are fetched
+    // once (1.05x the image at 1024x1024) instead of about twice.  The grid has
+    // at most INT32_MAX workgroups (checked at launch).
+    const int gx = gridDim.x, gxy = gx * gridDim.y, total = gxy * gridDim.z;
+    const int wid = blockIdx.x + gx * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int per = total >> 3, rem = total & 7, xcd = wid & 7, local = wid >> 3;
+    const int L = (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+    const int b = L / gxy, by = (L - b * gxy) / gx, bx = L - b * gxy - by * gx;
+    const int oh0 = by * CT_TH, ow0 = bx * CT_TW;
     const float *img = src + (int64_t)b * C * H * W;
     const int64_t plane = (int64_t)H * W;
     const int ty = tid >> 4, tx = (tid & 15) * 4;

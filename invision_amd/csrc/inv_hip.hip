@@ -1840,6 +1840,7 @@ int conv2d_impl(const float *src, inv_weight_t Wt, const float *bias, float *dst
         const dim3 grid((unsigned)((outW + inv::CT_TW - 1) / inv::CT_TW), (unsigned)((outH + inv::CT_TH - 1) / inv::CT_TH),
                         (unsigned)batch);
         if (grid.y > 65535) return fail(INV_ERR_UNSUPPORTED, "conv2d: image too tall");
+        if ((int64_t)grid.x * grid.y * grid.z > INT32_MAX) return fail(INV_ERR_UNSUPPORTED, "conv2d: too many tiles");
         if (out_ch <= 3)  // RGB
             hipLaunchKernelGGL(inv::conv3x3_thin<3>, grid, dim3(256), 0, g.stream, sd, Wt->w, Wt->ldw, bd, yd,
                                (int)in_ch, (int)H, (int)W, (int)padding, (int)out_ch, (int)outH, (int)outW);
