@@ -355,6 +355,21 @@ void release(Buf &b) {
     b.cap = 0;
 }
 
+int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return (v && *v) ? atoi(v) : dflt;
+}
+
+// The serial copies through the bounce buffers go in pieces of about this
+// many bytes (whole rows, at most a bounce buffer), two in flight: the host
+// side of one piece (a copy or a rounding into pinned memory) runs while the
+// DMA moves its neighbour, so pieces much smaller than a buffer leave less of
+// either exposed at the ends.  INV_HIP_COPY_CHUNK_MB changes it (1-32).
+size_t copy_chunk() {
+    const int mb = env_int("INV_HIP_COPY_CHUNK_MB", 8);
+    return (size_t)std::max(1, std::min(32, mb)) << 20;
+}
+
 // Host rows -> contiguous device rows, through the pinned bounce buffers.
 // rows x width bytes; host rows are `pitch` bytes apart.
 int h2d_rows(void *dev, const void *host, int64_t rows, size_t width, size_t pitch) {
@@ -373,7 +388,7 @@ int h2d_rows(void *dev, const void *host, int64_t rows, size_t width, size_t pit
             }
         return INV_OK;
     }
-    const int64_t rows_per = (int64_t)(kPinChunk / width);
+    const int64_t rows_per = std::max<int64_t>(1, (int64_t)(copy_chunk() / width));
     for (int64_t r0 = 0; r0 < rows; r0 += rows_per) {
         const int64_t nr = std::min(rows_per, rows - r0);
         HIPCHK(hipEventSynchronize(g.pin_ev[k]));
@@ -392,7 +407,7 @@ int h2d_rows(void *dev, const void *host, int64_t rows, size_t width, size_t pit
 int h2d_rows_bf16(uint16_t *dev, const float *host, int64_t rows, int64_t cols, int64_t ld, int64_t cols_pad) {
     const size_t width = (size_t)cols_pad * 2;
     if (width > kPinChunk) return fail(INV_ERR_ARG, "internal: bf16 row of %zu bytes above a bounce buffer", width);
-    const int64_t rows_per = (int64_t)(kPinChunk / width);
+    const int64_t rows_per = std::max<int64_t>(1, (int64_t)(copy_chunk() / width));
     int k = 0;
     for (int64_t r0 = 0; r0 < rows; r0 += rows_per) {
         const int64_t nr = std::min(rows_per, rows - r0);
@@ -419,7 +434,7 @@ int d2h_rows(void *host, const void *dev, int64_t rows, size_t width, size_t pit
         for (int64_t r = 0; r < rows; ++r)
             for (size_t off = 0; off < width; off += kPinChunk) pieces.push_back({r, 1, off, std::min(kPinChunk, width - off)});
     } else {
-        const int64_t rows_per = (int64_t)(kPinChunk / width);
+        const int64_t rows_per = std::max<int64_t>(1, (int64_t)(copy_chunk() / width));
         for (int64_t r0 = 0; r0 < rows; r0 += rows_per) {
             int64_t nr = std::min(rows_per, rows - r0);
             pieces.push_back({r0, nr, 0, (size_t)nr * width});
@@ -472,11 +487,6 @@ struct CfgMeta {
 const CfgMeta kCfg[INV_GEMM_NUM_CONFIGS] = {INV_GEMM_CONFIG_IDS(INV_META)};
 #undef INV_META
 constexpr int kNumCfg = INV_GEMM_NUM_CONFIGS;
-
-int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    return (v && *v) ? atoi(v) : dflt;
-}
 
 // Workgroups of configuration m resident per CU (LDS is the binding limit).
 int cfg_occupancy(const CfgMeta &m) { return std::max(1, std::min(2, (160 * 1024) / m.lds)); }
