@@ -44,6 +44,13 @@ __device__ __forceinline__ uint4 pack8(const uint16_t (&h)[8]) {
     return o;
 }
 
+// An image element as fp32: an fp32 image as it is, a bf16 image (an fp32
+// image the host already rounded) widened exactly.
+__device__ __forceinline__ float image_value(const float *p, int64_t i) { return p[i]; }
+__device__ __forceinline__ float image_value(const uint16_t *p, int64_t i) {
+    return __uint_as_float((uint32_t)p[i] << 16);
+}
+
 // Row-wise fp32 -> bf16 with nseg segments per output row: segment s of row r
 // starts at dst + r*ldd + s*cols_pad and holds lo parts if bit s of lo_mask is
 // set, hi parts otherwise (nseg = 1, lo_mask = 0: plain RNE rounding).
@@ -425,7 +432,7 @@ __global__ void __launch_bounds__(256) transpose64_to_bf16(const SrcT *__restric
 // consecutive pixels (one per lane, so reads along an image row coalesce; every
 // group's loads are issued before the first is used) into an LDS tile, then the
 // block is written out row by row, eight lanes per 128-byte row segment.  src
-// is one image [C x H x W] fp32; ldc % 64 == 0 and col 16-byte aligned; grid
+// is one image [C x H x W], fp32 or bf16; ldc % 64 == 0 and col 16-byte aligned; grid
 // (ceil(npix / (64 * IM2COL_PG)), ldc / 64).
 constexpr int IM2COL_PG = 4;
 
@@ -444,7 +451,8 @@ __global__ void __launch_bounds__(256) conv_filter_tap_major(const uint16_t *__r
     const int t = k / C, c = k - t * C;
     dst[i] = src[o * lds + (int64_t)c * taps + t];
 }
-__global__ void __launch_bounds__(512) im2col_bf16(const float *__restrict__ src, uint16_t *__restrict__ col, int H,
+template <typename SrcT>
+__global__ void __launch_bounds__(512) im2col_bf16(const SrcT *__restrict__ src, uint16_t *__restrict__ col, int H,
                                                    int W, int kH, int kW, int stride, int pad, int outW, int oh0,
                                                    int64_t npix, int K, int64_t ldc) {
     constexpr int PITCH = 72;  // bf16 per LDS row: 64 + 8, so 16-byte writes of 64 rows spread over the banks
@@ -471,7 +479,7 @@ __global__ void __launch_bounds__(512) im2col_bf16(const float *__restrict__ src
             for (int e = 0; e < 8; ++e) {
                 const int ih = ih0 + kr, iw = iw0 + kc;
                 v[g][e] = (in && k0 + e < K && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
-                              ? src[((int64_t)ic * H + ih) * W + iw]
+                              ? image_value(src, ((int64_t)ic * H + ih) * W + iw)
                               : 0.0f;
                 if (++kc == kW) {
                     kc = 0;
@@ -517,7 +525,8 @@ __global__ void __launch_bounds__(512) im2col_bf16(const float *__restrict__ src
 // pixels of one row per thread) for all OC (>= n_oc) output channels.  Input
 // channels go CT_CC at a time through an LDS tile of the (CT_TH + 2) x
 // (CT_TW + 2) input window, each value rounded to bf16 (RNE) as the patch
-// matrix rounds it and stored as bf16 pairs of channels (2p, 2p + 1); the
+// matrix rounds it (a bf16 image, rounded by the host, is used as it is) and
+// stored as bf16 pairs of channels (2p, 2p + 1); the
 // filter's bf16 values (the weight handle's rows, [out_ch x in_ch*9] in the
 // reference's (ic, kh, kw) order, row pitch ldw) are paired the same way, OC
 // consecutive per tap so each tap's are one broadcast read.  v_dot2_f32_bf16
@@ -528,8 +537,8 @@ __global__ void __launch_bounds__(512) im2col_bf16(const float *__restrict__ src
 // loads in flight, not of one row's latency at a time.
 // grid (ceil(outW / CT_TW), ceil(outH / CT_TH), batch).
 constexpr int CT_TH = 16, CT_TW = 64, CT_CC = 8;
-template <int OC>
-__global__ void __launch_bounds__(256) conv3x3_thin(const float *__restrict__ src, const uint16_t *__restrict__ filt,
+template <int OC, typename SrcT>
+__global__ void __launch_bounds__(256) conv3x3_thin(const SrcT *__restrict__ src, const uint16_t *__restrict__ filt,
                                                     int64_t ldw, const float *__restrict__ bias,
                                                     float *__restrict__ dst, int C, int H, int W, int pad, int n_oc,
                                                     int outH, int outW) {
@@ -558,7 +567,7 @@ __global__ void __launch_bounds__(256) conv3x3_thin(const float *__restrict__ sr
     const int L = (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
     const int b = L / gxy, by = (L - b * gxy) / gx, bx = L - b * gxy - by * gx;
     const int oh0 = by * CT_TH, ow0 = bx * CT_TW;
-    const float *img = src + (int64_t)b * C * H * W;
+    const SrcT *img = src + (int64_t)b * C * H * W;
     const int64_t plane = (int64_t)H * W;
     const int ty = tid >> 4, tx = (tid & 15) * 4;
     const int iw = ow0 - pad + lane;
@@ -568,9 +577,9 @@ __global__ void __launch_bounds__(256) conv3x3_thin(const float *__restrict__ sr
     // the two channels' values at one window position (zero outside the image or past C)
     auto pair_at = [&](int ic, int ih, int iwp, bool ok, float (&out)[2]) {
         const bool rin = ok && ic < C && (unsigned)ih < (unsigned)H;
-        const float *rp = img + (rin ? ((int64_t)ic * H + ih) * W + iwp : 0);
-        out[0] = rin ? rp[0] : 0.f;
-        out[1] = rin && ic + 1 < C ? rp[plane] : 0.f;
+        const SrcT *rp = img + (rin ? ((int64_t)ic * H + ih) * W + iwp : 0);
+        out[0] = rin ? image_value(rp, 0) : 0.f;
+        out[1] = rin && ic + 1 < C ? image_value(rp, plane) : 0.f;
     };
     // issue chunk c0's loads into v (window columns 0..63 of channels 2p and
     // 2p + 1, one row pair per wave and step), v2 (the two halo columns, spread

@@ -1794,6 +1794,23 @@ int conv_gather_cfg(int64_t in_ch, int64_t out_ch, int64_t H, int64_t W, int64_t
     return (mode == 2 || tiles * 2 >= cus) ? cfg : -1;
 }
 
+// The direct 3x3 kernel for at most 8 output channels on an fp32 or bf16 image.
+template <typename T>
+int launch_conv3x3_thin(dim3 grid, const T *sd, inv_weight_t Wt, const float *bd, float *yd, int64_t in_ch, int64_t H,
+                        int64_t W, int64_t padding, int64_t out_ch, int64_t outH, int64_t outW) {
+    if (out_ch <= 3)  // RGB
+        hipLaunchKernelGGL((inv::conv3x3_thin<3, T>), grid, dim3(256), 0, g.stream, sd, Wt->w, Wt->ldw, bd, yd,
+                           (int)in_ch, (int)H, (int)W, (int)padding, (int)out_ch, (int)outH, (int)outW);
+    else if (out_ch <= 4)
+        hipLaunchKernelGGL((inv::conv3x3_thin<4, T>), grid, dim3(256), 0, g.stream, sd, Wt->w, Wt->ldw, bd, yd,
+                           (int)in_ch, (int)H, (int)W, (int)padding, (int)out_ch, (int)outH, (int)outW);
+    else
+        hipLaunchKernelGGL((inv::conv3x3_thin<8, T>), grid, dim3(256), 0, g.stream, sd, Wt->w, Wt->ldw, bd, yd,
+                           (int)in_ch, (int)H, (int)W, (int)padding, (int)out_ch, (int)outH, (int)outW);
+    HIPCHK(hipGetLastError());
+    return INV_OK;
+}
+
 int conv2d_impl(const float *src, inv_weight_t Wt, const float *bias, float *dst, int64_t in_ch, int64_t out_ch,
                 int64_t H, int64_t W, int64_t kH, int64_t kW, int64_t stride, int64_t padding, int64_t batch,
                 int flags) {
@@ -1833,13 +1850,23 @@ int conv2d_impl(const float *src, inv_weight_t Wt, const float *bias, float *dst
             bd = (const float *)g.bias.p;
         }
     }
+    // A host image goes up rounded to bf16 by the host (every path rounds it
+    // to bf16 before use, so the results are the bits of an fp32 upload): sd16.
     const float *sd = src;
+    const uint16_t *sd16 = nullptr;
     float *yd = dst;
     const size_t sbytes = (size_t)(batch * img) * 4, ybytes = (size_t)(batch * out_ch * P) * 4;
     if (!dev) {
-        TRY(ensure(g.csrc, sbytes));
-        TRY(h2d_rows(g.csrc.p, src, 1, sbytes, sbytes));
-        sd = (const float *)g.csrc.p;
+        if ((size_t)W * 2 <= kPinChunk) {
+            TRY(ensure(g.csrc, sbytes / 2));
+            TRY(h2d_rows_bf16((uint16_t *)g.csrc.p, src, batch * in_ch * H, W, W, W));
+            sd16 = (const uint16_t *)g.csrc.p;
+            sd = nullptr;
+        } else {
+            TRY(ensure(g.csrc, sbytes));
+            TRY(h2d_rows(g.csrc.p, src, 1, sbytes, sbytes));
+            sd = (const float *)g.csrc.p;
+        }
         TRY(ensure(g.cdst, ybytes));
         yd = (float *)g.cdst.p;
     } else if (!aligned(src, 4) || !aligned(dst, 4)) {
@@ -1851,16 +1878,10 @@ int conv2d_impl(const float *src, inv_weight_t Wt, const float *bias, float *dst
                         (unsigned)batch);
         if (grid.y > 65535) return fail(INV_ERR_UNSUPPORTED, "conv2d: image too tall");
         if ((int64_t)grid.x * grid.y * grid.z > INT32_MAX) return fail(INV_ERR_UNSUPPORTED, "conv2d: too many tiles");
-        if (out_ch <= 3)  // RGB
-            hipLaunchKernelGGL(inv::conv3x3_thin<3>, grid, dim3(256), 0, g.stream, sd, Wt->w, Wt->ldw, bd, yd,
-                               (int)in_ch, (int)H, (int)W, (int)padding, (int)out_ch, (int)outH, (int)outW);
-        else if (out_ch <= 4)
-            hipLaunchKernelGGL(inv::conv3x3_thin<4>, grid, dim3(256), 0, g.stream, sd, Wt->w, Wt->ldw, bd, yd,
-                               (int)in_ch, (int)H, (int)W, (int)padding, (int)out_ch, (int)outH, (int)outW);
+        if (sd16)
+            TRY(launch_conv3x3_thin(grid, sd16, Wt, bd, yd, in_ch, H, W, padding, out_ch, outH, outW));
         else
-            hipLaunchKernelGGL(inv::conv3x3_thin<8>, grid, dim3(256), 0, g.stream, sd, Wt->w, Wt->ldw, bd, yd,
-                               (int)in_ch, (int)H, (int)W, (int)padding, (int)out_ch, (int)outH, (int)outW);
-        HIPCHK(hipGetLastError());
+            TRY(launch_conv3x3_thin(grid, sd, Wt, bd, yd, in_ch, H, W, padding, out_ch, outH, outW));
         g.calls++;
         if (!dev) {
             TRY(d2h_rows(dst, yd, 1, ybytes, ybytes));
@@ -1914,8 +1935,11 @@ int conv2d_impl(const float *src, inv_weight_t Wt, const float *bias, float *dst
         p.cv_stride = (int)stride;
         p.cv_pad = (int)padding;
         for (int64_t b = 0; b < batch; ++b) {
-            // image b: [C x HW] fp32 -> [HW x C] bf16
-            TRY(launch_transpose<float>(sd + b * img, HW, nhwc, in_ch, in_ch, HW, in_ch));
+            // image b: [C x HW] fp32 (or bf16) -> [HW x C] bf16
+            if (sd16)
+                TRY(launch_transpose<uint16_t>(sd16 + b * img, HW, nhwc, in_ch, in_ch, HW, in_ch));
+            else
+                TRY(launch_transpose<float>(sd + b * img, HW, nhwc, in_ch, in_ch, HW, in_ch));
             p.W = nhwc;
             p.Y = yd + b * out_ch * P;
             p.vec_store = (P % 4 == 0) && aligned(p.Y, 16);
@@ -1944,13 +1968,18 @@ int conv2d_impl(const float *src, inv_weight_t Wt, const float *bias, float *dst
     TRY(ensure(g.ccol, (size_t)(chunk_rows * row_bytes)));
     uint16_t *col = (uint16_t *)g.ccol.p;
     for (int64_t b = 0; b < batch; ++b) {
-        const float *in_b = sd + b * img;
         float *out_b = yd + b * out_ch * P;
         for (int64_t oh0 = 0; oh0 < outH; oh0 += chunk_rows) {
             const int64_t rows = std::min(chunk_rows, outH - oh0), npix = rows * outW;
             const dim3 grid((unsigned)((npix + 64 * inv::IM2COL_PG - 1) / (64 * inv::IM2COL_PG)), (unsigned)(ldc / 64));
-            hipLaunchKernelGGL(inv::im2col_bf16, grid, dim3(512), 0, g.stream, in_b, col, (int)H, (int)W, (int)kH,
-                               (int)kW, (int)stride, (int)padding, (int)outW, (int)oh0, npix, (int)K, ldc);
+            if (sd16)
+                hipLaunchKernelGGL(inv::im2col_bf16<uint16_t>, grid, dim3(512), 0, g.stream, sd16 + b * img, col,
+                                   (int)H, (int)W, (int)kH, (int)kW, (int)stride, (int)padding, (int)outW, (int)oh0,
+                                   npix, (int)K, ldc);
+            else
+                hipLaunchKernelGGL(inv::im2col_bf16<float>, grid, dim3(512), 0, g.stream, sd + b * img, col, (int)H,
+                                   (int)W, (int)kH, (int)kW, (int)stride, (int)padding, (int)outW, (int)oh0, npix,
+                                   (int)K, ldc);
             HIPCHK(hipGetLastError());
             // Y[oc][oh0*outW + q] (row pitch P) = Wt[oc] . col[q] + bias[oc]
             TRY(run_gemm(col, ldc, Wt->w, Wt->ldw, out_b + oh0 * outW, P, inv::OUT_F32, nullptr, nullptr, 0, 1.0f,

@@ -124,6 +124,47 @@ def test_conv2d_device_pointers_match_host(hiplib):
                 a.free()
 
 
+# (path, b, c, oc, H, W, kH, kW, s, p): the direct kernel, the implicit GEMM (forced with
+# INV_HIP_CONV_GATHER=2) and the patch matrix
+HOST_ROUNDING_CASES = [
+    ("direct", 1, 64, 3, 37, 70, 3, 3, 1, 1),
+    ("gather", 1, 128, 128, 24, 40, 3, 3, 1, 1),
+    ("patch", 2, 16, 24, 14, 18, 3, 3, 2, 1),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path,b,c,oc,H,W,kH,kW,s,p", HOST_ROUNDING_CASES)
+def test_conv2d_host_image_rounded_on_upload_matches_device(hiplib, monkeypatch, path, b, c, oc, H, W, kH, kW, s, p):
+    """A host image goes up rounded to bf16 by the host; the device-pointer call
+    rounds the same fp32 image on the device.  Image values sit at and around
+    the bf16 rounding ties, so any difference in the rounding shows: the two
+    results must be identical on every path."""
+    rng = np.random.default_rng(c + oc)
+    hi = rng.integers(0x3C00, 0x4100, size=(b, c, H, W), dtype=np.uint32)
+    sign = rng.integers(0, 2, size=hi.shape, dtype=np.uint32) << np.uint32(31)
+    low = rng.choice(np.array([0x0000, 0x0001, 0x7FFF, 0x8000, 0x8001, 0xFFFF], np.uint32), size=hi.shape)
+    x = np.ascontiguousarray(((hi << np.uint32(16)) | low | sign).view(np.float32))
+    _, w, bias = gen(14, b, c, oc, H, W, kH, kW)
+    monkeypatch.setenv("INV_HIP_CONV_GATHER", "2" if path == "gather" else "0")
+    dims = q.QNNConv2DShape(b, oc, H, W, kH, kW, p, s)
+    with q.Weight(w) as wt:
+        yh = q.conv2d(x, wt, bias, c, oc, H, W, kH, kW, s, p, b)
+        xd = q.DeviceArray.from_host(x)
+        bd = q.DeviceArray.from_host(bias)
+        yd = q.DeviceArray(tuple(dims), "f32")
+        try:
+            q.conv2d_device(xd, wt, yd, c, oc, H, W, kH, kW, s, p, b, bias=bd)
+            y_dev = yd.to_host()
+        finally:
+            for a in (xd, bd, yd):
+                a.free()
+    print(f"[conv2d host rounding] {path}: host == device", flush=True)
+    np.testing.assert_array_equal(yh, y_dev)
+    ref_b = oracle.conv2d_f64(round_bf16(x), w, bias, c, oc, H, W, kH, kW, s, p, b)
+    assert oracle.normwise_err(yh, ref_b) <= TOL_BF16
+
+
 @pytest.mark.gpu
 def test_conv2d_row_chunks_match_one_pass(hiplib):
     # A patch-matrix cap of 1 MiB splits the 64x56 output into bands of rows;
