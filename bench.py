@@ -233,8 +233,9 @@ def run_workload(name, steps, warmup, check=True, host_path=False, warmup_second
     res["launch_ms_p10_p50_p90"] = [round(p10, 5), round(p50, 5), round(p90, 5)]
     if host_path and epi in ("none", "silu", "gelu"):
         # The reference's own calling convention: fp32 X and Y in host memory,
-        # copied over PCIe on every call (pinned bounce buffers), X rounded on
-        # the device.  Reported beside the device-resident rate, never as it.
+        # copied over PCIe on every call (pinned bounce buffers), X rounded to
+        # bf16 by the host on its way up.  Reported beside the device-resident
+        # rate, never as it.
         # Y is the caller's buffer, written on every call (as the reference's
         # dst TMemoryBlock), not a fresh array whose first touch would be timed.
         Xh = np.ascontiguousarray(X if xdt == "f32" else bf16_bits_to_f32(Xin))
@@ -242,26 +243,7 @@ def run_workload(name, steps, warmup, check=True, host_path=False, warmup_second
         host_call = lambda: hip.call("inv_hip_linear", Xh.ctypes.data, hip.INV_DT_F32, w.handle, None, Yh.ctypes.data,
                                      hip.INV_DT_F32, M, K, R, hip.INV_EPI_NONE if epi == "none" else
                                      (hip.INV_EPI_SILU if epi == "silu" else hip.INV_EPI_GELU_ERF), 0)
-        def time_host():
-            host_call()
-            reps, th = 0, time.perf_counter()
-            while reps < 3 or time.perf_counter() - th < 1.0:
-                host_call()
-                reps += 1
-            return (time.perf_counter() - th) * 1e3 / reps
-
-        # Row bands overlap upload, GEMM and download (the library's default);
-        # the one serial pass (INV_HIP_HOST_PIPELINE=0) is timed beside it.
-        host_ms = time_host()
-        prev = os.environ.get("INV_HIP_HOST_PIPELINE")
-        os.environ["INV_HIP_HOST_PIPELINE"] = "0"
-        try:
-            res["host_fp32_io_serial_ms"] = time_host()
-        finally:
-            if prev is None:
-                del os.environ["INV_HIP_HOST_PIPELINE"]
-            else:
-                os.environ["INV_HIP_HOST_PIPELINE"] = prev
+        host_ms, res["host_fp32_io_serial_ms"] = host_times(host_call)
         res["host_fp32_io_ms"] = host_ms
         res["host_fp32_io_tflops"] = flops / (host_ms * 1e-3) / 1e12
     if check:
@@ -419,9 +401,39 @@ def vendor_gemm_child(d, workload, steps=50, warmup_seconds=1.0):
     return 0
 
 
-def run_attention(name, steps, warmup_seconds=0.5, check=True):
+def time_host_call(call):
+    """Wall milliseconds per call of a host-pointer entry point (one untimed call,
+    then at least 3 calls and 1 s)."""
+    call()
+    reps, th = 0, time.perf_counter()
+    while reps < 3 or time.perf_counter() - th < 1.0:
+        call()
+        reps += 1
+    return (time.perf_counter() - th) * 1e3 / reps
+
+
+def host_times(call):
+    """(banded, serial) wall ms of a host-pointer call: the library's default
+    overlaps upload, kernels and download in bands; INV_HIP_HOST_PIPELINE=0 is
+    the one serial pass."""
+    banded = time_host_call(call)
+    prev = os.environ.get("INV_HIP_HOST_PIPELINE")
+    os.environ["INV_HIP_HOST_PIPELINE"] = "0"
+    try:
+        serial = time_host_call(call)
+    finally:
+        if prev is None:
+            del os.environ["INV_HIP_HOST_PIPELINE"]
+        else:
+            os.environ["INV_HIP_HOST_PIPELINE"] = prev
+    return banded, serial
+
+
+def run_attention(name, steps, warmup_seconds=0.5, check=True, host_path=False):
     """inv_hip_attention on resident bf16 Q, K, V; FLOP = 4 * seq_q * seq_k * head_dim * heads
-    (halved for causal: the keys after the diagonal are skipped)."""
+    (halved for causal: the keys after the diagonal are skipped).  host_path: also
+    the wall time of the call on fp32 Q, K, V and O in host memory (the reference's
+    calling convention), banded and serial."""
     import ctypes
     from invision_amd import hip
     from invision_amd import quicknn_hip as q
@@ -501,16 +513,23 @@ def run_attention(name, steps, warmup_seconds=0.5, check=True):
         # is checked against unrounded fp32 inputs, which adds their bf16 rounding (1.5e-2 in the tests)
         res["parity_tol"] = (1.5e-2 if prep else 4e-3) + 2.0 ** -8
         res["parity_ok"] = bool(res["parity_normwise_sampled_rows"] <= res["parity_tol"])
+    if host_path and not prep:
+        Oh = np.zeros((sq, heads * d), np.float32)
+        host_call = lambda: hip.call("inv_hip_attention", Qf.ctypes.data, Kf.ctypes.data, Vf.ctypes.data,
+                                     Oh.ctypes.data, hip.INV_DT_F32, hip.INV_DT_F32, heads, kvh, sq, sk, d,
+                                     1.0 / float(np.sqrt(d)), hip.INV_ATTN_CAUSAL if causal else 0)
+        res["host_fp32_io_ms"], res["host_fp32_io_serial_ms"] = host_times(host_call)
     for a in (qd, kd, vd, od) + ((wqd, wkd, cd, sd) if prep else ()):
         a.free()
     return res
 
 
-def run_conv(name, steps, warmup_seconds=0.5, check=True):
+def run_conv(name, steps, warmup_seconds=0.5, check=True, host_path=False):
     """inv_hip_conv2d on a device-resident fp32 NCHW image (im2col into the bf16
     patch matrix, then the GEMM with the per-channel bias); FLOP = 2 * out_ch *
     outH * outW * in_ch * kH * kW.  The patch matrix is written once per call:
-    outH * outW * round_up(K, 64) * 2 bytes."""
+    outH * outW * round_up(K, 64) * 2 bytes.  host_path: also the wall time of
+    the call on an fp32 image and output in host memory."""
     import ctypes
     from invision_amd import hip
     from invision_amd import quicknn_hip as q
@@ -564,6 +583,11 @@ def run_conv(name, steps, warmup_seconds=0.5, check=True):
         res["parity_normwise_sampled_pixels"] = err / top
         res["parity_tol"] = 1e-4  # same bf16 image and filter values, fp32 accumulation
         res["parity_ok"] = bool(err / top <= res["parity_tol"])
+    if host_path:
+        yh = np.zeros((b, oc, oH, oW), np.float32)
+        res["host_fp32_io_ms"] = time_host_call(
+            lambda: hip.call("inv_hip_conv2d", x.ctypes.data, wt.handle, None, yh.ctypes.data, c, oc, H, W, kH, kW,
+                             s, p, b, 0))
     xd.free()
     yd.free()
     wt.free()
@@ -1006,12 +1030,14 @@ def main():
                     extra.append(run_workload(name, max(5, args.steps // 2), 3, warmup_seconds=0.5, cold=True))
                     log(f"[bench] {json.dumps(extra[-1])}")
         for name in ATTN_WORKLOADS:
-            extra.append(run_attention(name, max(5, args.steps // 4), warmup_seconds=min(args.warmup_seconds, 0.5)))
+            extra.append(run_attention(name, max(5, args.steps // 4), warmup_seconds=min(args.warmup_seconds, 0.5),
+                                       host_path=True))
             log(f"[bench] {json.dumps(extra[-1])}")
         r = run_block(max(5, args.steps // 20), warmup_seconds=min(args.warmup_seconds, 0.5))
         log(f"[bench] {json.dumps(r)}")
         for name in CONV_WORKLOADS:
-            extra.append(run_conv(name, max(5, args.steps // 20), warmup_seconds=min(args.warmup_seconds, 0.5)))
+            extra.append(run_conv(name, max(5, args.steps // 20), warmup_seconds=min(args.warmup_seconds, 0.5),
+                                  host_path=True))
             log(f"[bench] {json.dumps(extra[-1])}")
         failed += [r["name"] for r in extra if not r.get("parity_ok", True)]
 
