@@ -243,6 +243,34 @@ def test_banded_attention_equals_serial_and_device(hiplib, monkeypatch, sq, sk, 
     assert oracle.normwise_err(of, ref) <= 4e-3 + (2.0 ** -8 if odt == "bf16" else 0.0)
 
 
+def test_banded_causal_attention_with_fewer_keys_than_queries(hiplib, monkeypatch):
+    """Causal, 700 keys for 1100 queries: queries 0..399 see no key (their rows
+    are zero) and the first bands' diagonal offsets are negative."""
+    sq, sk, heads, d = 1100, 700, 8, 128
+    Q, K, V = attn_gen(31, sq, sk, heads, heads, d)
+    kw = dict(heads=heads, head_dim=d, causal=True)
+    monkeypatch.setenv("INV_HIP_HOST_BAND_MB", "1")
+    monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "2")
+    o_band = q.attention(Q, K, V, **kw)
+    monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "0")
+    o_serial = q.attention(Q, K, V, **kw)
+    devs = [q.DeviceArray.from_host(a, "f32") for a in (Q, K, V)]
+    od = q.DeviceArray((sq, heads * d), "f32")
+    try:
+        q.attention_device(*devs, od, **kw)
+        o_dev = od.to_host()
+    finally:
+        for a in devs + [od]:
+            a.free()
+    np.testing.assert_array_equal(o_band, o_serial)
+    np.testing.assert_array_equal(o_band, o_dev)
+    assert not np.any(o_band[: sq - sk])
+    # the remaining queries see keys 0 .. i - (sq - sk): a causal call of sk queries over the same keys
+    ref = oracle.attention_f64(round_bf16(Q[sq - sk:]), round_bf16(K), round_bf16(V), heads, heads, d,
+                               1.0 / np.sqrt(d), True)
+    assert oracle.normwise_err(o_band[sq - sk:], ref) <= 4e-3
+
+
 def test_attention_not_banded_below_two_bands(hiplib, monkeypatch):
     """A query count that fits one band runs the one-pass path (PIPELINE=2 then
     reports the call as not banded)."""
