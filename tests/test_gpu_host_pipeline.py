@@ -324,3 +324,19 @@ def test_fp32_weight_rounded_on_upload_is_the_oracle_rounding(hiplib):
         y32 = device_call(X, "f32", w32, M, "f32", "none")
         y16 = device_call(X, "f32", w16, M, "f32", "none")
     np.testing.assert_array_equal(y32, y16)
+
+
+def test_host_rounding_of_few_wide_rows(hiplib):
+    """Two rows of a million columns: the copy threads round column slices of
+    every row (fewer rows than slices).  An fp32 weight and fp32 X of that shape,
+    rounded by the host, give the products of the oracle-rounded bf16 weight and
+    of X rounded on the device."""
+    K = 1_000_003
+    rng = np.random.default_rng(79)
+    W = tie_values(rng, (2, K)) * np.float32(1e-3)
+    X = tie_values(rng, (3, K)) * np.float32(1e-3)
+    with q.Weight(W) as w32, q.Weight(oracle.f32_to_bf16_rne(W)) as w16:
+        y_host = q.linear(X, w32)
+        y_dev = device_call(X, "f32", w16, 3, "f32", "none")
+    np.testing.assert_array_equal(y_host, y_dev)
+    assert np.all(np.isfinite(y_host))
