@@ -856,13 +856,18 @@ def summarize_profile(workload, trace_dir, fetch_dir, write_dir, busy_dir=None, 
         return by
 
     def named_counters(d, kname):
-        """{counter: [(value, duration ns)] } of the dispatches of kernel kname."""
+        """{kernel: {counter: [(value, duration ns)]}} of the dispatches of the kernels matching kname."""
         by = {}
         for r in csv.DictReader(open(find(d, "counter_collection.csv"))):
             if kname in r["Kernel_Name"]:
                 dur = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
-                by.setdefault(r["Counter_Name"], []).append((float(r["Counter_Value"]), dur))
+                by.setdefault(r["Kernel_Name"], {}).setdefault(r["Counter_Name"], []).append(
+                    (float(r["Counter_Value"]), dur))
         return by
+
+    def per_call(by, c):
+        """A counter per call: the sum over the call's GEMM launches of each launch's median."""
+        return sum(statistics.median(v for v, _ in per[c]) for per in by.values())
 
     desc, M, K, N, has_bias, epi, xdt, ydt = WORKLOADS[workload]
     flops = 2.0 * M * N * K
@@ -870,21 +875,31 @@ def summarize_profile(workload, trace_dir, fetch_dir, write_dir, busy_dir=None, 
     stats = list(csv.DictReader(open(find(trace_dir, "kernel_stats.csv"))))
     fe, wr = counters(fetch_dir), counters(write_dir)
     copyk = next(k for k in fe if "copy_words16" in k)
-    gk = next(k for k in fe if kernel in k)
+    # A call's GEMM launches: one, or two with a split tail (the whole rounds as
+    # tiles, then the last round's tiles split two ways along K); per-call
+    # figures sum them.
+    gks = [k for k in fe if kernel in k]
+    gk = " + ".join(gks)
     copy_bytes = 512 << 20
     f_scale = copy_bytes / (statistics.median(fe[copyk]) * 1024)
     w_scale = copy_bytes / (statistics.median(wr[copyk]) * 1024)
-    g_fetch = statistics.median(fe[gk]) * 1024 * f_scale
-    g_write = statistics.median(wr[gk]) * 1024 * w_scale
+    fe_call = sum(statistics.median(fe[k]) for k in gks)
+    wr_call = sum(statistics.median(wr[k]) for k in wr if kernel in k)
+    g_fetch = fe_call * 1024 * f_scale
+    g_write = wr_call * 1024 * w_scale
     srow = next(r for r in stats if kernel in r["Name"])
     # Steady state: the timed launches of run_workload, i.e. the `steps` GEMM
     # dispatches before its final 30 isolated ones (the warm-up before them
     # includes the clock ramp, which the stats table averages in).
     trace = [r for r in csv.DictReader(open(find(trace_dir, "kernel_trace.csv"))) if kernel in r["Kernel_Name"]]
     trace.sort(key=lambda r: int(r["Start_Timestamp"]))
-    durs = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in trace]
-    timed = durs[-(steps + 30):-30] if len(durs) > steps + 30 else durs
-    avg_ns = float(sum(timed)) / len(timed)
+    by_name = {}
+    for r in trace:
+        by_name.setdefault(r["Kernel_Name"], []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    avg_ns, timed = 0.0, []
+    for durs in by_name.values():
+        timed = durs[-(steps + 30):-30] if len(durs) > steps + 30 else durs
+        avg_ns += float(sum(timed)) / len(timed)
     passes = {name: shown(argv) for name, argv, _ in profile_passes(workload, os.path.dirname(trace_dir), cold)}
     cmds = {k: passes[k] for k in ("trace", "fetch", "write", "busy", "l2")}
     tfl = flops / avg_ns / 1e3
@@ -894,14 +909,16 @@ def summarize_profile(workload, trace_dir, fetch_dir, write_dir, busy_dir=None, 
     for r in stats:
         lines.append(f"| `{r['Name'][:110]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
                      f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} |")
-    lines += ["", f"GEMM average over the {len(timed)} timed launches (after the warm-up): {avg_ns / 1e3:.1f} us -> "
+    lines += ["", f"GEMM average over the {len(timed)} timed calls (after the warm-up; {len(by_name)} launch"
+                  f"{'es' if len(by_name) > 1 else ''} each): {avg_ns / 1e3:.1f} us -> "
                   f"{tfl:.1f} TFLOP/s ({tfl / PEAK_BF16_TFLOPS * 100:.1f}% of the {PEAK_BF16_TFLOPS} TFLOP/s bf16 "
                   f"dense MFMA peak).  The table's averages include the warm-up launches.", "",
               "Counter passes (one counter per run):", "", "```", cmds["fetch"], cmds["write"], "```", "",
               "| Kernel | FETCH_SIZE (KiB, median) | WRITE_SIZE (KiB, median) |", "|---|---|---|",
               f"| copy_words16, 512 MiB read + 512 MiB written | {statistics.median(fe[copyk]):.0f} | "
               f"{statistics.median(wr[copyk]):.0f} |",
-              f"| GEMM | {statistics.median(fe[gk]):.0f} | {statistics.median(wr[gk]):.0f} |", "",
+              f"| GEMM{' (per call: its launches summed)' if len(gks) > 1 else ''} | {fe_call:.0f} | {wr_call:.0f} |",
+              "",
               f"Calibration against the copy kernel: FETCH_SIZE x {f_scale:.3f}, WRITE_SIZE x {w_scale:.3f} "
               f"(bytes per KiB the counter reports).", "",
               f"GEMM per launch: {g_fetch / 1e6:.1f} MB fetched from beyond L2 + {g_write / 1e6:.1f} MB written = "
@@ -918,8 +935,8 @@ def summarize_profile(workload, trace_dir, fetch_dir, write_dir, busy_dir=None, 
     extra = {"roofline_bound": bound.lower(), "roofline_frac": max(t_mfma, t_hbm) / avg_ns}
     if busy_dir:
         bc = named_counters(busy_dir, kernel)
-        med = lambda c: statistics.median(v for v, _ in bc[c])
-        dur = statistics.median(d for _, d in bc["GRBM_GUI_ACTIVE"])
+        med = lambda c: per_call(bc, c)
+        dur = sum(statistics.median(d for _, d in per["GRBM_GUI_ACTIVE"]) for per in bc.values())
         cus = 256
         mfma_cyc = med("SQ_VALU_MFMA_BUSY_CYCLES") / (cus * 4)  # per SIMD
         mops = med("SQ_INSTS_VALU_MFMA_MOPS_BF16") * 512.0
@@ -928,8 +945,8 @@ def summarize_profile(workload, trace_dir, fetch_dir, write_dir, busy_dir=None, 
                       "lds_wait_frac_of_wave_cycles": med("SQ_WAIT_INST_LDS") / waves,
                       "lds_bank_conflicts": med("SQ_LDS_BANK_CONFLICT"), "counter_pass_duration_ns": dur})
         lines += ["Activity counters (one pass, their own run):", "", "```", cmds["busy"], "```", "",
-                  "| Counter | Median per dispatch |", "|---|---|"]
-        lines += [f"| {c} | {med(c):.4g} |" for c in sorted(bc)]
+                  "| Counter | Median per dispatch (per call) |", "|---|---|"]
+        lines += [f"| {c} | {med(c):.4g} |" for c in sorted(next(iter(bc.values())))]
         lines += ["", f"- Work check: SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 = {mops:.4g} FLOP against 2*M*N*K = "
                       f"{flops:.4g} ({mops / flops:.3f}x; tiles past the matrix edges multiply zero padding).",
                   f"- MFMA pipe: SQ_VALU_MFMA_BUSY_CYCLES / ({cus} CUs x 4 SIMDs) = {mfma_cyc:.4g} busy cycles per "
@@ -943,8 +960,8 @@ def summarize_profile(workload, trace_dir, fetch_dir, write_dir, busy_dir=None, 
                   f"derived from it.", ""]
     if l2_dir:
         lc = named_counters(l2_dir, kernel)
-        hit = statistics.median(v for v, _ in lc["TCC_HIT_sum"])
-        miss = statistics.median(v for v, _ in lc["TCC_MISS_sum"])
+        hit = per_call(lc, "TCC_HIT_sum")
+        miss = per_call(lc, "TCC_MISS_sum")
         extra["l2_hit_frac"] = hit / max(1.0, hit + miss)
         lines += ["L2 (one pass, its own run):", "", "```", cmds["l2"], "```", "",
                   f"TCC_HIT_sum {hit:.4g}, TCC_MISS_sum {miss:.4g} per dispatch: L2 hit rate "

@@ -58,7 +58,8 @@ bool launch_epi(const inv::GemmParams &p, int epi, int out, dim3 grid, dim3 bloc
 template <class C>
 hipError_t launch_cfg(const inv::GemmParams &p, int epi, int out, int mode, hipStream_t s) {
     dim3 block(C::NTHREADS);
-    const unsigned ntiles = (unsigned)(p.tiles_m * p.tiles_n);
+    // tiles of this launch: p.tile_count from p.tile_base, or all of them
+    const unsigned ntiles = (unsigned)(p.tile_count > 0 ? p.tile_count : p.tiles_m * p.tiles_n);
     bool ok;
     if (mode == inv::LAUNCH_GATHER) {
         if constexpr (kGatherCfg && C::REG_STAGED && C::STAGED_EPI) {

@@ -68,6 +68,7 @@ struct GemmParams {
     int tiles_m, tiles_n, group_m;
     int ksplit, kt_per_split;  // split-K: splits, K tiles per split; stream-K: ksplit = persistent grid size
     int sk_dp_tiles;           // stream-K: tiles done one per workgroup (whole rounds) before the balanced phase
+    int tile_base, tile_count; // tile grid / split-K: tiles tile_base .. +tile_count-1 of the grouped order (count 0: all)
     float alpha, beta;
     int has_bias, vec_store;
     int nout;             // EPI_SWIGLU: output columns (N = its padded gate+up row count)
@@ -468,7 +469,7 @@ template <int MODE, class C>
 __device__ __forceinline__ float *unit_slot(const GemmParams &p, const UnitFix &f, int seg) {
     constexpr int64_t SZ = (int64_t)C::NTHREADS * C::ACC_REGS;
     if constexpr (MODE == GRID_SPLITK) {
-        return p.partial + ((int64_t)f.tile * f.nseg + seg) * SZ;
+        return p.partial + ((int64_t)(f.tile - p.tile_base) * f.nseg + seg) * SZ;
     } else {
         const int64_t g = f.g_first + seg;
         const bool starts_before = sk_start(g, f.I, f.G) < (int64_t)f.rel_tile * f.KT;
@@ -1329,8 +1330,10 @@ __device__ __forceinline__ void gemm_unit(const GemmParams &p, char *smem, int t
 
 // The body is compiled only in the device pass: the host pass needs just the
 // launch stub, and buffer-resource types do not exist for the host target.
-//  GRID_TILES:   one workgroup per output tile.
-//  GRID_SPLITK:  ksplit workgroups per tile, equal K ranges.
+//  GRID_TILES:   one workgroup per output tile (tiles tile_base ..
+//                tile_base + tile_count - 1 of the grouped order when
+//                tile_count > 0).
+//  GRID_SPLITK:  ksplit workgroups per tile (of the same range), equal K ranges.
 //  GRID_STREAMK: a persistent grid of G workgroups.  The first sk_dp_tiles
 //                tiles (whole rounds) go one per workgroup; then workgroup g
 //                takes k-iterations [g*I/G, (g+1)*I/G) of the I = (remaining
@@ -1341,10 +1344,11 @@ __global__ void __launch_bounds__(C::NTHREADS, 1) gemm_nt_bf16_kernel(const Gemm
 #if defined(__HIP_DEVICE_COMPILE__)
     __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
     const int ntiles = p.tiles_m * p.tiles_n;
+    const int nt = p.tile_count > 0 ? p.tile_count : ntiles;  // tiles of this launch, from p.tile_base
     const int KT = (p.K + C::BK - 1) / C::BK;
     int tm, tn;
     if constexpr (MODE == GRID_TILES) {
-        grouped_tile(xcd_remap(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+        grouped_tile(p.tile_base + xcd_remap(blockIdx.x, nt), p.tiles_m, p.tiles_n, p.group_m, tm, tn);
         UnitFix fix{};
         fix.nseg = 1;
         gemm_unit<C, EPI, OUT, MODE, GATHER>(p, smem, tm, tn, 0, KT, fix);
@@ -1352,9 +1356,9 @@ __global__ void __launch_bounds__(C::NTHREADS, 1) gemm_nt_bf16_kernel(const Gemm
         // Logical units in split-major order, remapped so that consecutive ones
         // share an XCD: the m-tiles of one n-tile and one K range then run on one
         // XCD and its L2 fetches their W panel slice once.
-        const int L = xcd_remap(blockIdx.x, ntiles * p.ksplit);
-        const int split = L / ntiles;
-        const int tile = L - split * ntiles;
+        const int L = xcd_remap(blockIdx.x, nt * p.ksplit);
+        const int split = L / nt;
+        const int tile = p.tile_base + (L - split * nt);
         grouped_tile(tile, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
         UnitFix fix{};
         fix.tile = tile;

@@ -517,6 +517,10 @@ int cfg_occupancy(const CfgMeta &m) { return std::max(1, std::min(2, (160 * 1024
 //    128x128 split two to four ways, and 16.3 with a 6-stage ring.  More
 //    splits lose to the partial-sum traffic, stream-K to its bookkeeping;
 //  - M <= 64: the W-streaming ring tiles with a short X tile.
+// A host-side grid mode: the whole rounds of a tile grid, then the last
+// round's tiles split two ways along K (count: the tiles done whole).
+constexpr int kGridSplitTail = 8;
+
 TileChoice choose_tiles(int64_t M, int64_t N, int64_t K, int epi = INV_EPI_NONE) {
     TileChoice c{17, inv::GRID_TILES, 1};
     const int cus = g.cu_count > 0 ? g.cu_count : 256;
@@ -567,6 +571,23 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K, int epi = INV_EPI_NONE)
         // gate | up wave columns over 256-row tiles, one workgroup per tile
         if (!kCfg[c.cfg].swiglu_ok) c.cfg = (M > 128) ? 8 : 2;
         c.mode = inv::GRID_TILES;
+    }
+    // Split tail: a tile grid whose last round is at most half full, on a long
+    // K, runs its whole rounds as tiles and then its last round's tiles split
+    // two ways along K (twice the workgroups, half the loop each; their
+    // partial sums summed in K order).  The second launch and the partial sums
+    // cost about what the half round saves at K = 3840 (9216 x 3840 -> 3840:
+    // 253 us against 248 whole; -> 15360: 912 against 930), so it is taken from
+    // 128 k-tiles (9216 x 15360 -> 3840: 912 us against 986).
+    // INV_HIP_SPLIT_TAIL=0 turns it off; INV_HIP_SPLIT_TAIL_SLOTS sets the
+    // slots per round and lifts the K limit (tests).
+    const int64_t sl = env_int("INV_HIP_SPLIT_TAIL_SLOTS", 0) > 0 ? env_int("INV_HIP_SPLIT_TAIL_SLOTS", 0) : slots;
+    const int64_t nt = tiles_of(c.cfg), tail = nt % sl, KT = (K + m.bk - 1) / m.bk;
+    const int64_t min_kt = env_int("INV_HIP_SPLIT_TAIL_SLOTS", 0) > 0 ? 16 : 128;
+    if (c.mode == inv::GRID_TILES && mode < 0 && epi != INV_EPI_SWIGLU && kCfg[c.cfg].staged_epi &&
+        env_int("INV_HIP_SPLIT_TAIL", 1) && nt > sl && tail > 0 && 2 * tail <= sl && KT >= min_kt) {
+        c.mode = kGridSplitTail;
+        c.count = (int)(nt - tail);
     }
     return c;
 }
@@ -629,11 +650,20 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
     if (bias && !aligned(bias, 16)) return fail(INV_ERR_ARG, "internal: bias not 16-byte aligned");
     const int64_t KT = (K + cm.bk - 1) / cm.bk;  // the kernel's k-tiles
     const int64_t ntiles = (int64_t)p.tiles_m * p.tiles_n;
-    int mode = tc.mode;
+    int mode = tc.mode, count = tc.count;
     p.ksplit = 1;
     p.kt_per_split = (int)KT;
+    // Split tail: tiles 0 .. dp_tiles-1 in a tile launch, the rest split two ways.
+    int64_t dp_tiles = 0;
+    if (mode == kGridSplitTail) {
+        dp_tiles = std::max<int64_t>(0, std::min<int64_t>(count, ntiles - 1));
+        p.tile_base = (int)dp_tiles;
+        p.tile_count = (int)(ntiles - dp_tiles);
+        mode = inv::GRID_SPLITK;
+        count = 2;
+    }
     if (mode == inv::GRID_SPLITK) {
-        p.kt_per_split = (int)((KT + tc.count - 1) / tc.count);
+        p.kt_per_split = (int)((KT + count - 1) / count);
         p.ksplit = (int)((KT + p.kt_per_split - 1) / p.kt_per_split);
         if (p.ksplit <= 1) {
             mode = inv::GRID_TILES;
@@ -653,7 +683,8 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
         p.sk_dp_tiles = (int)(dp_rounds * G);
     }
     if (mode != inv::GRID_TILES) {
-        const int64_t slots = (mode == inv::GRID_SPLITK) ? ntiles * p.ksplit : 2 * (int64_t)p.ksplit;
+        const int64_t slots = (mode == inv::GRID_SPLITK) ? (p.tile_count > 0 ? p.tile_count : ntiles) * p.ksplit
+                                                          : 2 * (int64_t)p.ksplit;
         const size_t pbytes = (size_t)(slots * cm.threads * cm.acc_regs) * sizeof(float);
         const size_t cbytes = (size_t)ntiles * sizeof(unsigned);
         if (fixed_ws) {
@@ -680,6 +711,14 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
         }
     }
     if (g.stats) HIPCHK(hipEventRecord(g.st0, g.stream));
+    if (dp_tiles > 0) {  // the whole rounds, before the split tail
+        inv::GemmParams pd = p;
+        pd.tile_base = 0;
+        pd.tile_count = (int)dp_tiles;
+        pd.ksplit = 1;
+        pd.kt_per_split = (int)KT;
+        HIPCHK(cm.launch(pd, row_bias ? inv::EPI_ROWBIAS : epi, out, inv::GRID_TILES, g.stream));
+    }
     HIPCHK(cm.launch(p, row_bias ? inv::EPI_ROWBIAS : epi, out, mode, g.stream));
     if (g.stats) {
         HIPCHK(hipEventRecord(g.st1, g.stream));
@@ -1418,7 +1457,10 @@ int linear_impl(const char *who, const void *X, int x_dtype, inv_weight_t W, con
     if (!dev) {
         const int pipe_mode = env_int("INV_HIP_HOST_PIPELINE", 1);
         if (pipe_mode && !precise) {
-            const TileChoice tc = choose_tiles(M, W->rows, W->ldw, epilogue);
+            // bands run the whole product's tile grid, one launch each (a split
+            // tail belongs to the whole grid's last round, not to a band's)
+            TileChoice tc = choose_tiles(M, W->rows, W->ldw, epilogue);
+            if (tc.mode == kGridSplitTail) tc = TileChoice{tc.cfg, inv::GRID_TILES, 1};
             // bytes a row sends up: fp32 X not normalised goes as bf16 operand rows
             const size_t x_up = (x_dtype == INV_DT_F32 && !nm) ? (size_t)W->ldw * 2
                                                                : (size_t)K * (x_dtype == INV_DT_F32 ? 4 : 2);

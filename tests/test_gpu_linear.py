@@ -198,6 +198,53 @@ def test_shared_tiles_bf16_out_and_gelu(hiplib, monkeypatch, cfg, grid):
     check(bf16_bits_to_f32(y), X, W, b, "gelu", tight=TOL_TIGHT + 2.0 ** -8, ref_tol=TOL_REF + 2.0 ** -8)
 
 
+# Split tail: the tile grid's whole rounds as tiles, then the last round's tiles split two ways
+# along K.  INV_HIP_SPLIT_TAIL_SLOTS=12 makes rounds of 12 tiles, so the 30 tiles of these
+# products run as 24 whole tiles and 6 split ones (12 workgroups of half the K loop).
+@pytest.mark.parametrize("cfg", [16, 17])
+@pytest.mark.parametrize("epi,ydt", [("none", "f32"), ("silu", "bf16"), ("gelu", "f32")])
+def test_split_tail_matches_plain_grid_and_oracle(hiplib, monkeypatch, cfg, epi, ydt):
+    M, K, N = 1100, 1024, 1300
+    X, W, b = gen(23, M, K, N)
+    monkeypatch.setenv("INV_HIP_TILE_CFG", str(cfg))
+    monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "0")
+    monkeypatch.setenv("INV_HIP_SPLIT_TAIL_SLOTS", "12")
+    with q.Weight(W, b) as w:
+        y = q.linear(X, w, epilogue=epi, out_dtype=ydt)
+        y2 = q.linear(X, w, epilogue=epi, out_dtype=ydt)
+        monkeypatch.setenv("INV_HIP_SPLIT_TAIL", "0")
+        y_plain = q.linear(X, w, epilogue=epi, out_dtype=ydt)
+    np.testing.assert_array_equal(y, y2)  # deterministic, counters reset
+    f = (lambda a: bf16_bits_to_f32(a)) if ydt == "bf16" else (lambda a: a)
+    if ydt == "f32":  # the split tiles sum their two K halves in another order than one loop
+        assert not np.array_equal(y, y_plain)
+    assert oracle.normwise_err(f(y), f(y_plain)) <= (2.0 ** -8 if ydt == "bf16" else 1e-6)
+    extra = 2.0 ** -8 if ydt == "bf16" else 0.0
+    check(f(y), X, W, b, epi, tight=TOL_TIGHT + extra, ref_tol=TOL_REF + extra)
+
+
+def test_split_tail_accumulate(hiplib, monkeypatch):
+    """Y += gate * (X W^T + b) (beta = 1, Y read in place): the whole tiles and
+    the split tiles each read and write only their own rows and columns."""
+    M, K, N = 1100, 1024, 1300
+    X, W, b = gen(24, M, K, N)
+    rng = np.random.default_rng(24)
+    Y0 = rng.standard_normal((M, N)).astype(np.float32)
+    gate = (rng.standard_normal(N) * 0.5).astype(np.float32)
+    monkeypatch.setenv("INV_HIP_TILE_CFG", "16")
+    monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "0")
+    monkeypatch.setenv("INV_HIP_SPLIT_TAIL_SLOTS", "12")
+    with q.Weight(W, b) as w:
+        y = Y0.copy()
+        q.linear_gated_add(y, X, w, gate)
+        monkeypatch.setenv("INV_HIP_SPLIT_TAIL", "0")
+        y_plain = Y0.copy()
+        q.linear_gated_add(y_plain, X, w, gate)
+    assert oracle.normwise_err(y - Y0, y_plain - Y0) <= 1e-6
+    ref = gate * oracle.linear_bf16w(round_bf16(X), W, b, oracle.EPI_NONE)
+    assert oracle.normwise_err(y - Y0, ref) <= TOL_TIGHT
+
+
 @pytest.mark.parametrize("cfg", REG_STAGED_CFGS)
 @pytest.mark.parametrize("K", [8, 64, 128, 200, 576, 1000, 3072])
 def test_register_staged_k_tile_counts(hiplib, monkeypatch, cfg, K):
