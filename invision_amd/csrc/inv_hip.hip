@@ -655,6 +655,10 @@ int run_gemm(const uint16_t *W, int64_t ldw, const uint16_t *X, int64_t ldx, voi
     p.kt_per_split = (int)KT;
     // Split tail: tiles 0 .. dp_tiles-1 in a tile launch, the rest split two ways.
     int64_t dp_tiles = 0;
+    if (mode == kGridSplitTail && fixed_ws &&
+        (size_t)((ntiles - std::min<int64_t>(count, ntiles - 1)) * 2 * cm.threads * cm.acc_regs) * sizeof(float) >
+            fixed_ws->partial_bytes)
+        mode = inv::GRID_TILES;  // a caller's scratch too small for the split tail: the plain grid
     if (mode == kGridSplitTail) {
         dp_tiles = std::max<int64_t>(0, std::min<int64_t>(count, ntiles - 1));
         p.tile_base = (int)dp_tiles;

@@ -64,6 +64,29 @@ def test_noalloc_matches_linear_twice(hiplib, case):
             bd.free()
 
 
+def test_noalloc_split_tail(hiplib, monkeypatch):
+    """The split tail (rounds of 12 tiles here: 24 whole tiles, 6 split two
+    ways along K) through the static scratch, against inv_hip_linear, on two
+    calls in a row (the second's 12 tiles: no tail)."""
+    monkeypatch.setenv("INV_HIP_SPLIT_TAIL_SLOTS", "12")
+    monkeypatch.setenv("INV_HIP_TILE_CFG", "16")
+    M, K, N = 1100, 1024, 1300
+    X, W, b = _gen(32, M, K, N)
+    Xin = as_bf16_bits(X)
+    with q.Weight(W) as w:
+        bd = q.DeviceArray.from_host(b, "f32")
+        for rows in (M, 400):
+            xd = q.DeviceArray.from_host(np.ascontiguousarray(Xin[:rows]), "bf16")
+            y_ref = q.DeviceArray((rows, N), "f32")
+            y_na = q.DeviceArray((rows, N), "f32")
+            ref = _run("inv_hip_linear", xd, w, bd, y_ref, rows, K, N, "bf16", "f32", hip.INV_EPI_NONE, 0)
+            got = _run("inv_hip_linear_noalloc", xd, w, bd, y_na, rows, K, N, "bf16", "f32", hip.INV_EPI_NONE, 0)
+            np.testing.assert_array_equal(got, ref)
+            for d in (xd, y_ref, y_na):
+                d.free()
+        bd.free()
+
+
 def test_noalloc_swiglu_and_misaligned_bias(hiplib):
     M, K, F = 700, 1536, 1024
     X, W, b = _gen(32, M, K, 2 * F)
