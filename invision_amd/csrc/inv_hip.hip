@@ -576,14 +576,16 @@ TileChoice choose_tiles(int64_t M, int64_t N, int64_t K, int epi = INV_EPI_NONE)
     // K, runs its whole rounds as tiles and then its last round's tiles split
     // two ways along K (twice the workgroups, half the loop each; their
     // partial sums summed in K order).  The second launch and the partial sums
-    // cost about what the half round saves at K = 3840 (9216 x 3840 -> 3840:
-    // 253 us against 248 whole; -> 15360: 912 against 930), so it is taken from
-    // 128 k-tiles (9216 x 15360 -> 3840: 912 us against 986).
+    // cost about what the half round saves at K = 3840 on the 256x224 tiles
+    // (9216 x 3840 -> 3840: 253 us against 248 whole), and a little less on
+    // the 8-wave 256x256 ones (-> 11520: 672 against 681; -> 15360: 912
+    // against 930), so it is taken from 128 k-tiles (9216 x 15360 -> 3840: 912
+    // us against 986), or from 60 on configuration 17.
     // INV_HIP_SPLIT_TAIL=0 turns it off; INV_HIP_SPLIT_TAIL_SLOTS sets the
     // slots per round and lifts the K limit (tests).
     const int64_t sl = env_int("INV_HIP_SPLIT_TAIL_SLOTS", 0) > 0 ? env_int("INV_HIP_SPLIT_TAIL_SLOTS", 0) : slots;
     const int64_t nt = tiles_of(c.cfg), tail = nt % sl, KT = (K + m.bk - 1) / m.bk;
-    const int64_t min_kt = env_int("INV_HIP_SPLIT_TAIL_SLOTS", 0) > 0 ? 16 : 128;
+    const int64_t min_kt = env_int("INV_HIP_SPLIT_TAIL_SLOTS", 0) > 0 ? 16 : (c.cfg == 17 ? 60 : 128);
     if (c.mode == inv::GRID_TILES && mode < 0 && epi != INV_EPI_SWIGLU && kCfg[c.cfg].staged_epi &&
         env_int("INV_HIP_SPLIT_TAIL", 1) && nt > sl && tail > 0 && 2 * tail <= sl && KT >= min_kt) {
         c.mode = kGridSplitTail;
