@@ -246,78 +246,119 @@ __global__ void __launch_bounds__(256) norm_rows_f32_bf16_reg(const float *__res
 //                    (QNNApplyRoPE2D, src/quicknncpu.pas:2968-2992);
 //  ROPE_HALF:        pairs (i, i + D/2) with column i, tables [tokens x D/2]
 //                    (QNNApplyRoPE2, src/quicknncpu.pas:2892-2917).
-// One wave per head row, EPT consecutive values per lane: the sum of squares is
+// One wave per head row at a time, EPT consecutive values per lane: the sum of squares is
 // a wave reduction; a pair's partner is in the same lane (interleaved, EPT 2),
 // in lane l ^ 1 (interleaved, EPT 1) or in lane l ^ 32 (half).
 enum { ROPE_NONE = 0, ROPE_INTERLEAVED = 1, ROPE_HALF = 2 };
 
 // BF16OUT: the result goes to y [rows x D] (packed) as bf16 (nearest-even)
 // instead of back into x, the Q/K operand staging of the fused attention entry.
+// A 256-thread workgroup covers 4 * HNR_ROWS rows.
+constexpr int HNR_ROWS = 4;
 template <int EPT, int ROPE, bool NORM, bool BF16OUT = false>
 __global__ void __launch_bounds__(256) head_norm_rope(float *__restrict__ x, int64_t rows, int heads,
                                                       const float *__restrict__ w, const float *__restrict__ ct,
                                                       const float *__restrict__ st, float eps,
                                                       uint16_t *__restrict__ y, int64_t ldx) {
     constexpr int D = 64 * EPT;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;  // the whole wave
     const int lane = threadIdx.x & 63;
-    // token row / heads starts ldx floats after the previous one (heads * D: packed)
-    float *v = x + (row / heads) * ldx + (row % heads) * D + EPT * lane;
-    float e[EPT];
-    if constexpr (EPT == 2) {
-        const float2 t = *(const float2 *)v;
-        e[0] = t.x;
-        e[1] = t.y;
-    } else {
-        e[0] = v[0];
-    }
-    if constexpr (NORM) {
-        float sq = 0.0f;
+    // HNR_ROWS consecutive rows per wave, their loads issued together: one row's
+    // 64 x EPT floats alone leave too few bytes in flight to stream at the HBM rate
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * HNR_ROWS;
+    // token row / heads starts ldx floats after the previous one (heads * D:
+    // packed); one division per wave, then the rows step through the heads
+    float *vp[HNR_ROWS];
+    int64_t toks[HNR_ROWS];
+    {
+        int64_t tok = row0 / heads;
+        int hd = (int)(row0 - tok * heads);
 #pragma unroll
-        for (int j = 0; j < EPT; ++j) sq += e[j] * e[j];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
-        const float rstd = 1.0f / sqrtf(sq / (float)D + eps);
-#pragma unroll
-        for (int j = 0; j < EPT; ++j) e[j] = e[j] * w[EPT * lane + j] * rstd;
-    }
-    if constexpr (ROPE != ROPE_NONE) {
-        const int64_t tok = row / heads;
-        if constexpr (ROPE == ROPE_INTERLEAVED) {
-            if constexpr (EPT == 2) {
-                const float c = ct[tok * D + 2 * lane], sn = st[tok * D + 2 * lane];
-                const float x0 = e[0], x1 = e[1];
-                e[0] = x0 * c - x1 * sn;
-                e[1] = x1 * c + x0 * sn;
-            } else {
-                const float p = __shfl_xor(e[0], 1);
-                const int col = lane & ~1;
-                const float c = ct[tok * D + col], sn = st[tok * D + col];
-                e[0] = (lane & 1) ? e[0] * c + p * sn : e[0] * c - p * sn;
-            }
-        } else {
-            constexpr int H = D / 2;
-            const bool lo = lane < 32;
-#pragma unroll
-            for (int j = 0; j < EPT; ++j) {
-                const float p = __shfl_xor(e[j], 32);
-                const int i = EPT * (lane & 31) + j;  // column of the pair
-                const float c = ct[tok * H + i], sn = st[tok * H + i];
-                e[j] = lo ? e[j] * c - p * sn : p * sn + e[j] * c;
+        for (int i = 0; i < HNR_ROWS; ++i) {
+            vp[i] = x + tok * ldx + hd * D + EPT * lane;
+            toks[i] = tok;
+            if (++hd == heads) {
+                hd = 0;
+                ++tok;
             }
         }
     }
-    if constexpr (BF16OUT) {
-        uint16_t *o = y + row * D + EPT * lane;
-        if constexpr (EPT == 2)
-            *(uint32_t *)o = (uint32_t)bf16_rne(e[0]) | ((uint32_t)bf16_rne(e[1]) << 16);
+    float wv[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        if constexpr (NORM)
+            wv[j] = w[EPT * lane + j];
         else
-            o[0] = bf16_rne(e[0]);
-    } else if constexpr (EPT == 2) {
-        *(float2 *)v = make_float2(e[0], e[1]);
-    } else {
-        v[0] = e[0];
+            wv[j] = 1.0f;  // unused: no norm (w may be null)
+    }
+    float e[HNR_ROWS][EPT];
+#pragma unroll
+    for (int i = 0; i < HNR_ROWS; ++i) {
+        const int64_t row = row0 + i;
+        const float *v = vp[i];
+        if (row >= rows) {
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) e[i][j] = 0.0f;
+        } else if constexpr (EPT == 2) {
+            const float2 t = *(const float2 *)v;
+            e[i][0] = t.x;
+            e[i][1] = t.y;
+        } else {
+            e[i][0] = v[0];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < HNR_ROWS; ++i) {
+        const int64_t row = row0 + i;
+        if (row >= rows) break;  // the whole wave
+        float *v = vp[i];
+        if constexpr (NORM) {
+            float sq = 0.0f;
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) sq += e[i][j] * e[i][j];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
+            const float rstd = 1.0f / sqrtf(sq / (float)D + eps);
+#pragma unroll
+            for (int j = 0; j < EPT; ++j) e[i][j] = e[i][j] * wv[j] * rstd;
+        }
+        if constexpr (ROPE != ROPE_NONE) {
+            const int64_t tok = toks[i];
+            if constexpr (ROPE == ROPE_INTERLEAVED) {
+                if constexpr (EPT == 2) {
+                    const float c = ct[tok * D + 2 * lane], sn = st[tok * D + 2 * lane];
+                    const float x0 = e[i][0], x1 = e[i][1];
+                    e[i][0] = x0 * c - x1 * sn;
+                    e[i][1] = x1 * c + x0 * sn;
+                } else {
+                    const float p = __shfl_xor(e[i][0], 1);
+                    const int col = lane & ~1;
+                    const float c = ct[tok * D + col], sn = st[tok * D + col];
+                    e[i][0] = (lane & 1) ? e[i][0] * c + p * sn : e[i][0] * c - p * sn;
+                }
+            } else {
+                constexpr int H = D / 2;
+                const bool lo = lane < 32;
+#pragma unroll
+                for (int j = 0; j < EPT; ++j) {
+                    const float p = __shfl_xor(e[i][j], 32);
+                    const int col = EPT * (lane & 31) + j;  // column of the pair
+                    const float c = ct[tok * H + col], sn = st[tok * H + col];
+                    e[i][j] = lo ? e[i][j] * c - p * sn : p * sn + e[i][j] * c;
+                }
+            }
+        }
+        if constexpr (BF16OUT) {
+            uint16_t *o = y + row * D + EPT * lane;
+            if constexpr (EPT == 2)
+                *(uint32_t *)o = (uint32_t)bf16_rne(e[i][0]) | ((uint32_t)bf16_rne(e[i][1]) << 16);
+            else
+                o[0] = bf16_rne(e[i][0]);
+        } else if constexpr (EPT == 2) {
+            *(float2 *)v = make_float2(e[i][0], e[i][1]);
+        } else {
+            v[0] = e[i][0];
+        }
     }
 }
 

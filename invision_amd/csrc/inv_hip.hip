@@ -1567,7 +1567,9 @@ int launch_head_norm_rope(float *x, uint16_t *y, int64_t rows, int64_t heads, in
                           int rope, const float *ct, const float *st, int64_t ldx = 0) {
     if (rows == 0) return INV_OK;
     if (ldx == 0) ldx = heads * head_dim;
-    const dim3 grid((unsigned)((rows + 3) / 4));
+    const int64_t per_wg = 4 * inv::HNR_ROWS;
+    if ((rows + per_wg - 1) / per_wg > INT32_MAX) return fail(INV_ERR_UNSUPPORTED, "head_norm_rope: too many rows");
+    const dim3 grid((unsigned)((rows + per_wg - 1) / per_wg));
     auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, grid, dim3(256), 0, g.stream, x, rows, (int)heads, w, ct, st, 1e-6f, y, ldx);
     };
