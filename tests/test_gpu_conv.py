@@ -166,6 +166,26 @@ def test_conv2d_host_image_rounded_on_upload_matches_device(hiplib, monkeypatch,
 
 
 @pytest.mark.gpu
+def test_conv2d_patch_gemm_with_a_split_tail(hiplib, monkeypatch):
+    """The patch-matrix GEMM with its per-channel row bias, run as whole tiles
+    plus a split tail (rounds of 12 tiles forced): the split tiles' finishing
+    unit adds the row bias; against the plain grid and the oracle.  4608 pixels
+    make 18 tiles of 256 (x 96 channels): 12 whole, 6 split."""
+    b, c, oc, H, W, kH, kW, s, p = 1, 128, 96, 72, 64, 3, 3, 1, 1
+    x, w, bias = gen(15, b, c, oc, H, W, kH, kW)
+    monkeypatch.setenv("INV_HIP_CONV_GATHER", "0")
+    monkeypatch.setenv("INV_HIP_TILE_CFG", "16")
+    with q.Weight(w) as wt:
+        monkeypatch.setenv("INV_HIP_SPLIT_TAIL_SLOTS", "12")
+        y = q.conv2d(x, wt, bias, c, oc, H, W, kH, kW, s, p, b)
+        monkeypatch.delenv("INV_HIP_SPLIT_TAIL_SLOTS")
+        y_plain = q.conv2d(x, wt, bias, c, oc, H, W, kH, kW, s, p, b)
+    assert not np.array_equal(y, y_plain)  # the split tiles sum their K halves in another order
+    assert oracle.normwise_err(y, y_plain) <= 1e-6
+    check(y, x, w, bias, c, oc, H, W, kH, kW, s, p, b)
+
+
+@pytest.mark.gpu
 def test_conv2d_row_chunks_match_one_pass(hiplib):
     # A patch-matrix cap of 1 MiB splits the 64x56 output into bands of rows;
     # every band is a GEMM over its own pixels, so the result is identical.
