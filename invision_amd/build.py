@@ -29,7 +29,7 @@ HOST_CXX = os.environ.get("INV_HOST_CXX", "/opt/rocm/llvm/bin/clang++")
 ARCH = "gfx950"
 
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
-NUM_GEMM_CONFIGS = 18  # INV_GEMM_NUM_CONFIGS in csrc/gemm_configs.hpp
+NUM_GEMM_CONFIGS = 19  # INV_GEMM_NUM_CONFIGS in csrc/gemm_configs.hpp
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -36,10 +36,11 @@
 
 #define INV_CFG_16 inv::Rs16Cfg<256, 224, 2, 2, 1> /* 16x16x32 MFMAs, 4 waves of 128x112, one register stage */
 #define INV_CFG_17 inv::Rs16Cfg<256, 256, 2, 4, 1> /* 16x16x32 MFMAs, 8 waves of 128x64, two per SIMD */
+#define INV_CFG_18 inv::Rs16Cfg<256, 192, 2, 2, 1> /* 16x16x32 MFMAs, 4 waves of 128x96, one register stage */
 
 #define INV_GEMM_CONFIG_IDS(X) \
-    X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10) X(11) X(12) X(13) X(14) X(15) X(16) X(17)
-#define INV_GEMM_NUM_CONFIGS 18
+    X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8) X(9) X(10) X(11) X(12) X(13) X(14) X(15) X(16) X(17) X(18)
+#define INV_GEMM_NUM_CONFIGS 19
 
 namespace inv {
 struct GemmParams;

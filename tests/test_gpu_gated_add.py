@@ -68,7 +68,7 @@ def test_gated_add_equals_projection_then_gated_add(hiplib):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("cfg", [0, 2, 3, 4, 5, 8, 16, 17])
+@pytest.mark.parametrize("cfg", [0, 2, 3, 4, 5, 8, 16, 17, 18])
 @pytest.mark.parametrize("grid", ["tiles", "splitk3", "streamk37"])
 def test_gated_add_every_tile_and_grid_mode(hiplib, monkeypatch, cfg, grid):
     """The residual is read once, by the unit that writes the tile, in every grid mode."""
@@ -147,7 +147,7 @@ def test_gated_add_argument_errors(hiplib):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("cfg", [8, 13, 15, 16, 17])
+@pytest.mark.parametrize("cfg", [8, 13, 15, 16, 17, 18])
 @pytest.mark.parametrize("grid", [{"INV_HIP_MODE": "1", "INV_HIP_KSPLIT": "3"},
                                   {"INV_HIP_MODE": "2", "INV_HIP_SK_GRID": "37"}], ids=["splitk3", "streamk37"])
 def test_gated_add_with_shared_tiles(hiplib, monkeypatch, cfg, grid):

@@ -165,8 +165,8 @@ GRID_MODES = {  # INV_HIP_MODE / INV_HIP_KSPLIT / INV_HIP_SK_GRID
 }
 
 
-ALL_CFGS = list(range(18))  # INV_GEMM_NUM_CONFIGS in invision_amd/csrc/gemm_configs.hpp
-REG_STAGED_CFGS = [8, 9, 10, 11, 12, 13, 14, 15, 16, 17]  # 11-14, 16: unequal W and X copy-chunk counts
+ALL_CFGS = list(range(19))  # INV_GEMM_NUM_CONFIGS in invision_amd/csrc/gemm_configs.hpp
+REG_STAGED_CFGS = [8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18]  # 11-14, 16, 18: unequal W and X copy-chunk counts
 
 
 @pytest.mark.parametrize("cfg", ALL_CFGS)
@@ -184,7 +184,7 @@ def test_every_tile_shape_and_grid_mode(hiplib, monkeypatch, cfg, grid):
     np.testing.assert_array_equal(y, y2)  # deterministic, counters reset
 
 
-@pytest.mark.parametrize("cfg", [8, 13, 15, 16, 17])
+@pytest.mark.parametrize("cfg", [8, 13, 15, 16, 17, 18])
 @pytest.mark.parametrize("grid", ["splitk3", "streamk37"])
 def test_shared_tiles_bf16_out_and_gelu(hiplib, monkeypatch, cfg, grid):
     """Split- and stream-K tiles with the bf16 output and GELU epilogue."""
@@ -201,10 +201,10 @@ def test_shared_tiles_bf16_out_and_gelu(hiplib, monkeypatch, cfg, grid):
 # Split tail: the tile grid's whole rounds as tiles, then the last round's tiles split two ways
 # along K.  INV_HIP_SPLIT_TAIL_SLOTS=12 makes rounds of 12 tiles, so the 30 tiles of these
 # products run as 24 whole tiles and 6 split ones (12 workgroups of half the K loop).
-@pytest.mark.parametrize("cfg", [16, 17])
+@pytest.mark.parametrize("cfg", [16, 17, 18])
 @pytest.mark.parametrize("epi,ydt", [("none", "f32"), ("silu", "bf16"), ("gelu", "f32")])
 def test_split_tail_matches_plain_grid_and_oracle(hiplib, monkeypatch, cfg, epi, ydt):
-    M, K, N = 1100, 1024, 1300
+    M, K, N = (900 if cfg == 18 else 1100), 1024, 1300  # 5 x 6 tiles of 224, 256 or 192 X rows
     X, W, b = gen(23, M, K, N)
     monkeypatch.setenv("INV_HIP_TILE_CFG", str(cfg))
     monkeypatch.setenv("INV_HIP_HOST_PIPELINE", "0")

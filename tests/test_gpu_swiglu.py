@@ -56,7 +56,7 @@ def test_swiglu_matches_oracle(hiplib, M, K, F, bias, out):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("cfg", [2, 8, 16, 17])
+@pytest.mark.parametrize("cfg", [2, 8, 16, 17, 18])
 def test_swiglu_on_every_swiglu_tile(hiplib, monkeypatch, cfg):
     """The SwiGLU epilogue on each tile configuration that splits into gate | up wave columns:
     32x32 MFMA blocks (2, 8) and 16x16 blocks (16: a 16-row block finished 8 rows per wave)."""
