@@ -292,6 +292,7 @@ __global__ void __launch_bounds__(256) head_norm_rope(float *__restrict__ x, int
             wv[j] = 1.0f;  // unused: no norm (w may be null)
     }
     float e[HNR_ROWS][EPT];
+    float tc = 0.0f, ts = 0.0f;  // the current token's rotary pair (interleaved, EPT 2)
 #pragma unroll
     for (int i = 0; i < HNR_ROWS; ++i) {
         const int64_t row = row0 + i;
@@ -326,7 +327,13 @@ __global__ void __launch_bounds__(256) head_norm_rope(float *__restrict__ x, int
             const int64_t tok = toks[i];
             if constexpr (ROPE == ROPE_INTERLEAVED) {
                 if constexpr (EPT == 2) {
-                    const float c = ct[tok * D + 2 * lane], sn = st[tok * D + 2 * lane];
+                    // the wave's rows are heads of one token but at a token boundary:
+                    // its table pair is loaded once for them
+                    if (i == 0 || tok != toks[i - 1]) {
+                        tc = ct[tok * D + 2 * lane];
+                        ts = st[tok * D + 2 * lane];
+                    }
+                    const float c = tc, sn = ts;
                     const float x0 = e[i][0], x1 = e[i][1];
                     e[i][0] = x0 * c - x1 * sn;
                     e[i][1] = x1 * c + x0 * sn;
